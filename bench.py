@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""MoC hot-path benchmark on one MI355X.
+
+Headline: the MoC layer forward + backward at
+B=4, T=4096, D=2048, z_dim=2048, K=16, S=4, bf16, softmax routing, fused SiLU,
+basis init_std=0.002, router ~ N(0, 0.02), loss = y.sum(), gradients of x, z,
+router and basis.  One step = zero grads, forward, backward on synthetic
+inputs already resident in HBM.  Printed as one JSON line:
+
+  value         tokens/s (millions) of the full layer step (router GEMMs + MoC)
+  roofline      HBM roofline of the dominant entry (the fused backward)
+  kernel_scope  forward / backward entry times alone (no router GEMMs)
+  decode        configs[3]: batch-256 single-token steps, us/step
+  cpu_baseline  the CPU oracle on a bounded slice of the same workload
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "mixture-of-convolutions_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/step"
+HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
+DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
+
+
+def bytes_fwd(N, D, K, S, ex=2, ea=2, eb=2):
+    return 2 * N * D * ex + N * K * ea + K * S * D * eb
+
+
+def bytes_bwd(N, D, K, S, ex=2, ea=2, eb=2):
+    return 3 * N * D * ex + 2 * N * K * ea + 2 * K * S * D * eb
+
+
+def flops_fwd(N, D, K, S):
+    return 2 * N * D * S * (K + 1)
+
+
+def flops_bwd(N, D, K, S, silu=True):
+    return N * D * S * (6 * K + 3 + 2 * int(silu))
+
+
+def build_layer(dev, dtype=torch.bfloat16, cfg=CFG, seed=0):
+    import moc
+    g = torch.Generator().manual_seed(seed)
+    torch.manual_seed(seed)
+    m = moc.MoC(cfg["D"], cfg["Z"], cfg["S"], cfg["K"], activation="silu", init_std=0.002)
+    with torch.no_grad():
+        m.router.copy_(torch.randn(cfg["K"], cfg["Z"], generator=g) * 0.02)
+    m = m.to(dev, dtype)
+    x = (torch.randn(cfg["B"], cfg["T"], cfg["D"], generator=g)).to(dev, dtype).requires_grad_()
+    z = (torch.randn(cfg["B"], cfg["T"], cfg["Z"], generator=g)).to(dev, dtype).requires_grad_()
+    return m, x, z
+
+
+def time_region(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps  # ms
+
+
+def bench_layer(dev, steps, warmup):
+    m, x, z = build_layer(dev)
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        x.grad = None
+        z.grad = None
+        y, _ = m(x, z)
+        y.sum().backward()
+
+    return time_region(step, steps, warmup)
+
+
+def bench_entries(dev, steps, warmup):
+    """Forward and backward C-ABI entries alone, on the layer's logits."""
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX
+    m, x, z = build_layer(dev)
+    with torch.no_grad():
+        logits = torch.nn.functional.linear(z, m.router)
+        basis = m.conv_bases.detach()
+        xd = x.detach()
+        dy = torch.ones_like(xd)
+    fwd = lambda: ops.launch_forward(xd, logits, basis, activation_flag=1,  # noqa: E731
+                                     routing=ROUTE_SOFTMAX)
+    bwd = lambda: ops.launch_backward(xd, logits, basis, dy, activation_flag=1,  # noqa: E731
+                                      need_x=True, routing=ROUTE_SOFTMAX)
+    return time_region(fwd, steps, warmup), time_region(bwd, steps, warmup)
+
+
+def bench_decode(dev):
+    """prefill a 1024-token prompt, then 512 single-token steps."""
+    import moc
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX
+    c = DECODE
+    g = torch.Generator().manual_seed(0)
+    torch.manual_seed(0)
+    m = moc.MoC(c["D"], c["Z"], c["S"], c["K"], activation="silu")
+    with torch.no_grad():
+        m.router.copy_(torch.randn(c["K"], c["Z"], generator=g) * 0.02)
+    m = m.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        xp = torch.randn(c["B"], c["prompt"], c["D"], generator=g).to(dev, torch.bfloat16)
+        zp = torch.randn(c["B"], c["prompt"], c["Z"], generator=g).to(dev, torch.bfloat16)
+        _, cache = m(xp, zp, output_final_state=True)
+        del xp, zp
+        xs = torch.randn(c["B"], c["steps"], c["D"], generator=g).to(dev, torch.bfloat16)
+        zs = torch.randn(c["B"], c["steps"], c["Z"], generator=g).to(dev, torch.bfloat16)
+        for t in range(8):  # warm-up on a scratch copy
+            m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache.clone())
+        torch.cuda.synchronize()
+        per_step = []
+        for t in range(c["steps"]):
+            t0 = time.perf_counter()
+            y, _ = m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache, output_final_state=True)
+            torch.cuda.synchronize()
+            per_step.append((time.perf_counter() - t0) * 1e6)
+        # kernel-only: 32 decode launches captured in one HIP graph, replayed
+        logits = torch.nn.functional.linear(zs[:, 0], m.router)
+        xt = xs[:, 0].contiguous()
+        basis = m.conv_bases.detach()
+        scratch = cache.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                ops.launch_update(xt, logits, basis, scratch, activation_flag=1,
+                                  routing=ROUTE_SOFTMAX)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        n_in_graph = 32
+        with torch.cuda.graph(graph):
+            for _ in range(n_in_graph):
+                ops.launch_update(xt, logits, basis, scratch, activation_flag=1,
+                                  routing=ROUTE_SOFTMAX)
+        ms = time_region(graph.replay, 20, 3)
+    kbytes = c["B"] * c["D"] * 2 * (1 + 1 + (c["S"] - 1) + c["S"]) + c["K"] * c["S"] * c["D"] * 2
+    kernel_us = ms * 1e3 / n_in_graph
+    return dict(B=c["B"], D=c["D"], K=c["K"], S=c["S"], prompt=c["prompt"], steps=c["steps"],
+                step_us_median=round(statistics.median(per_step), 2),
+                step_us_p10=round(sorted(per_step)[len(per_step) // 10], 2),
+                kernel_us=round(kernel_us, 3),
+                kernel_GBps=round(kbytes / (kernel_us * 1e-6) / 1e9, 1),
+                kernel_roofline_us=round(kbytes / HBM_PEAK * 1e6, 3))
+
+
+def cpu_baseline(seconds):
+    """The CPU oracle (oracle/moc_oracle.py) on a bounded slice of the headline
+    workload: one sequence of 2048 tokens at D=Z=2048, K=16, S=4, fp32, layer
+    forward + backward (router GEMM + softmax + MoC), all host cores."""
+    from oracle import moc_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    T = 2048
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, T, CFG["D"], generator=g).requires_grad_()
+    z = torch.randn(1, T, CFG["Z"], generator=g).requires_grad_()
+    router = (torch.randn(CFG["K"], CFG["Z"], generator=g) * 0.02).requires_grad_()
+    basis = ((torch.rand(CFG["K"], CFG["S"], CFG["D"], generator=g) * 2 - 1)
+             * 0.002 * 3 ** 0.5).requires_grad_()
+
+    def step():
+        for t in (x, z, router, basis):
+            t.grad = None
+        a = O.route(torch.nn.functional.linear(z, router), "softmax")
+        O.moc_ref(x, a, basis, "silu").sum().backward()
+
+    step()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and reps >= 2:
+            break
+    tok_s = reps * T / el
+    return {"value": round(tok_s / 1e6, 5), "unit": "Mtok/s", "cores": cores, "kind": "port",
+            "sample": f"CPU oracle, layer fwd+bwd on B=1 T={T} D={CFG['D']} Z={CFG['Z']} "
+                      f"K={CFG['K']} S={CFG['S']} fp32, {reps} reps in {el:.1f}s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "multi-GPU sharding is design-only", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    N = CFG["B"] * CFG["T"]
+    D, K, S = CFG["D"], CFG["K"], CFG["S"]
+
+    ms = bench_layer(dev, args.steps, args.warmup)
+    t_fwd, t_bwd = bench_entries(dev, args.steps, args.warmup)
+    fb, bb = bytes_fwd(N, D, K, S), bytes_bwd(N, D, K, S)
+    roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / 2.5e15)
+               + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / 2.5e15)) * 1e6
+    achieved = bb / (t_bwd * 1e-3)
+    out = {
+        "metric": METRIC,
+        "value": round(N / (ms * 1e-3) / 1e6, 3),
+        "unit": "Mtok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) x, z; router N(0,0.02); basis U(+-0.002*sqrt(3)))",
+        "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[1]", "B": CFG["B"],
+                   "T": CFG["T"], "D": D, "z_dim": CFG["Z"], "K": K, "S": S,
+                   "activation": "silu", "routing": "softmax", "loss": "y.sum()"},
+        "roofline": {"bound": "hbm", "kernel": "moc_backward",
+                     "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
+                     "traffic": None, "algorithmic_bytes": bb},
+        "kernel_scope": {"fwd_us": round(t_fwd * 1e3, 2), "bwd_us": round(t_bwd * 1e3, 2),
+                         "mtok_s": round(N / ((t_fwd + t_bwd) * 1e-3) / 1e6, 3),
+                         "fwd_GBps": round(fb / (t_fwd * 1e-3) / 1e9, 1),
+                         "bwd_GBps": round(bb / (t_bwd * 1e-3) / 1e9, 1),
+                         "hbm_roofline_us": round(roof_us, 2),
+                         "roofline_frac": round(roof_us / ((t_fwd + t_bwd) * 1e3), 4)},
+    }
+    if not args.no_decode:
+        out["decode"] = bench_decode(dev)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,139 @@
+/*
+ * moc_hip.h - C ABI of libmoc_hip.so, the MI355X (gfx950) Mixture-of-Convolutions
+ * hot path: fused forward, backward (dx / dalpha / dbasis) and the decode-step
+ * cache update, for fixed-length [B,T,D] and packed (cu_seqlens) inputs.
+ *
+ * Every entry point replaces one launch function of the reference's launch layer
+ * (andrewmouldon/mixture-of-convolutions, moc/ops.py); the Python package in this
+ * repository binds them with ctypes (moc/_lib.py) the way that layer launched
+ * its kernels.  Conventions:
+ *   - plain device pointers, element counts and dtype codes; no framework types;
+ *   - all tensors contiguous row-major, except the decode cache (strided);
+ *   - the caller owns every buffer, including the workspace, whose size comes
+ *     from the matching *_workspace_bytes query; the library never allocates;
+ *   - all work is enqueued on `stream` (a hipStream_t, NULL = default stream);
+ *     no call synchronises the host;
+ *   - return 0 on success, a negative MOC_ERR_* code otherwise;
+ *     moc_last_error() then returns a message (thread-local).
+ *
+ * Math (tap s = S-1 multiplies the current token, moc/reference.py:29-32):
+ *   alpha[n,k] = alpha_in[n,k]            (MOC_ROUTE_ALPHA)
+ *              = softmax_k(logits[n,:])    (MOC_ROUTE_SOFTMAX)
+ *              = exp(logits[n,k])          (MOC_ROUTE_EXP)
+ *   P[n,d] = sum_s x[n-(S-1-s), d] * sum_k alpha[n,k] * basis[k,s,d]
+ *            (x taken as 0 before the start of n's sequence)
+ *   y = silu(P) if activation else P
+ */
+#ifndef MOC_HIP_H
+#define MOC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* storage dtype codes */
+#define MOC_DT_F32  0
+#define MOC_DT_BF16 1
+#define MOC_DT_F16  2
+
+/* what the `alpha` argument holds: routing weights, or router logits whose
+ * activation (softmax / exp, moc/api.py:383-388) is fused into the kernels */
+#define MOC_ROUTE_ALPHA   0
+#define MOC_ROUTE_SOFTMAX 1
+#define MOC_ROUTE_EXP     2
+
+/* status codes */
+#define MOC_OK             0
+#define MOC_ERR_ARG       -1
+#define MOC_ERR_DTYPE     -2
+#define MOC_ERR_WORKSPACE -3
+#define MOC_ERR_HIP       -4
+
+/* ABI version of this header. */
+int moc_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* moc_last_error(void);
+
+/*
+ * Sequence description shared by forward / backward:
+ *   cu_seqlens == NULL: fixed length, n_tokens = B*T tokens, sequences of
+ *                       seq_len = T tokens each ([B,T,D] viewed as [B*T,D]);
+ *   cu_seqlens != NULL: packed, n_seqs sequences, token n of sequence j lies in
+ *                       [cu_seqlens[j], cu_seqlens[j+1]); int32 entries, or
+ *                       int64 when cu_seqlens_i64 != 0; seq_len is ignored.
+ * Tokens outside every [cu_seqlens[j], cu_seqlens[j+1]) start their own history.
+ */
+
+/* Workspace bytes moc_forward needs for this problem (0 is valid). */
+size_t moc_forward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
+                                   int64_t kernel_size, int x_dtype, int routing);
+
+/*
+ * y[n,d] for all tokens.  Replaces launch_forward (moc/ops.py:129-194), which
+ * launched _moc_fwd_kernel (moc/kernels.py:36-153), and launch_preact
+ * (moc/ops.py:197-213) when called with activation = 0.
+ *   x, y  : [n_tokens, dim], x_dtype (bf16 or f32); y has x's dtype
+ *   alpha : [n_tokens, k], alpha_dtype (weights or logits, see routing)
+ *   basis : [k, kernel_size, dim], basis_dtype
+ * With a bf16 x, alpha and basis are rounded to bf16 before the mixture, as the
+ * reference kernels do (moc/kernels.py:92-95, 125-128); accumulation is fp32.
+ */
+int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
+                const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                int64_t n_tokens, int64_t seq_len,
+                int64_t dim, int64_t k, int64_t kernel_size,
+                int x_dtype, int alpha_dtype, int basis_dtype,
+                int activation, int routing,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes moc_backward needs for this problem. */
+size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
+                                    int64_t kernel_size, int x_dtype, int routing);
+
+/*
+ * Gradients for upstream gradient dy (x_dtype, [n_tokens, dim]).  Replaces
+ * launch_backward (moc/ops.py:216-338) and the preact recompute it needed
+ * (moc/ops.py:197-213), i.e. _moc_bwd_dx_kernel (moc/kernels.py:156-279) and
+ * _moc_bwd_dalpha_dbasis_dot_kernel (moc/kernels.py:282-439).
+ *   dx     : [n_tokens, dim] in x_dtype, or NULL to skip it (need_x = False)
+ *   dalpha : [n_tokens, k] in alpha_dtype; d/dalpha for MOC_ROUTE_ALPHA, or
+ *            d/dlogits with the softmax / exp gradient fused in
+ *   dbasis : [k, kernel_size, dim] in basis_dtype
+ * dbasis and dalpha are reduced in a fixed order: results are bitwise
+ * reproducible run to run (the reference used relaxed fp32 atomics).
+ */
+int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy,
+                 void* dx, void* dalpha, void* dbasis,
+                 const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                 int64_t n_tokens, int64_t seq_len,
+                 int64_t dim, int64_t k, int64_t kernel_size,
+                 int x_dtype, int alpha_dtype, int basis_dtype,
+                 int activation, int routing,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One decode step, in place.  Replaces launch_update (moc/ops.py:341-362) and
+ * _moc_update_kernel (moc/kernels.py:442-550).
+ *   x     : [batch, dim] contiguous, x_dtype
+ *   alpha : [batch, k] contiguous (weights or logits, see routing)
+ *   cache : [batch, dim, kernel_size] in x_dtype with element strides
+ *           (cache_stride_b, cache_stride_d, cache_stride_s); slot S-1 newest
+ *   y     : [batch, dim] contiguous, x_dtype
+ * y = act(sum_{s<S-1} cache[:,:,s+1] * W_s + x * W_{S-1}); afterwards the cache
+ * holds its old slots 1..S-1 in slots 0..S-2 and x in slot S-1.
+ */
+int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
+               int64_t cache_stride_b, int64_t cache_stride_d, int64_t cache_stride_s,
+               void* y, int64_t batch, int64_t dim, int64_t k, int64_t kernel_size,
+               int x_dtype, int alpha_dtype, int basis_dtype,
+               int activation, int routing, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOC_HIP_H */

@@ -1,0 +1,208 @@
+// C ABI of libmoc_hip.so (declared in include/moc_hip.h): argument checks,
+// workspace carving and dispatch to the kernels.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/moc_hip.h"
+#include "moc_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool dt_ok(int dt) { return dt == MOC_DT_F32 || dt == MOC_DT_BF16 || dt == MOC_DT_F16; }
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Largest extents the launch grids are sized for.
+constexpr int64_t kMaxTokens = int64_t(1) << 31;
+constexpr int64_t kMaxBatch = 65535;
+
+int check_dims(int64_t n_tokens, int64_t dim, int64_t k, int64_t ks) {
+  if (n_tokens <= 0 || dim <= 0 || k <= 0 || ks <= 0)
+    return fail(MOC_ERR_ARG, "n_tokens, dim, k and kernel_size must be positive "
+                             "(got %lld, %lld, %lld, %lld)",
+                (long long)n_tokens, (long long)dim, (long long)k, (long long)ks);
+  if (n_tokens >= kMaxTokens) return fail(MOC_ERR_ARG, "n_tokens too large: %lld", (long long)n_tokens);
+  return MOC_OK;
+}
+
+int check_common(int x_dt, int a_dt, int b_dt, int activation, int routing) {
+  if (x_dt != MOC_DT_F32 && x_dt != MOC_DT_BF16)
+    return fail(MOC_ERR_DTYPE, "unsupported x dtype code %d (bf16 or f32 only)", x_dt);
+  if (!dt_ok(a_dt)) return fail(MOC_ERR_DTYPE, "unsupported alpha dtype code %d", a_dt);
+  if (!dt_ok(b_dt)) return fail(MOC_ERR_DTYPE, "unsupported basis dtype code %d", b_dt);
+  if (activation != 0 && activation != 1)
+    return fail(MOC_ERR_ARG, "activation must be 0 or 1, got %d", activation);
+  if (routing < MOC_ROUTE_ALPHA || routing > MOC_ROUTE_EXP)
+    return fail(MOC_ERR_ARG, "routing must be 0, 1 or 2, got %d", routing);
+  return MOC_OK;
+}
+
+struct Carve {
+  char* base;
+  size_t used;
+  template <typename T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base + used);
+    used += align_up(count * sizeof(T));
+    return p;
+  }
+};
+
+size_t fwd_bytes(int64_t n, int64_t d, int64_t k, int64_t s) {
+  return align_up(size_t(n * k) * 4) + align_up(size_t(k * s * d) * 4);
+}
+
+size_t bwd_bytes(const moc::Problem& p) {
+  return fwd_bytes(p.n_tokens, p.D, p.K, p.S) +
+         align_up(moc::generic_bwd_scratch_floats(p) * 4);
+}
+
+moc::Problem make_problem(const void* cu, int cu64, int64_t n_seqs, int64_t n_tokens,
+                          int64_t seq_len, int64_t dim, int64_t k, int64_t ks, int x_dt,
+                          int a_dt, int b_dt, int activation, int routing) {
+  moc::Problem p;
+  p.seq.cu = cu;
+  p.seq.cu64 = cu64 ? 1 : 0;
+  p.seq.n_seqs = n_seqs;
+  p.seq.seq_len = seq_len;
+  p.seq.n_tokens = n_tokens;
+  p.n_tokens = n_tokens;
+  p.D = dim;
+  p.K = k;
+  p.S = ks;
+  p.x_dt = x_dt;
+  p.a_dt = a_dt;
+  p.b_dt = b_dt;
+  p.activation = activation;
+  p.routing = routing;
+  return p;
+}
+
+int check_seq(const void* cu, int64_t n_seqs, int64_t seq_len) {
+  if (cu == nullptr && seq_len <= 0)
+    return fail(MOC_ERR_ARG, "seq_len must be positive for fixed-length inputs");
+  if (cu != nullptr && n_seqs <= 0)
+    return fail(MOC_ERR_ARG, "n_seqs must be positive when cu_seqlens is given");
+  return MOC_OK;
+}
+
+int hip_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MOC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MOC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moc_abi_version(void) { return 1; }
+
+const char* moc_last_error(void) { return g_err; }
+
+size_t moc_forward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
+                                   int64_t kernel_size, int x_dtype, int routing) {
+  (void)x_dtype;
+  (void)routing;
+  if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
+  return fwd_bytes(n_tokens, dim, k, kernel_size);
+}
+
+int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
+                const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                int64_t n_tokens, int64_t seq_len, int64_t dim, int64_t k, int64_t kernel_size,
+                int x_dtype, int alpha_dtype, int basis_dtype, int activation, int routing,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  int rc;
+  if ((rc = check_dims(n_tokens, dim, k, kernel_size)) != MOC_OK) return rc;
+  if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
+  if ((rc = check_seq(cu_seqlens, n_seqs, seq_len)) != MOC_OK) return rc;
+  if (!x || !alpha || !basis || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
+  const size_t need = fwd_bytes(n_tokens, dim, k, kernel_size);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  moc::Problem p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k,
+                                kernel_size, x_dtype, alpha_dtype, basis_dtype, activation,
+                                routing);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Carve cv{static_cast<char*>(workspace), 0};
+  float* a_r = cv.take<float>(size_t(n_tokens * k));
+  float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
+  moc::launch_prep(p, alpha, basis, a_r, basis_c, st);
+  moc::launch_forward_generic(p, x, a_r, basis_c, y, st);
+  return hip_status("moc_forward launch");
+}
+
+size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
+                                    int64_t kernel_size, int x_dtype, int routing) {
+  if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
+  moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
+                                MOC_DT_F32, MOC_DT_F32, 0, routing);
+  return bwd_bytes(p);
+}
+
+int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy, void* dx,
+                 void* dalpha, void* dbasis, const void* cu_seqlens, int cu_seqlens_i64,
+                 int64_t n_seqs, int64_t n_tokens, int64_t seq_len, int64_t dim, int64_t k,
+                 int64_t kernel_size, int x_dtype, int alpha_dtype, int basis_dtype,
+                 int activation, int routing, void* workspace, size_t workspace_bytes,
+                 void* stream) {
+  g_err[0] = '\0';
+  int rc;
+  if ((rc = check_dims(n_tokens, dim, k, kernel_size)) != MOC_OK) return rc;
+  if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
+  if ((rc = check_seq(cu_seqlens, n_seqs, seq_len)) != MOC_OK) return rc;
+  if (!x || !alpha || !basis || !dy || !dalpha || !dbasis)
+    return fail(MOC_ERR_ARG, "null tensor pointer");
+  if ((n_tokens + 255) / 256 > 65535)
+    return fail(MOC_ERR_ARG, "n_tokens too large for the backward grid: %lld", (long long)n_tokens);
+  moc::Problem p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k,
+                                kernel_size, x_dtype, alpha_dtype, basis_dtype, activation,
+                                routing);
+  const size_t need = bwd_bytes(p);
+  if (workspace_bytes < need || !workspace)
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Carve cv{static_cast<char*>(workspace), 0};
+  float* a_r = cv.take<float>(size_t(n_tokens * k));
+  float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
+  float* scratch = cv.take<float>(moc::generic_bwd_scratch_floats(p));
+  moc::launch_prep(p, alpha, basis, a_r, basis_c, st);
+  moc::launch_backward_generic(p, x, dy, dx, dalpha, dbasis, a_r, basis_c, scratch, st);
+  return hip_status("moc_backward launch");
+}
+
+int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
+               int64_t cache_stride_b, int64_t cache_stride_d, int64_t cache_stride_s, void* y,
+               int64_t batch, int64_t dim, int64_t k, int64_t kernel_size, int x_dtype,
+               int alpha_dtype, int basis_dtype, int activation, int routing, void* stream) {
+  g_err[0] = '\0';
+  int rc;
+  if ((rc = check_dims(batch, dim, k, kernel_size)) != MOC_OK) return rc;
+  if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
+  if (batch > kMaxBatch) return fail(MOC_ERR_ARG, "batch too large: %lld", (long long)batch);
+  if (!x || !alpha || !basis || !cache || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
+  moc::launch_update_generic(x, alpha, basis, cache, cache_stride_b, cache_stride_d,
+                             cache_stride_s, y, batch, dim, k, kernel_size, x_dtype, alpha_dtype,
+                             basis_dtype, activation, routing, static_cast<hipStream_t>(stream));
+  return hip_status("moc_update launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,96 @@
+// Shared device helpers for the MoC HIP kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moc {
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+enum Route : int { ROUTE_ALPHA = 0, ROUTE_SOFTMAX = 1, ROUTE_EXP = 2 };
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+  __bf16 h = static_cast<__bf16>(v);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+// Round v to the precision of storage dtype dt and return it as fp32.
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == DT_BF16) return bf16_to_f32(f32_to_bf16(v));
+  if (dt == DT_F16) return static_cast<float>(static_cast<_Float16>(v));
+  return v;
+}
+
+__device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
+  if (dt == DT_F32) return static_cast<const float*>(p)[i];
+  if (dt == DT_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+}
+
+__device__ __forceinline__ void store_any(void* p, int dt, int64_t i, float v) {
+  if (dt == DT_F32) {
+    static_cast<float*>(p)[i] = v;
+  } else if (dt == DT_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+  } else {
+    static_cast<_Float16*>(p)[i] = static_cast<_Float16>(v);
+  }
+}
+
+// Logistic function with the hardware exp2 / reciprocal (v_exp_f32, v_rcp_f32).
+__device__ __forceinline__ float sigmoid_f(float p) {
+  const float e = __builtin_amdgcn_exp2f(-p * 1.4426950408889634f);
+  return __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// Sequence layout of the flat token axis [0, n_tokens).
+//   fixed : sequences of seq_len tokens back to back ([B,T,D] viewed as [B*T,D])
+//   packed: token n of sequence j lies in [cu[j], cu[j+1]).
+// bounds() returns [lo, hi) of the sequence holding token t, clamped to
+// [0, n_tokens] and always containing t, so every access derived from it stays
+// inside the token axis whatever cu_seqlens holds.
+struct SeqLayout {
+  const void* cu;
+  int cu64;
+  int64_t n_seqs;
+  int64_t seq_len;
+  int64_t n_tokens;
+
+  __device__ __forceinline__ int64_t cu_at(int64_t j) const {
+    return cu64 ? static_cast<const int64_t*>(cu)[j]
+                : static_cast<int64_t>(static_cast<const int32_t*>(cu)[j]);
+  }
+
+  __device__ __forceinline__ void bounds(int64_t t, int64_t& lo, int64_t& hi) const {
+    if (cu == nullptr) {
+      lo = (t / seq_len) * seq_len;
+      hi = lo + seq_len;
+      if (hi > n_tokens) hi = n_tokens;
+      return;
+    }
+    // largest j in [0, n_seqs] with cu[j] <= t
+    int64_t a = 0, b = n_seqs;  // invariant: answer in [a, b] or -1
+    if (cu_at(0) > t) {
+      lo = t;
+      hi = t + 1;
+      return;
+    }
+    while (a < b) {
+      const int64_t m = (a + b + 1) >> 1;
+      if (cu_at(m) <= t) a = m; else b = m - 1;
+    }
+    lo = cu_at(a);
+    hi = (a < n_seqs) ? cu_at(a + 1) : t + 1;
+    if (lo < 0) lo = 0;
+    if (lo > t) lo = t;
+    if (hi > n_tokens) hi = n_tokens;
+    if (hi <= t) hi = t + 1;
+  }
+};
+
+}  // namespace moc

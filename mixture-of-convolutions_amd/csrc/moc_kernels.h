@@ -1,0 +1,35 @@
+// Internal host-side interface between the C ABI (moc_capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "moc_common.h"
+
+namespace moc {
+
+struct Problem {
+  SeqLayout seq;     // token axis layout (n_tokens lives here)
+  int64_t n_tokens;
+  int64_t D, K, S;
+  int x_dt, a_dt, b_dt;
+  int activation;    // 0 = none, 1 = SiLU
+  int routing;       // Route
+};
+
+// generic path (moc_generic.hip)
+void launch_prep(const Problem& p, const void* alpha, const void* basis, float* a_r,
+                 float* basis_c, hipStream_t st);
+void launch_forward_generic(const Problem& p, const void* x, const float* a_r,
+                            const float* basis_c, void* y, hipStream_t st);
+size_t generic_bwd_scratch_floats(const Problem& p);
+void launch_backward_generic(const Problem& p, const void* x, const void* dy, void* dx,
+                             void* dalpha, void* dbasis, const float* a_r,
+                             const float* basis_c, float* scratch, hipStream_t st);
+void launch_update_generic(const void* x, const void* alpha, const void* basis, void* cache,
+                           int64_t cs_b, int64_t cs_d, int64_t cs_s, void* y, int64_t B,
+                           int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
+                           int activation, int routing, hipStream_t st);
+
+}  // namespace moc

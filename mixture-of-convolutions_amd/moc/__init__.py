@@ -1,0 +1,16 @@
+"""Mixture-of-Convolutions on MI355X: drop-in for the reference ``moc`` package.
+
+The forward, backward and decode paths run as hand-written gfx950 HIP kernels
+in libmoc_hip.so, reached through a C ABI (include/moc_hip.h).
+"""
+from .api import MoC, moc_hip, moc_triton
+from .optim import match_lr_to_init_std, match_weight_decay_to_lr, moc_fan_in_std
+
+__all__ = [
+    "MoC",
+    "moc_triton",
+    "moc_hip",
+    "moc_fan_in_std",
+    "match_lr_to_init_std",
+    "match_weight_decay_to_lr",
+]

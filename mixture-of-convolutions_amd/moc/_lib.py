@@ -1,0 +1,113 @@
+"""ctypes binding of libmoc_hip.so (C ABI declared in include/moc_hip.h).
+
+The library is loaded on first use from this package's directory.  There is no
+fallback: if it is missing or fails to load, every MoC op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
+
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
+ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
+
+_DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float16: DT_F16}
+
+EXPORTED_SYMBOLS = (
+    "moc_abi_version",
+    "moc_last_error",
+    "moc_forward_workspace_bytes",
+    "moc_forward",
+    "moc_backward_workspace_bytes",
+    "moc_backward",
+    "moc_update",
+)
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_l = ctypes.c_int64
+_z = ctypes.c_size_t
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.moc_abi_version.argtypes = []
+    lib.moc_abi_version.restype = _i
+    lib.moc_last_error.argtypes = []
+    lib.moc_last_error.restype = ctypes.c_char_p
+    lib.moc_forward_workspace_bytes.argtypes = [_l, _l, _l, _l, _i, _i]
+    lib.moc_forward_workspace_bytes.restype = _z
+    lib.moc_backward_workspace_bytes.argtypes = [_l, _l, _l, _l, _i, _i]
+    lib.moc_backward_workspace_bytes.restype = _z
+    lib.moc_forward.argtypes = [
+        _p, _p, _p, _p,            # x, alpha, basis, y
+        _p, _i, _l,                # cu_seqlens, cu_seqlens_i64, n_seqs
+        _l, _l,                    # n_tokens, seq_len
+        _l, _l, _l,                # dim, k, kernel_size
+        _i, _i, _i,                # dtypes
+        _i, _i,                    # activation, routing
+        _p, _z, _p,                # workspace, bytes, stream
+    ]
+    lib.moc_forward.restype = _i
+    lib.moc_backward.argtypes = [
+        _p, _p, _p, _p,            # x, alpha, basis, dy
+        _p, _p, _p,                # dx, dalpha, dbasis
+        _p, _i, _l,
+        _l, _l,
+        _l, _l, _l,
+        _i, _i, _i,
+        _i, _i,
+        _p, _z, _p,
+    ]
+    lib.moc_backward.restype = _i
+    lib.moc_update.argtypes = [
+        _p, _p, _p, _p,            # x, alpha, basis, cache
+        _l, _l, _l,                # cache strides (elements)
+        _p,                        # y
+        _l, _l, _l, _l,            # batch, dim, k, kernel_size
+        _i, _i, _i,                # dtypes
+        _i, _i, _p,                # activation, routing, stream
+    ]
+    lib.moc_update.restype = _i
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises RuntimeError if it is not built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise RuntimeError(
+                        f"{LIB_PATH} is not built; run "
+                        "`python mixture-of-convolutions_amd/build_lib.py` "
+                        "(or __graft_entry__.build()) first"
+                    )
+                handle = ctypes.CDLL(str(LIB_PATH))
+                _declare(handle)
+                _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().moc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dt]
+    except KeyError:
+        raise TypeError(f"libmoc_hip has no kernel operand of dtype {dt}") from None
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

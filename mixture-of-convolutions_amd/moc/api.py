@@ -1,0 +1,350 @@
+"""Public MoC API, drop-in for the reference's moc/api.py.
+
+Same names, signatures, validation (exception types and messages), return
+conventions, parameter names and cache layout as the reference
+(moc/api.py:15-425).  What differs is underneath: the autograd functions call
+the gfx950 HIP kernels of libmoc_hip.so through ``ops`` and
+
+* the backward recomputes the pre-activation inside the kernel instead of
+  re-running the forward (moc/api.py:176-183);
+* ``MoC.forward`` / ``MoC.step`` hand the router *logits* to the kernels, which
+  apply softmax / exp themselves and return d(logits) directly, so the router
+  activation and its gradient cost no separate kernels (moc/api.py:383-388).
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.autograd.function import once_differentiable
+
+from . import ops
+from ._lib import ROUTE_ALPHA, ROUTE_EXP, ROUTE_SOFTMAX
+from .optim import moc_fan_in_std
+
+SUPPORTED_DTYPES = (torch.bfloat16, torch.float32)
+
+_ROUTING_CODES = {"softmax": ROUTE_SOFTMAX, "exp": ROUTE_EXP}
+
+
+# ---------------------------------------------------------------------------
+# validation (moc/api.py:18-92, 198-215)
+
+def activation_flag(activation: str | None) -> int:
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"unsupported activation: {activation}")
+    return 0 if activation is None else 1
+
+
+def check_router_activation(router_activation: str) -> None:
+    if router_activation not in _ROUTING_CODES:
+        raise ValueError(
+            f"unsupported router activation: {router_activation}; "
+            "expected 'softmax' or 'exp'"
+        )
+
+
+def check_common_dtypes(x: torch.Tensor, alpha: torch.Tensor, basis: torch.Tensor) -> None:
+    if not all(t.is_cuda for t in (x, alpha, basis)):
+        raise ValueError("x, alpha, and basis must all be CUDA tensors")
+    if alpha.device != x.device or basis.device != x.device:
+        raise ValueError("x, alpha, and basis must be on the same CUDA device")
+    if x.dtype not in SUPPORTED_DTYPES:
+        raise TypeError(f"unsupported x dtype: {x.dtype}")
+    if not alpha.is_floating_point():
+        raise TypeError(f"alpha must be floating point, got {alpha.dtype}")
+    if not basis.is_floating_point():
+        raise TypeError(f"basis must be floating point, got {basis.dtype}")
+
+
+def check_fixed_inputs(x: torch.Tensor, alpha: torch.Tensor, basis: torch.Tensor
+                       ) -> tuple[int, int, int, int, int]:
+    check_common_dtypes(x, alpha, basis)
+    if (x.ndim, alpha.ndim, basis.ndim) != (3, 3, 3):
+        raise ValueError("fixed-length inputs must have x/alpha/basis ranks 3/3/3")
+    B, T, D = x.shape
+    Ba, Ta, K = alpha.shape
+    Kb, KS, Db = basis.shape
+    if (Ba, Ta) != (B, T):
+        raise ValueError(f"x and alpha batch/time shapes differ: {(B, T)} vs {(Ba, Ta)}")
+    if (Kb, Db) != (K, D):
+        raise ValueError(f"alpha/basis dimensions disagree: K,D={(K, D)} vs {(Kb, Db)}")
+    if min(B, T, D, K, KS) <= 0:
+        raise ValueError("B, T, D, K, and KS must all be positive")
+    return B, T, D, K, KS
+
+
+def check_packed_inputs(x: torch.Tensor, alpha: torch.Tensor, basis: torch.Tensor,
+                        cu_seqlens: torch.Tensor, max_seqlen: int
+                        ) -> tuple[int, int, int, int, int]:
+    check_common_dtypes(x, alpha, basis)
+    if (x.ndim, alpha.ndim, basis.ndim) != (2, 2, 3):
+        raise ValueError("packed inputs must have x/alpha/basis ranks 2/2/3 internally")
+    N, D = x.shape
+    Na, K = alpha.shape
+    Kb, KS, Db = basis.shape
+    if Na != N:
+        raise ValueError(f"x and alpha token counts differ: {N} vs {Na}")
+    if (Kb, Db) != (K, D):
+        raise ValueError(f"alpha/basis dimensions disagree: K,D={(K, D)} vs {(Kb, Db)}")
+    if min(N, D, K, KS) <= 0:
+        raise ValueError("total tokens, D, K, and KS must all be positive")
+    if not cu_seqlens.is_cuda or cu_seqlens.device != x.device:
+        raise ValueError("cu_seqlens must be a CUDA tensor on the same device as x")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be rank-1 with at least two entries")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise TypeError("cu_seqlens must have dtype torch.int32 or torch.int64")
+    if not isinstance(max_seqlen, int) or max_seqlen <= 0:
+        raise ValueError("max_seqlen must be a positive Python int")
+    return N, cu_seqlens.numel() - 1, D, K, KS
+
+
+def _canonicalize_packed_input(x: torch.Tensor, alpha: torch.Tensor
+                               ) -> tuple[torch.Tensor, torch.Tensor, bool]:
+    if x.ndim == 2 and alpha.ndim == 2:
+        return x, alpha, False
+    if x.ndim == 3 and alpha.ndim == 3 and x.shape[0] == 1 and alpha.shape[0] == 1:
+        return x[0], alpha[0], True
+    raise ValueError("varlen x/alpha must be [N,D]/[N,K] or [1,N,D]/[1,N,K]")
+
+
+def _check_cache(x: torch.Tensor, basis: torch.Tensor, cache: torch.Tensor) -> None:
+    B, _, D = x.shape
+    KS = basis.shape[1]
+    if tuple(cache.shape) != (B, D, KS):
+        raise ValueError(f"cache must have shape {(B, D, KS)}, got {tuple(cache.shape)}")
+    if cache.device != x.device or cache.dtype != x.dtype:
+        raise ValueError("cache must have the same device and dtype as x")
+
+
+def _final_state(x: torch.Tensor, cache: torch.Tensor | None, kernel_size: int) -> torch.Tensor:
+    """The last ``kernel_size`` inputs as [B,D,S] (moc/api.py:218-227)."""
+    B, T, D = x.shape
+    xt = x.transpose(1, 2)
+    if T >= kernel_size:
+        return xt[:, :, T - kernel_size:].contiguous()
+    head = x.new_zeros(B, D, kernel_size - T) if cache is None else cache[:, :, T:]
+    return torch.cat((head, xt), dim=-1)
+
+
+# ---------------------------------------------------------------------------
+# autograd
+
+def _prepare(ctx_like, x, alpha, basis, cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices):
+    """Shared argument handling of the two autograd functions
+    (moc/api.py:108-134).  Returns contiguous (x, alpha, basis, cu_seqlens)."""
+    x = x.contiguous()
+    alpha = alpha.contiguous()
+    basis = basis.contiguous()
+    if cu_seqlens is not None:
+        if max_seqlen is None:
+            raise ValueError("max_seqlen is required when cu_seqlens is provided")
+        cu_seqlens = cu_seqlens.contiguous()
+        check_packed_inputs(x, alpha, basis, cu_seqlens, max_seqlen)
+        if chunk_indices is not None:
+            ops.check_chunk_indices(chunk_indices.contiguous(), cu_seqlens)
+        elif cu_seqlens_cpu is not None:
+            ops.check_cu_seqlens_cpu(cu_seqlens_cpu, cu_seqlens)
+    else:
+        if max_seqlen is not None:
+            raise ValueError("max_seqlen must be None when cu_seqlens is None")
+        if cu_seqlens_cpu is not None or chunk_indices is not None:
+            raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+        check_fixed_inputs(x, alpha, basis)
+    return x, alpha, basis, cu_seqlens
+
+
+def _moc_forward(ctx, x, alpha, basis, activation, routing, cu_seqlens, max_seqlen,
+                 cu_seqlens_cpu, chunk_indices):
+    x, alpha, basis, cu_seqlens = _prepare(ctx, x, alpha, basis, cu_seqlens, max_seqlen,
+                                           cu_seqlens_cpu, chunk_indices)
+    act = activation_flag(activation)
+    y = ops.launch_forward(x, alpha, basis, activation_flag=act, cu_seqlens=cu_seqlens,
+                           routing=routing)
+    if cu_seqlens is None:
+        ctx.save_for_backward(x, alpha, basis)
+    else:
+        ctx.save_for_backward(x, alpha, basis, cu_seqlens)
+    ctx.act = act
+    ctx.routing = routing
+    ctx.varlen = cu_seqlens is not None
+    return y
+
+
+def _moc_backward(ctx, dy):
+    saved = ctx.saved_tensors
+    x, alpha, basis = saved[:3]
+    cu_seqlens = saved[3] if ctx.varlen else None
+    return ops.launch_backward(x, alpha, basis, dy, activation_flag=ctx.act,
+                               need_x=ctx.needs_input_grad[0], cu_seqlens=cu_seqlens,
+                               routing=ctx.routing)
+
+
+class _MoCFunction(torch.autograd.Function):
+    """MoC on routing weights ``alpha`` (moc/api.py:95-195)."""
+
+    @staticmethod
+    def forward(ctx, x, alpha, basis, activation, cu_seqlens, max_seqlen, cu_seqlens_cpu,
+                chunk_indices):
+        return _moc_forward(ctx, x, alpha, basis, activation, ROUTE_ALPHA, cu_seqlens,
+                            max_seqlen, cu_seqlens_cpu, chunk_indices)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        dx, dalpha, dbasis = _moc_backward(ctx, dy)
+        return dx, dalpha, dbasis, None, None, None, None, None
+
+
+class _MoCRoutedFunction(torch.autograd.Function):
+    """MoC on router logits: alpha = softmax(logits) or exp(logits) is formed
+    inside the kernels and the backward returns d(logits)."""
+
+    @staticmethod
+    def forward(ctx, x, logits, basis, activation, router_activation, cu_seqlens, max_seqlen,
+                cu_seqlens_cpu, chunk_indices):
+        return _moc_forward(ctx, x, logits, basis, activation, _ROUTING_CODES[router_activation],
+                            cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        dx, dlogits, dbasis = _moc_backward(ctx, dy)
+        return dx, dlogits, dbasis, None, None, None, None, None, None
+
+
+def _apply(x, a, basis, activation, router_activation, cu_seqlens=None, max_seqlen=None,
+           cu_seqlens_cpu=None, chunk_indices=None):
+    if router_activation is None:
+        return _MoCFunction.apply(x, a, basis, activation, cu_seqlens, max_seqlen,
+                                  cu_seqlens_cpu, chunk_indices)
+    return _MoCRoutedFunction.apply(x, a, basis, activation, router_activation, cu_seqlens,
+                                    max_seqlen, cu_seqlens_cpu, chunk_indices)
+
+
+def _step(x, a, basis, cache, activation, router_activation):
+    """Decode step (moc/api.py:242-259): in place on ``cache``."""
+    _, T, _, _, _ = check_fixed_inputs(x, a, basis)
+    if T != 1:
+        raise ValueError(f"step expects sequence length 1, got {T}")
+    _check_cache(x, basis, cache)
+    routing = ROUTE_ALPHA if router_activation is None else _ROUTING_CODES[router_activation]
+    y = ops.launch_update(x[:, 0], a[:, 0], basis, cache,
+                          activation_flag=activation_flag(activation), routing=routing)
+    return y[:, None]
+
+
+def _dispatch(x, a, basis, cache, output_final_state, activation, router_activation,
+              cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices):
+    """Routing of moc/api.py:262-335 for weights (router_activation None) or
+    logits."""
+    activation_flag(activation)
+    if cu_seqlens is None:
+        if cu_seqlens_cpu is not None or chunk_indices is not None:
+            raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+        B, T, D, K, KS = check_fixed_inputs(x, a, basis)
+        if cache is not None:
+            _check_cache(x, basis, cache)
+            if T == 1:
+                y = _step(x, a, basis, cache, activation, router_activation)
+                return y, (cache if output_final_state else None)
+            # Prefill continuing from a cache: the cached tokens are prepended as
+            # history; their own outputs are computed and dropped.
+            hist = cache.transpose(1, 2)
+            a_hist = a.new_zeros(B, KS, K)
+            y = _apply(torch.cat((hist, x), 1), torch.cat((a_hist, a), 1), basis, activation,
+                       router_activation)[:, KS:]
+        else:
+            y = _apply(x, a, basis, activation, router_activation)
+        return y, (_final_state(x, cache, KS) if output_final_state else None)
+
+    if cache is not None or output_final_state:
+        raise ValueError("cache and output_final_state are only supported for fixed-length inputs")
+    if max_seqlen is None:
+        raise ValueError("max_seqlen is required for varlen inputs")
+    xp, ap, restore = _canonicalize_packed_input(x, a)
+    check_packed_inputs(xp, ap, basis, cu_seqlens, max_seqlen)
+    y = _apply(xp, ap, basis, activation, router_activation, cu_seqlens, max_seqlen,
+               cu_seqlens_cpu, chunk_indices)
+    return (y[None] if restore else y), None
+
+
+def moc_triton(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    cache: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    activation: str | None = None,
+    cu_seqlens: Optional[torch.Tensor] = None,
+    max_seqlen: Optional[int] = None,
+    cu_seqlens_cpu: Optional[torch.Tensor] = None,
+    chunk_indices: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Functional MoC on routing weights (moc/api.py:262-335), backed by the
+    HIP kernels.  The name is kept for drop-in compatibility; ``moc_hip`` is the
+    same function."""
+    return _dispatch(x, alpha, basis, cache, output_final_state, activation, None,
+                     cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices)
+
+
+moc_hip = moc_triton
+
+
+class MoC(nn.Module):
+    """Mixture-of-Convolutions layer (moc/api.py:338-425).
+
+    Parameters ``conv_bases`` [k, kernel_size, dim] and ``router`` [k, z_dim]
+    have the reference's names, shapes and initialisation, so state dicts load
+    unchanged.
+    """
+
+    def __init__(self, dim: int, z_dim: int, kernel_size: int, k: int,
+                 activation: str | None = None, init_std: float | None = None,
+                 router_activation: str = "softmax") -> None:
+        super().__init__()
+        activation_flag(activation)
+        check_router_activation(router_activation)
+        self.dim = dim
+        self.z_dim = z_dim
+        self.kernel_size = kernel_size
+        self.k = k
+        self.activation = activation
+        self.router_activation = router_activation
+        self.conv_bases = nn.Parameter(torch.empty(k, kernel_size, dim))
+        self.router = nn.Parameter(torch.zeros(k, z_dim))
+        if init_std is None:
+            init_std = moc_fan_in_std(k, kernel_size)
+        bound = init_std * math.sqrt(3)
+        nn.init.uniform_(self.conv_bases, a=-bound, b=bound)
+
+    def forward(self, x: torch.Tensor, z: torch.Tensor, cache: torch.Tensor | None = None,
+                output_final_state: bool = False, cu_seqlens: Optional[torch.Tensor] = None,
+                max_seqlen: Optional[int] = None, cu_seqlens_cpu: Optional[torch.Tensor] = None,
+                chunk_indices: Optional[torch.Tensor] = None
+                ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        logits = F.linear(z, self.router)
+        return _dispatch(x, logits, self.conv_bases, cache, output_final_state,
+                         self.activation, self.router_activation, cu_seqlens, max_seqlen,
+                         cu_seqlens_cpu, chunk_indices)
+
+    def step(self, x: torch.Tensor, z: torch.Tensor, cache: torch.Tensor | None = None,
+             output_final_state: bool = False) -> tuple[torch.Tensor, torch.Tensor | None]:
+        if x.ndim != 3 or x.shape[1] != 1:
+            raise ValueError(f"step expects x with shape [B, 1, D], got {tuple(x.shape)}")
+        if z.ndim != 3 or z.shape[:2] != x.shape[:2]:
+            raise ValueError(f"step expects z with shape [B, 1, Z], got {tuple(z.shape)}")
+        if cache is None:
+            cache = x.new_zeros(x.shape[0], self.dim, self.kernel_size)
+        return self.forward(x, z, cache=cache, output_final_state=output_final_state)
+
+    @property
+    def state_size(self) -> int:
+        return self.dim * self.kernel_size
+
+
+__all__ = ["MoC", "moc_triton", "moc_hip"]

@@ -1,0 +1,242 @@
+"""Launch layer: torch tensors in, libmoc_hip.so C-ABI calls out.
+
+Each ``launch_*`` function keeps the name and argument meaning of the
+reference's launch function it replaces (moc/ops.py:129-362) and calls one
+entry point of the HIP library on the current stream of the tensors' device.
+Output tensors and the workspace come from torch's caching allocator; the
+library itself never allocates.
+
+``prepare_chunk_indices`` / ``clear_chunk_index_cache`` (moc/ops.py:30-104) are
+kept for callers that precompute chunk indices; the HIP kernels locate sequence
+boundaries from ``cu_seqlens`` directly and do not need them.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from ._lib import ROUTE_ALPHA
+
+VARLEN_BLOCK_T = 64
+_CHUNK_CACHE_SIZE = 4
+_chunk_index_cache: list[tuple] = []
+
+# operand dtypes the kernels read directly; others are cast to fp32 around the call
+_KERNEL_OPERAND_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def clear_chunk_index_cache() -> None:
+    _chunk_index_cache.clear()
+
+
+def prepare_chunk_indices(
+    cu_seqlens: torch.Tensor,
+    chunk_size: int = VARLEN_BLOCK_T,
+    cu_seqlens_cpu: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """[n_chunks, 2] int32 (sequence id, chunk id within the sequence) for
+    ``chunk_size``-token chunks; a 4-entry LRU keyed on tensor identity and
+    version (same contract as moc/ops.py:47-104)."""
+    if not isinstance(chunk_size, int) or chunk_size <= 0:
+        raise ValueError("chunk_size must be a positive Python int")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be rank-1 with at least two entries")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise TypeError("cu_seqlens must have dtype torch.int32 or torch.int64")
+    if cu_seqlens_cpu is not None:
+        check_cu_seqlens_cpu(cu_seqlens_cpu, cu_seqlens)
+
+    key = (cu_seqlens, cu_seqlens._version, chunk_size, cu_seqlens_cpu,
+           None if cu_seqlens_cpu is None else cu_seqlens_cpu._version)
+    for i, entry in enumerate(_chunk_index_cache):
+        if all(a is b if isinstance(a, torch.Tensor) or a is None else a == b
+               for a, b in zip(entry[:5], key)):
+            _chunk_index_cache.insert(0, _chunk_index_cache.pop(i))
+            return entry[5]
+
+    src = cu_seqlens_cpu if cu_seqlens_cpu is not None else cu_seqlens
+    lengths = (src[1:] - src[:-1]).to(torch.int64)
+    counts = torch.div(lengths + chunk_size - 1, chunk_size, rounding_mode="floor")
+    seq_ids = torch.repeat_interleave(torch.arange(counts.numel(), device=src.device), counts)
+    first = F.pad(counts.cumsum(0), (1, 0))[:-1]
+    local = torch.arange(seq_ids.numel(), device=src.device) - first[seq_ids]
+    chunks = torch.stack((seq_ids, local), 1).to(device=cu_seqlens.device, dtype=torch.int32)
+    chunks = chunks.contiguous()
+    _chunk_index_cache.insert(0, (*key, chunks))
+    del _chunk_index_cache[_CHUNK_CACHE_SIZE:]
+    return chunks
+
+
+def check_cu_seqlens_cpu(cu_seqlens_cpu: torch.Tensor, cu_seqlens: torch.Tensor) -> None:
+    """Same acceptance rules as moc/ops.py:59-65."""
+    if cu_seqlens_cpu.device.type != "cpu":
+        raise ValueError("cu_seqlens_cpu must be a CPU tensor")
+    if cu_seqlens_cpu.ndim != 1 or cu_seqlens_cpu.numel() != cu_seqlens.numel():
+        raise ValueError("cu_seqlens_cpu must match cu_seqlens shape")
+    if cu_seqlens_cpu.dtype not in (torch.int32, torch.int64):
+        raise TypeError("cu_seqlens_cpu must have dtype torch.int32 or torch.int64")
+
+
+def check_chunk_indices(chunk_indices: torch.Tensor, cu_seqlens: torch.Tensor) -> None:
+    """Same acceptance rules as moc/ops.py:118-126."""
+    if not chunk_indices.is_cuda or chunk_indices.device != cu_seqlens.device:
+        raise ValueError("chunk_indices must be a CUDA tensor on the same device as cu_seqlens")
+    if chunk_indices.ndim != 2 or chunk_indices.shape[1] != 2:
+        raise ValueError("chunk_indices must have shape [num_chunks, 2]")
+    if chunk_indices.dtype not in (torch.int32, torch.int64):
+        raise TypeError("chunk_indices must have dtype torch.int32 or torch.int64")
+    if not chunk_indices.is_contiguous():
+        raise ValueError("chunk_indices must be contiguous")
+
+
+def _operand(t: torch.Tensor) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.dtype in _KERNEL_OPERAND_DTYPES else t.float()
+
+
+def _seq_args(x: torch.Tensor, cu_seqlens: torch.Tensor | None):
+    """(cu_ptr, cu_is_i64, n_seqs, n_tokens, seq_len, dim) of a [B,T,D] or [N,D] x."""
+    if cu_seqlens is None:
+        B, T, D = x.shape
+        return None, 0, 0, B * T, T, D
+    N, D = x.shape
+    return (cu_seqlens.data_ptr(), int(cu_seqlens.dtype == torch.int64),
+            cu_seqlens.numel() - 1, N, 0, D)
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def launch_forward(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    *,
+    activation_flag: int,
+    cu_seqlens: torch.Tensor | None = None,
+    cu_seqlens_cpu: torch.Tensor | None = None,
+    chunk_indices: torch.Tensor | None = None,
+    routing: int = ROUTE_ALPHA,
+) -> torch.Tensor:
+    """y = MoC(x, alpha, basis) (moc/ops.py:129-194).  ``alpha`` holds routing
+    weights (routing=0) or router logits whose softmax (1) / exp (2) is fused."""
+    del cu_seqlens_cpu, chunk_indices  # boundaries come from cu_seqlens on device
+    L = _lib.lib()
+    x = x.contiguous()
+    a = _operand(alpha)
+    b = _operand(basis)
+    K, S, _ = b.shape
+    cu_ptr, cu64, n_seqs, n_tokens, seq_len, D = _seq_args(x, cu_seqlens)
+    out = torch.empty_like(x)
+    x_dt = _lib.dtype_code(x.dtype)
+    nbytes = L.moc_forward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
+    ws = _workspace(nbytes, x.device)
+    with torch.cuda.device(x.device):
+        rc = L.moc_forward(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+            cu_ptr, cu64, n_seqs, n_tokens, seq_len, D, K, S,
+            x_dt, _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
+            int(activation_flag), int(routing),
+            ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device),
+        )
+    _lib.check(rc, "moc_forward")
+    return out
+
+
+def launch_preact(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    *,
+    cu_seqlens: torch.Tensor | None = None,
+    cu_seqlens_cpu: torch.Tensor | None = None,
+    chunk_indices: torch.Tensor | None = None,
+    routing: int = ROUTE_ALPHA,
+) -> torch.Tensor:
+    """Pre-activation P (moc/ops.py:197-213).  The fused backward recomputes P
+    itself; this stays for callers that want P explicitly."""
+    return launch_forward(x, alpha, basis, activation_flag=0, cu_seqlens=cu_seqlens,
+                          cu_seqlens_cpu=cu_seqlens_cpu, chunk_indices=chunk_indices,
+                          routing=routing)
+
+
+def launch_backward(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    moc_dy: torch.Tensor,
+    preact: torch.Tensor | None = None,
+    *,
+    activation_flag: int,
+    need_x: bool,
+    cu_seqlens: torch.Tensor | None = None,
+    cu_seqlens_cpu: torch.Tensor | None = None,
+    chunk_indices: torch.Tensor | None = None,
+    routing: int = ROUTE_ALPHA,
+) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
+    """(dx or None, dalpha, dbasis) (moc/ops.py:216-338).  ``preact`` is
+    accepted for signature compatibility and ignored: the kernel recomputes the
+    pre-activation in registers.  With routing != 0, ``dalpha`` is the
+    gradient with respect to the logits."""
+    del preact, cu_seqlens_cpu, chunk_indices
+    L = _lib.lib()
+    x = x.contiguous()
+    dy = moc_dy.contiguous()
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    a = _operand(alpha)
+    b = _operand(basis)
+    K, S, _ = b.shape
+    cu_ptr, cu64, n_seqs, n_tokens, seq_len, D = _seq_args(x, cu_seqlens)
+    dx = torch.empty_like(x) if need_x else None
+    dalpha = torch.empty_like(a)
+    dbasis = torch.empty_like(b)
+    x_dt = _lib.dtype_code(x.dtype)
+    nbytes = L.moc_backward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
+    ws = _workspace(nbytes, x.device)
+    with torch.cuda.device(x.device):
+        rc = L.moc_backward(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(),
+            None if dx is None else dx.data_ptr(), dalpha.data_ptr(), dbasis.data_ptr(),
+            cu_ptr, cu64, n_seqs, n_tokens, seq_len, D, K, S,
+            x_dt, _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
+            int(activation_flag), int(routing),
+            ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device),
+        )
+    _lib.check(rc, "moc_backward")
+    if dalpha.dtype != alpha.dtype:
+        dalpha = dalpha.to(alpha.dtype)
+    if dbasis.dtype != basis.dtype:
+        dbasis = dbasis.to(basis.dtype)
+    return dx, dalpha, dbasis
+
+
+def launch_update(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    cache: torch.Tensor,
+    *,
+    activation_flag: int,
+    routing: int = ROUTE_ALPHA,
+) -> torch.Tensor:
+    """One decode step, cache updated in place (moc/ops.py:341-362).
+    x [B,D], alpha [B,K] (weights or logits), cache [B,D,S] (any strides)."""
+    L = _lib.lib()
+    x = x.contiguous()
+    a = _operand(alpha)
+    b = _operand(basis)
+    B, D = x.shape
+    K, S, _ = b.shape
+    out = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        rc = L.moc_update(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), cache.data_ptr(),
+            *cache.stride(), out.data_ptr(), B, D, K, S,
+            _lib.dtype_code(x.dtype), _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
+            int(activation_flag), int(routing), _lib.stream_ptr(x.device),
+        )
+    _lib.check(rc, "moc_update")
+    return out

@@ -1,0 +1,43 @@
+"""Shared helpers of the GPU parity tests: seeded inputs and the tolerance rule.
+
+Tolerance (fp32 compare against the CPU oracle run on the same inputs, with
+alpha / basis rounded to the compute dtype as verify.py:54-64 does):
+  bf16 I/O : |got - ref| <= 1e-2 * rms(ref) + 1.6e-2 * |ref|   elementwise
+  fp32 I/O : |got - ref| <= 1e-4 * rms(ref) + 1e-5   * |ref|   elementwise
+The reference's own bar (verify.py:20-23) is atol = rtol = 1e-1 (bf16) and
+5e-3 (fp32); both rules above are tighter at the shapes tested.
+"""
+from __future__ import annotations
+
+import torch
+
+TOL = {
+    torch.bfloat16: (1e-2, 1.6e-2),
+    torch.float32: (1e-4, 1e-5),
+}
+
+
+def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype) -> None:
+    got = got.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert got.shape == ref.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{name}: non-finite values"
+    a_rms, r_rel = TOL[dtype]
+    rms = ref.pow(2).mean().sqrt().item() if ref.numel() else 0.0
+    err = (got - ref).abs()
+    bound = a_rms * rms + r_rel * ref.abs() + 1e-30
+    bad = err > bound
+    if bad.any():
+        i = int(torch.argmax((err / bound).flatten()))
+        raise AssertionError(
+            f"{name} ({dtype}): {int(bad.sum())}/{err.numel()} elements out of tolerance; "
+            f"worst at flat {i}: got {got.flatten()[i].item():.6g} ref {ref.flatten()[i].item():.6g} "
+            f"(max abs err {err.max().item():.3g}, rms(ref) {rms:.3g})")
+
+
+def gen(seed: int = 0) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(g, *shape, scale=1.0):
+    return torch.randn(*shape, generator=g) * scale

@@ -1,0 +1,106 @@
+"""The C ABI library without a GPU: it loads, exports every symbol
+include/moc_hip.h declares, sizes workspaces, and rejects bad arguments with the
+documented status codes before touching the device."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from moc import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "moc_hip.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(moc_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared()
+    assert set(names) == set(_lib.EXPORTED_SYMBOLS)
+    for name in names:
+        assert hasattr(L, name), name
+    assert L.moc_abi_version() == 1
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define (MOC_\w+)\s+(-?\d+)", text))
+    assert int(consts["MOC_DT_F32"]) == _lib.DT_F32
+    assert int(consts["MOC_DT_BF16"]) == _lib.DT_BF16
+    assert int(consts["MOC_DT_F16"]) == _lib.DT_F16
+    assert int(consts["MOC_ROUTE_ALPHA"]) == _lib.ROUTE_ALPHA
+    assert int(consts["MOC_ROUTE_SOFTMAX"]) == _lib.ROUTE_SOFTMAX
+    assert int(consts["MOC_ROUTE_EXP"]) == _lib.ROUTE_EXP
+
+
+def test_workspace_queries():
+    L = _lib.lib()
+    for x_dt in (_lib.DT_BF16, _lib.DT_F32):
+        f = L.moc_forward_workspace_bytes(16384, 2048, 16, 4, x_dt, 1)
+        b = L.moc_backward_workspace_bytes(16384, 2048, 16, 4, x_dt, 1)
+        assert f % 256 == 0 and b % 256 == 0 and b >= f
+    assert L.moc_forward_workspace_bytes(0, 2048, 16, 4, 1, 0) == 0
+    assert L.moc_backward_workspace_bytes(16, -1, 16, 4, 1, 0) == 0
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def _fwd(**kw):
+    args = dict(x=FAKE, alpha=FAKE, basis=FAKE, y=FAKE, cu=None, cu64=0, n_seqs=0,
+                n_tokens=8, seq_len=8, dim=16, k=4, ks=4, x_dt=1, a_dt=1, b_dt=1,
+                act=0, route=0, ws=FAKE, ws_bytes=1 << 30, stream=None)
+    args.update(kw)
+    return _lib.lib().moc_forward(*args.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(x_dt=2), -2),          # fp16 x is not a supported compute dtype
+    (dict(a_dt=7), -2),
+    (dict(b_dt=-1), -2),
+    (dict(dim=0), -1),
+    (dict(k=-3), -1),
+    (dict(act=2), -1),
+    (dict(route=3), -1),
+    (dict(x=None), -1),
+    (dict(seq_len=0), -1),
+    (dict(cu=FAKE, n_seqs=0), -1),
+    (dict(ws_bytes=16), -3),
+])
+def test_forward_rejects_bad_arguments(kw, code):
+    assert _fwd(**kw) == code
+    assert _lib.lib().moc_last_error().decode()
+
+
+def test_status_maps_to_runtime_error():
+    rc = _fwd(x_dt=5)
+    with pytest.raises(RuntimeError, match="unsupported x dtype code 5"):
+        _lib.check(rc, "moc_forward")
+
+
+def test_backward_and_update_reject_bad_arguments():
+    L = _lib.lib()
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+                        1, 1, 1, 0, 0, FAKE, 1 << 30, None)
+    assert rc == -1 and b"null" in L.moc_last_error()
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+                        1, 1, 1, 0, 0, FAKE, 8, None)
+    assert rc == -3
+    rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 70000, 16, 4, 4, 1, 1, 1, 0, 0, None)
+    assert rc == -1
+    rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 2, 16, 4, 4, 1, 9, 1, 0, 0, None)
+    assert rc == -2
+
+
+def test_dtype_codes():
+    import torch
+    assert _lib.dtype_code(torch.bfloat16) == 1
+    with pytest.raises(TypeError):
+        _lib.dtype_code(torch.int8)
+    assert isinstance(_lib.lib(), ctypes.CDLL)

@@ -1,0 +1,350 @@
+"""GPU parity: the HIP kernels (through moc -> ctypes -> libmoc_hip.so) against
+the CPU oracle on identical seeded inputs.
+
+Covers the reference's verify.py matrix (moc/../verify.py:243-285: {bf16, fp32} x
+S in {2,4} x {plain, SiLU} x {fixed, varlen in both forms, step} plus mixed
+storage dtypes) and what it leaves out: the MoC module with
+softmax / exp routing, prefill from a cache, final states, need_x=False, int64
+cu_seqlens, sequences shorter than S, D not a multiple of any tile, odd K and
+S, bitwise varlen isolation, bitwise determinism.  Tolerances: tests/_parity.py.
+"""
+from __future__ import annotations
+
+import itertools
+
+import pytest
+import torch
+
+import moc
+from moc import MoC, moc_triton
+from oracle import moc_oracle as O
+from tests._parity import assert_close, gen, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+B, T, D, K = 2, 64, 64, 8
+VARLEN_LENGTHS = [31, 17, 5, 23]
+STEP_T = 8
+
+
+def _verify_inputs(seed=0):
+    g = gen(seed)
+    x = randn(g, B, T, D, scale=0.5)
+    alpha = torch.softmax(randn(g, B, T, K), -1)
+    dy = randn(g, B, T, D, scale=0.1)
+    N = sum(VARLEN_LENGTHS)
+    xv = randn(g, N, D, scale=0.5)
+    av = torch.softmax(randn(g, N, K), -1)
+    dyv = randn(g, N, D, scale=0.1)
+    return g, x, alpha, dy, xv, av, dyv
+
+
+def _cu(lengths, dtype=torch.int32):
+    return torch.tensor([0, *itertools.accumulate(lengths)], dtype=dtype)
+
+
+def _run_fixed(x, a, b, dy, dtype, a_dt, b_dt, act):
+    kx = x.to(DEV, dtype).requires_grad_()
+    ka = a.to(DEV, a_dt).requires_grad_()
+    kb = b.to(DEV, b_dt).requires_grad_()
+    y, st = moc_triton(kx, ka, kb, activation=act)
+    assert st is None and y.dtype == dtype
+    y.backward(dy.to(DEV, dtype))
+    rx, ra, rb = O.reference_inputs(kx, ka, kb, dtype)
+    ry, rdx, rda, rdb = O.moc_grads_ref(rx, ra, rb, dy.to(dtype).float(), act)
+    assert_close("y", y, ry, dtype)
+    assert_close("dx", kx.grad, rdx, dtype)
+    assert_close("dalpha", ka.grad, rda, dtype)
+    assert_close("dbasis", kb.grad, rdb, dtype)
+    assert kx.grad.dtype == dtype and ka.grad.dtype == a_dt and kb.grad.dtype == b_dt
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S", [2, 4])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_fixed(dtype, S, act):
+    g, x, a, dy, *_ = _verify_inputs()
+    b = randn(g, K, S, D, scale=0.1)
+    _run_fixed(x, a, b, dy, dtype, dtype, dtype, act)
+
+
+@pytest.mark.parametrize("dtype,a_dt,b_dt", [
+    (torch.bfloat16, torch.float32, torch.float16),
+    (torch.float32, torch.bfloat16, torch.float16),
+    (torch.bfloat16, torch.float64, torch.float32),
+])
+def test_mixed_storage_dtypes(dtype, a_dt, b_dt):
+    g, x, a, dy, *_ = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1)
+    _run_fixed(x, a, b, dy, dtype, a_dt, b_dt, None)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S", [2, 4])
+@pytest.mark.parametrize("act", [None, "silu"])
+@pytest.mark.parametrize("cu_dt", [torch.int32, torch.int64])
+def test_varlen(dtype, S, act, cu_dt):
+    g, _, _, _, xv, av, dyv = _verify_inputs()
+    b = randn(g, K, S, D, scale=0.1)
+    cu = _cu(VARLEN_LENGTHS, cu_dt).to(DEV)
+    kx = xv.to(DEV, dtype).requires_grad_()
+    ka = av.to(DEV, dtype).requires_grad_()
+    kb = b.to(DEV, dtype).requires_grad_()
+    y, st = moc_triton(kx, ka, kb, cu_seqlens=cu, max_seqlen=max(VARLEN_LENGTHS), activation=act)
+    assert st is None
+    y.backward(dyv.to(DEV, dtype))
+    rx, ra, rb = O.reference_inputs(kx, ka, kb, dtype)
+    ry, rdx, rda, rdb = O.moc_varlen_grads_ref(rx, ra, rb, cu.cpu(), dyv.to(dtype).float(), act)
+    assert_close("y", y, ry, dtype)
+    assert_close("dx", kx.grad, rdx, dtype)
+    assert_close("dalpha", ka.grad, rda, dtype)
+    assert_close("dbasis", kb.grad, rdb, dtype)
+    y3, _ = moc_triton(kx.detach()[None], ka.detach()[None], kb.detach(), cu_seqlens=cu,
+                       max_seqlen=max(VARLEN_LENGTHS), activation=act)
+    assert y3.shape == (1, *y.shape)
+    assert torch.equal(y3[0], y.detach())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S", [2, 4])
+@pytest.mark.parametrize("act", [None, "silu"])
+def test_step(dtype, S, act):
+    g, x, a, *_ = _verify_inputs()
+    b = randn(g, K, S, D, scale=0.1)
+    kx = x[:, :STEP_T].to(DEV, dtype)
+    ka = a[:, :STEP_T].to(DEV, dtype)
+    kb = b.to(DEV, dtype)
+    ref = O.moc_ref(kx.float().cpu(), ka.float().cpu(), kb.float().cpu(), act)
+    cache = torch.zeros(B, D, S, device=DEV, dtype=dtype)
+    outs = []
+    for t in range(STEP_T):
+        y, cache2 = moc_triton(kx[:, t:t + 1], ka[:, t:t + 1], kb, cache=cache,
+                               output_final_state=True, activation=act)
+        assert cache2 is cache            # the same object, mutated in place
+        outs.append(y)
+    assert_close("step y", torch.cat(outs, 1), ref, dtype)
+    assert torch.equal(cache, kx[:, -S:].transpose(1, 2))
+
+
+def test_step_with_strided_cache_and_no_final_state():
+    g, x, a, *_ = _verify_inputs()
+    S = 4
+    b = randn(g, K, S, D, scale=0.1).to(DEV, torch.bfloat16)
+    store = torch.zeros(B, S, D, device=DEV, dtype=torch.bfloat16)
+    cache = store.transpose(1, 2)        # [B, D, S] view with non-unit slot stride
+    kx = x[:, :6].to(DEV, torch.bfloat16)
+    ka = a[:, :6].to(DEV, torch.bfloat16)
+    for t in range(6):
+        y, st = moc_triton(kx[:, t:t + 1], ka[:, t:t + 1], b, cache=cache)
+        assert st is None
+    assert torch.equal(cache, kx[:, -S:].transpose(1, 2))
+
+
+@pytest.mark.parametrize("route", ["softmax", "exp"])
+@pytest.mark.parametrize("act", [None, "silu"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_module_routed_fwd_bwd(route, act, dtype):
+    torch.manual_seed(0)
+    Z = 48
+    m = MoC(dim=D, z_dim=Z, kernel_size=4, k=K, activation=act, init_std=0.1,
+            router_activation=route)
+    g = gen(3)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.2))
+    m = m.to(DEV, dtype)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, dtype).requires_grad_()
+    z = randn(g, B, T, Z).to(DEV, dtype).requires_grad_()
+    dy = randn(g, B, T, D, scale=0.1).to(DEV, dtype)
+    y, _ = m(x, z)
+    y.backward(dy)
+
+    rx = x.detach().float().cpu().requires_grad_()
+    rz = z.detach().float().cpu().requires_grad_()
+    rr = m.router.detach().float().cpu().requires_grad_()
+    rb = m.conv_bases.detach().float().cpu().requires_grad_()
+    # the router activation output has the logits' dtype (torch semantics)
+    logits = torch.nn.functional.linear(rz, rr)
+    alpha = O.route(logits, route)
+    alpha = alpha + (alpha.detach().to(dtype).float() - alpha.detach())  # round, keep grad
+    ry = O.moc_ref(rx, alpha, rb, act)
+    ry.backward(dy.float().cpu())
+    assert_close("y", y, ry, dtype)
+    assert_close("dx", x.grad, rx.grad, dtype)
+    assert_close("dz", z.grad, rz.grad, dtype)
+    assert_close("drouter", m.router.grad, rr.grad, dtype)
+    assert_close("dbasis", m.conv_bases.grad, rb.grad, dtype)
+
+
+@pytest.mark.parametrize("T1,T2", [(10, 7), (2, 9), (3, 2)])
+def test_prefill_from_cache_and_final_state(T1, T2):
+    dtype, S, act = torch.bfloat16, 4, "silu"
+    g, x, a, dy, *_ = _verify_inputs()
+    b = randn(g, K, S, D, scale=0.1).to(DEV, dtype)
+    kx = x[:, :T1 + T2].to(DEV, dtype)
+    ka = a[:, :T1 + T2].to(DEV, dtype)
+    y1, st1 = moc_triton(kx[:, :T1], ka[:, :T1], b, output_final_state=True, activation=act)
+    assert torch.equal(st1, O.final_state(kx[:, :T1], None, S))
+    x2 = kx[:, T1:].clone().requires_grad_()
+    y2, st2 = moc_triton(x2, ka[:, T1:], b, cache=st1, output_final_state=True, activation=act)
+    assert torch.equal(st2, O.final_state(kx, None, S))
+    ref = O.moc_ref(kx.float().cpu(), ka.float().cpu(), b.float().cpu(), act)
+    assert_close("prefill y", y2, ref[:, T1:], dtype)
+    assert_close("first y", y1, ref[:, :T1], dtype)
+    y2.sum().backward()
+    assert x2.grad is not None and torch.isfinite(x2.grad.float()).all()
+
+
+def test_need_x_false_and_alpha_only_grads():
+    g, x, a, dy, *_ = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1)
+    kx = x.to(DEV, torch.float32)
+    ka = a.to(DEV).requires_grad_()
+    kb = b.to(DEV).requires_grad_()
+    y, _ = moc_triton(kx, ka, kb, activation="silu")
+    y.backward(dy.to(DEV))
+    rx, ra, rb = O.reference_inputs(kx, ka, kb, torch.float32)
+    _, _, rda, rdb = O.moc_grads_ref(rx, ra, rb, dy, "silu")
+    assert_close("dalpha", ka.grad, rda, torch.float32)
+    assert_close("dbasis", kb.grad, rdb, torch.float32)
+
+
+@pytest.mark.parametrize("Dd,Kk,S,Tt", [
+    (67, 5, 3, 11), (16, 1, 1, 5), (130, 17, 5, 9), (96, 33, 8, 20), (40, 16, 4, 3),
+    (200, 32, 8, 37), (64, 12, 6, 2),
+])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_odd_shapes(Dd, Kk, S, Tt, dtype):
+    g = gen(Dd * 31 + Kk)
+    x = randn(g, 3, Tt, Dd, scale=0.5)
+    a = torch.softmax(randn(g, 3, Tt, Kk), -1)
+    b = randn(g, Kk, S, Dd, scale=0.2)
+    dy = randn(g, 3, Tt, Dd, scale=0.1)
+    _run_fixed(x, a, b, dy, dtype, dtype, dtype, "silu")
+
+
+def test_varlen_short_sequences_and_empty_ones():
+    # lengths below S, length-1 and zero-length sequences
+    lengths = [1, 0, 2, 3, 0, 9, 1]
+    dtype = torch.float32
+    g = gen(5)
+    N = sum(lengths)
+    xv = randn(g, N, D)
+    av = torch.softmax(randn(g, N, K), -1)
+    b = randn(g, K, 4, D, scale=0.2)
+    dyv = randn(g, N, D)
+    cu = _cu(lengths).to(DEV)
+    kx = xv.to(DEV).requires_grad_()
+    ka = av.to(DEV).requires_grad_()
+    kb = b.to(DEV).requires_grad_()
+    y, _ = moc_triton(kx, ka, kb, cu_seqlens=cu, max_seqlen=9, activation="silu")
+    y.backward(dyv.to(DEV))
+    ry, rdx, rda, rdb = O.moc_varlen_grads_ref(xv, av, b, cu.cpu(), dyv, "silu")
+    assert_close("y", y, ry, dtype)
+    assert_close("dx", kx.grad, rdx, dtype)
+    assert_close("dalpha", ka.grad, rda, dtype)
+    assert_close("dbasis", kb.grad, rdb, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_varlen_isolation_is_bitwise(dtype):
+    """Perturbing other sequences leaves y, dx and dalpha of a probed sequence
+    bitwise unchanged."""
+    g, _, _, _, xv, av, dyv = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1).to(DEV, dtype)
+    cu = _cu(VARLEN_LENGTHS).to(DEV)
+    lo, hi = 31, 48  # sequence 1
+
+    def run(xs, as_, dys):
+        kx = xs.to(DEV, dtype).requires_grad_()
+        ka = as_.to(DEV, dtype).requires_grad_()
+        y, _ = moc_triton(kx, ka, b, cu_seqlens=cu, max_seqlen=31, activation="silu")
+        y.backward(dys.to(DEV, dtype))
+        return y.detach()[lo:hi], kx.grad[lo:hi], ka.grad[lo:hi]
+
+    base = run(xv, av, dyv)
+    x2, a2, d2 = xv.clone(), av.clone(), dyv.clone()
+    for sl in (slice(0, lo), slice(hi, None)):
+        x2[sl] = x2[sl] * 3 + 1
+        a2[sl] = a2[sl].flip(-1)
+        d2[sl] = -d2[sl]
+    pert = run(x2, a2, d2)
+    for u, v in zip(base, pert):
+        assert torch.equal(u, v)
+
+
+def test_determinism_bitwise():
+    g, x, a, dy, *_ = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1)
+    grads = []
+    for _ in range(3):
+        kx = x.to(DEV, torch.bfloat16).requires_grad_()
+        ka = a.to(DEV, torch.bfloat16).requires_grad_()
+        kb = b.to(DEV, torch.bfloat16).requires_grad_()
+        y, _ = moc_triton(kx, ka, kb, activation="silu")
+        y.backward(dy.to(DEV, torch.bfloat16))
+        grads.append((y.detach(), kx.grad, ka.grad, kb.grad))
+    for other in grads[1:]:
+        for u, v in zip(grads[0], other):
+            assert torch.equal(u, v)
+
+
+def test_module_decode_matches_full_forward():
+    """Config-4 pattern at reduced size: prefill through forward(output_final_state),
+    then single-token steps; y within tolerance of the full forward, cache
+    bit-exact."""
+    torch.manual_seed(0)
+    Bd, Dd, Z, Kd, S, Tp, Ts = 8, 256, 64, 16, 4, 40, 24
+    m = MoC(Dd, Z, S, Kd, activation="silu")
+    g = gen(9)
+    with torch.no_grad():
+        m.router.copy_(randn(g, Kd, Z, scale=0.02))
+    m = m.to(DEV, torch.bfloat16)
+    x = randn(g, Bd, Tp + Ts, Dd).to(DEV, torch.bfloat16)
+    z = randn(g, Bd, Tp + Ts, Z).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        y_pre, cache = m(x[:, :Tp], z[:, :Tp], output_final_state=True)
+        steps = []
+        for t in range(Tp, Tp + Ts):
+            y, c2 = m.step(x[:, t:t + 1], z[:, t:t + 1], cache=cache, output_final_state=True)
+            assert c2 is cache
+            steps.append(y)
+        y_full, _ = m(x, z)
+    assert torch.equal(cache, x[:, -S:].transpose(1, 2))
+    assert_close("decode y", torch.cat(steps, 1), y_full[:, Tp:], torch.bfloat16)
+    assert_close("prefill y", y_pre, y_full[:, :Tp], torch.bfloat16)
+    with torch.no_grad():
+        y0, c0 = m.step(x[:, :1], z[:, :1])   # cache=None: zeros are created
+    assert c0 is None
+    assert_close("first step", y0, y_full[:, :1], torch.bfloat16)
+
+
+def test_module_varlen_routed():
+    torch.manual_seed(0)
+    Z = 32
+    m = MoC(D, Z, 4, K, router_activation="exp", init_std=0.1)
+    g = gen(11)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.1))
+    m = m.to(DEV)
+    cu = _cu(VARLEN_LENGTHS).to(DEV)
+    N = sum(VARLEN_LENGTHS)
+    x = randn(g, N, D).to(DEV).requires_grad_()
+    z = randn(g, N, Z).to(DEV).requires_grad_()
+    y, st = m(x, z, cu_seqlens=cu, max_seqlen=31)
+    assert st is None
+    y.sum().backward()
+    rx = x.detach().cpu().requires_grad_()
+    rz = z.detach().cpu().requires_grad_()
+    rr = m.router.detach().cpu().requires_grad_()
+    ry = O.moc_varlen_ref(rx, O.route(torch.nn.functional.linear(rz, rr), "exp"),
+                          m.conv_bases.detach().cpu(), cu.cpu())
+    ry.sum().backward()
+    assert_close("y", y, ry, torch.float32)
+    assert_close("dx", x.grad, rx.grad, torch.float32)
+    assert_close("dz", z.grad, rz.grad, torch.float32)
+    assert_close("drouter", m.router.grad, rr.grad, torch.float32)
+
+
+def test_moc_triton_name_is_hip_path():
+    assert moc.moc_triton is moc.moc_hip
