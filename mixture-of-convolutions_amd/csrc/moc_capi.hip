@@ -29,6 +29,8 @@ size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 // Largest extents the launch grids are sized for.
 constexpr int64_t kMaxTokens = int64_t(1) << 31;
 constexpr int64_t kMaxBatch = 65535;
+constexpr int64_t kMaxK = 4096;   // dynamic LDS of the reduction kernels holds K floats
+constexpr int64_t kMaxS = 1024;
 
 int check_dims(int64_t n_tokens, int64_t dim, int64_t k, int64_t ks) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || ks <= 0)
@@ -36,6 +38,9 @@ int check_dims(int64_t n_tokens, int64_t dim, int64_t k, int64_t ks) {
                              "(got %lld, %lld, %lld, %lld)",
                 (long long)n_tokens, (long long)dim, (long long)k, (long long)ks);
   if (n_tokens >= kMaxTokens) return fail(MOC_ERR_ARG, "n_tokens too large: %lld", (long long)n_tokens);
+  if (k > kMaxK) return fail(MOC_ERR_ARG, "k too large: %lld (max %lld)", (long long)k, (long long)kMaxK);
+  if (ks > kMaxS)
+    return fail(MOC_ERR_ARG, "kernel_size too large: %lld (max %lld)", (long long)ks, (long long)kMaxS);
   return MOC_OK;
 }
 
