@@ -18,6 +18,10 @@ TOL = {
 
 
 def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype) -> None:
+    """Check ``got`` against the fp32 oracle result ``ref``.  ``dtype`` is the
+    compute (x) dtype; a result stored in a 16-bit dtype is held to the bf16 rule."""
+    if got.dtype in (torch.bfloat16, torch.float16):
+        dtype = torch.bfloat16
     got = got.detach().float().cpu()
     ref = ref.detach().float().cpu()
     assert got.shape == ref.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
@@ -33,6 +37,11 @@ def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.d
             f"{name} ({dtype}): {int(bad.sum())}/{err.numel()} elements out of tolerance; "
             f"worst at flat {i}: got {got.flatten()[i].item():.6g} ref {ref.flatten()[i].item():.6g} "
             f"(max abs err {err.max().item():.3g}, rms(ref) {rms:.3g})")
+
+
+def round_like(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """t rounded to ``dtype`` in value, with the gradient of the identity."""
+    return t + (t.detach().to(dtype).to(t.dtype) - t.detach())
 
 
 def gen(seed: int = 0) -> torch.Generator:

@@ -18,7 +18,7 @@ import torch
 import moc
 from moc import MoC, moc_triton
 from oracle import moc_oracle as O
-from tests._parity import assert_close, gen, randn
+from tests._parity import assert_close, gen, randn, round_like
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -163,10 +163,10 @@ def test_module_routed_fwd_bwd(route, act, dtype):
     rz = z.detach().float().cpu().requires_grad_()
     rr = m.router.detach().float().cpu().requires_grad_()
     rb = m.conv_bases.detach().float().cpu().requires_grad_()
-    # the router activation output has the logits' dtype (torch semantics)
-    logits = torch.nn.functional.linear(rz, rr)
-    alpha = O.route(logits, route)
-    alpha = alpha + (alpha.detach().to(dtype).float() - alpha.detach())  # round, keep grad
+    # torch's GPU router GEMM returns logits in the module dtype, and the router
+    # activation output has the logits' dtype: round both, keep the gradients
+    logits = round_like(torch.nn.functional.linear(rz, rr), dtype)
+    alpha = round_like(O.route(logits, route), dtype)
     ry = O.moc_ref(rx, alpha, rb, act)
     ry.backward(dy.float().cpu())
     assert_close("y", y, ry, dtype)
