@@ -51,9 +51,11 @@ __device__ __forceinline__ float sigmoid_f(float p) {
 // Sequence layout of the flat token axis [0, n_tokens).
 //   fixed : sequences of seq_len tokens back to back ([B,T,D] viewed as [B*T,D])
 //   packed: token n of sequence j lies in [cu[j], cu[j+1]).
-// bounds() returns [lo, hi) of the sequence holding token t, clamped to
-// [0, n_tokens] and always containing t, so every access derived from it stays
-// inside the token axis whatever cu_seqlens holds.
+// The packed axis is cut into the segments [0, cu[0]), [cu[0], cu[1]), ...,
+// [cu[n], n_tokens); tokens outside every sequence therefore form segments of
+// their own.  bounds() returns [lo, hi) of the segment holding token t,
+// clamped to [0, n_tokens] and always containing t, so every access derived
+// from it stays inside the token axis whatever cu_seqlens holds.
 struct SeqLayout {
   const void* cu;
   int cu64;
@@ -73,19 +75,20 @@ struct SeqLayout {
       if (hi > n_tokens) hi = n_tokens;
       return;
     }
-    // largest j in [0, n_seqs] with cu[j] <= t
-    int64_t a = 0, b = n_seqs;  // invariant: answer in [a, b] or -1
-    if (cu_at(0) > t) {
-      lo = t;
-      hi = t + 1;
-      return;
+    const int64_t c0 = cu_at(0);
+    if (t < c0) {
+      lo = 0;
+      hi = c0;
+    } else {
+      // largest a in [0, n_seqs] with cu[a] <= t
+      int64_t a = 0, b = n_seqs;
+      while (a < b) {
+        const int64_t m = (a + b + 1) >> 1;
+        if (cu_at(m) <= t) a = m; else b = m - 1;
+      }
+      lo = cu_at(a);
+      hi = (a < n_seqs) ? cu_at(a + 1) : n_tokens;
     }
-    while (a < b) {
-      const int64_t m = (a + b + 1) >> 1;
-      if (cu_at(m) <= t) a = m; else b = m - 1;
-    }
-    lo = cu_at(a);
-    hi = (a < n_seqs) ? cu_at(a + 1) : t + 1;
     if (lo < 0) lo = 0;
     if (lo > t) lo = t;
     if (hi > n_tokens) hi = n_tokens;
