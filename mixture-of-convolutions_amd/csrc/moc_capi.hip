@@ -4,6 +4,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/moc_hip.h"
@@ -105,6 +106,23 @@ int check_seq(const void* cu, int64_t n_seqs, int64_t seq_len) {
   return MOC_OK;
 }
 
+// Kernel family for a problem: the MFMA kernels where they are instantiated,
+// the generic kernels otherwise.  MOC_HIP_PATH=generic forces the generic
+// kernels (used to cross-check the two families).
+bool use_mfma(const moc::Problem& p) {
+  const char* env = std::getenv("MOC_HIP_PATH");
+  if (env != nullptr && std::strcmp(env, "generic") == 0) return false;
+  return moc::mfma::supported(p);
+}
+
+size_t forward_bytes(const moc::Problem& p) {
+  return use_mfma(p) ? moc::mfma::forward_workspace(p) : fwd_bytes(p.n_tokens, p.D, p.K, p.S);
+}
+
+size_t backward_bytes(const moc::Problem& p) {
+  return use_mfma(p) ? moc::mfma::backward_workspace(p) : bwd_bytes(p);
+}
+
 int hip_status(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(MOC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
@@ -121,10 +139,10 @@ const char* moc_last_error(void) { return g_err; }
 
 size_t moc_forward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                    int64_t kernel_size, int x_dtype, int routing) {
-  (void)x_dtype;
-  (void)routing;
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
-  return fwd_bytes(n_tokens, dim, k, kernel_size);
+  moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
+                                MOC_DT_F32, MOC_DT_F32, 0, routing);
+  return forward_bytes(p);
 }
 
 int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
@@ -138,14 +156,18 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
   if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
   if ((rc = check_seq(cu_seqlens, n_seqs, seq_len)) != MOC_OK) return rc;
   if (!x || !alpha || !basis || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
-  const size_t need = fwd_bytes(n_tokens, dim, k, kernel_size);
-  if (workspace_bytes < need || (need && !workspace))
-    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
-                workspace_bytes);
   moc::Problem p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k,
                                 kernel_size, x_dtype, alpha_dtype, basis_dtype, activation,
                                 routing);
+  const size_t need = forward_bytes(p);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(p)) {
+    moc::mfma::forward(p, x, alpha, basis, y, workspace, st);
+    return hip_status("moc_forward launch");
+  }
   Carve cv{static_cast<char*>(workspace), 0};
   float* a_r = cv.take<float>(size_t(n_tokens * k));
   float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
@@ -159,7 +181,7 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, routing);
-  return bwd_bytes(p);
+  return backward_bytes(p);
 }
 
 int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy, void* dx,
@@ -180,11 +202,15 @@ int moc_backward(const void* x, const void* alpha, const void* basis, const void
   moc::Problem p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k,
                                 kernel_size, x_dtype, alpha_dtype, basis_dtype, activation,
                                 routing);
-  const size_t need = bwd_bytes(p);
+  const size_t need = backward_bytes(p);
   if (workspace_bytes < need || !workspace)
     return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
                 workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (use_mfma(p)) {
+    moc::mfma::backward(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
+    return hip_status("moc_backward launch");
+  }
   Carve cv{static_cast<char*>(workspace), 0};
   float* a_r = cv.take<float>(size_t(n_tokens * k));
   float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));

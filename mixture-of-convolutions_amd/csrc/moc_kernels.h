@@ -32,4 +32,16 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st);
 
+// MFMA path (moc_mfma_common.hip): S in {2, 3, 4, 8}, K <= 32, D % 4 == 0
+namespace mfma {
+bool supported(const Problem& p);
+size_t forward_workspace(const Problem& p);
+size_t backward_workspace(const Problem& p);
+void forward(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,
+             void* workspace, hipStream_t st);
+void backward(const Problem& p, const void* x, const void* alpha, const void* basis,
+              const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+              hipStream_t st);
+}  // namespace mfma
+
 }  // namespace moc

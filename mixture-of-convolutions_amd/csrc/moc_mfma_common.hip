@@ -1,0 +1,230 @@
+// MFMA path: operand preparation, backward stage 2, workspace plans, dispatch.
+#include "moc_mfma_launch.h"
+
+namespace moc {
+namespace mfma {
+
+// ---------------------------------------------------------------------------
+// Operand preparation (one launch):
+//   blocks [0, a_blocks): one lane per token; a_c[t, k] = alpha in the compute
+//     dtype, K padded to KP with zeros; with routing, alpha = softmax / exp of
+//     the logits rounded to the logits' dtype (what torch's router activation
+//     returns), and a_r[t, k] keeps that value in fp32 for the backward's
+//     activation gradient;
+//   other blocks: b_c[k, s, d] = basis in the compute dtype, rows k >= K zero.
+template <bool BF>
+__global__ void __launch_bounds__(256)
+prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* __restrict__ basis,
+            int b_dt, int64_t N, int K, int KP, int S, int64_t D,
+            typename CT<BF>::elem* __restrict__ a_c, float* __restrict__ a_r,
+            typename CT<BF>::elem* __restrict__ b_c, int64_t a_blocks) {
+  using C = CT<BF>;
+  using E = typename C::elem;
+  if (static_cast<int64_t>(blockIdx.x) < a_blocks) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= N) return;
+    const int64_t base = t * K;
+    float m = -INFINITY, inv = 1.f;
+    if (routing == ROUTE_SOFTMAX) {
+      for (int k = 0; k < K; ++k) m = fmaxf(m, load_any(alpha, a_dt, base + k));
+      float sum = 0.f;
+      for (int k = 0; k < K; ++k) sum += __expf(load_any(alpha, a_dt, base + k) - m);
+      inv = 1.0f / sum;
+    }
+    for (int k = 0; k < KP; ++k) {
+      float v = 0.f;
+      if (k < K) {
+        const float l = load_any(alpha, a_dt, base + k);
+        if (routing == ROUTE_SOFTMAX) v = round_to(__expf(l - m) * inv, a_dt);
+        else if (routing == ROUTE_EXP) v = round_to(__expf(l), a_dt);
+        else v = l;
+        if (routing != ROUTE_ALPHA) a_r[base + k] = v;
+      }
+      a_c[t * KP + k] = C::from_f(v);
+    }
+  } else {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) - a_blocks) * 256 + threadIdx.x;
+    const int64_t sd = static_cast<int64_t>(S) * D;
+    if (i >= KP * sd) return;
+    const int64_t k = i / sd;
+    b_c[i] = (k < K) ? C::from_f(load_any(basis, b_dt, i)) : E(0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward stage 2 (one launch):
+//   blocks [0, da_blocks): one lane per token; dalpha = sum of the n_da channel
+//     partials in order, then the router activation gradient
+//     (softmax: a (da - <a, da>), exp: a da), stored in the alpha dtype;
+//   other blocks: one lane per basis element; dbasis = sum of the n_db token
+//     partials in order, stored in the basis dtype.
+template <int KC>
+__global__ void __launch_bounds__(256)
+stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __restrict__ part_db,
+              int64_t n_db, const float* __restrict__ a_r, void* __restrict__ dalpha, int a_dt,
+              int routing, void* __restrict__ dbasis, int b_dt, int64_t N, int K, int S,
+              int64_t D, int64_t da_blocks) {
+  constexpr int KP = 16 * KC;
+  if (static_cast<int64_t>(blockIdx.x) < da_blocks) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (t >= N) return;
+    float da[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) da[k] = 0.f;
+    for (int64_t p = 0; p < n_da; ++p) {
+      const float4* src = reinterpret_cast<const float4*>(part_da + (p * N + t) * KP);
+#pragma unroll
+      for (int i = 0; i < KP / 4; ++i) {
+        const float4 v = src[i];
+        da[4 * i + 0] += v.x;
+        da[4 * i + 1] += v.y;
+        da[4 * i + 2] += v.z;
+        da[4 * i + 3] += v.w;
+      }
+    }
+    float dot = 0.f;
+    if (routing == ROUTE_SOFTMAX) {
+#pragma unroll
+      for (int k = 0; k < KP; ++k)
+        if (k < K) dot = fmaf(a_r[t * K + k], da[k], dot);
+    }
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+      if (k < K) {
+        float v = da[k];
+        if (routing == ROUTE_SOFTMAX) v = a_r[t * K + k] * (v - dot);
+        else if (routing == ROUTE_EXP) v = a_r[t * K + k] * v;
+        store_any(dalpha, a_dt, t * K + k, v);
+      }
+    }
+  } else {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x;
+    const int64_t sd = static_cast<int64_t>(S) * D;
+    if (i >= static_cast<int64_t>(K) * sd) return;
+    const int64_t k = i / sd, rest = i - k * sd;
+    float acc = 0.f;
+    for (int64_t p = 0; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
+    store_any(dbasis, b_dt, i, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// workspace plans
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t al(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Plan {
+  int KP;
+  size_t esz;
+  size_t off_ac, off_bc, off_ar, off_pda, off_pdb, total;
+  Grid2 bg;
+};
+
+Plan plan(const Problem& p, bool backward) {
+  Plan pl{};
+  pl.KP = static_cast<int>(16 * ((p.K + 15) / 16));
+  pl.esz = (p.x_dt == DT_BF16) ? 2 : 4;
+  size_t off = 0;
+  pl.off_ac = off;
+  off += al(static_cast<size_t>(p.n_tokens) * pl.KP * pl.esz);
+  pl.off_bc = off;
+  off += al(static_cast<size_t>(pl.KP) * p.S * p.D * pl.esz);
+  pl.off_ar = off;
+  if (p.routing != ROUTE_ALPHA) off += al(static_cast<size_t>(p.n_tokens) * p.K * 4);
+  if (backward) {
+    pl.bg = bwd_grid(p.n_tokens, p.D, p.S);
+    pl.off_pda = off;
+    off += al(static_cast<size_t>(pl.bg.gx) * p.n_tokens * pl.KP * 4);
+    pl.off_pdb = off;
+    off += al(static_cast<size_t>(pl.bg.gy) * pl.KP * p.S * p.D * 4);
+  }
+  pl.total = off;
+  return pl;
+}
+
+void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
+                 hipStream_t st) {
+  const int64_t a_blocks = cdiv(p.n_tokens, 256);
+  const int64_t b_blocks = cdiv(static_cast<int64_t>(pl.KP) * p.S * p.D, 256);
+  float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<float*>(ws + pl.off_ar) : nullptr;
+  const dim3 grid(static_cast<unsigned>(a_blocks + b_blocks));
+  if (p.x_dt == DT_BF16) {
+    hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(256), 0, st, alpha, p.a_dt, p.routing, basis,
+                       p.b_dt, p.n_tokens, static_cast<int>(p.K), pl.KP, static_cast<int>(p.S),
+                       p.D, reinterpret_cast<uint16_t*>(ws + pl.off_ac), a_r,
+                       reinterpret_cast<uint16_t*>(ws + pl.off_bc), a_blocks);
+  } else {
+    hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(256), 0, st, alpha, p.a_dt, p.routing, basis,
+                       p.b_dt, p.n_tokens, static_cast<int>(p.K), pl.KP, static_cast<int>(p.S),
+                       p.D, reinterpret_cast<float*>(ws + pl.off_ac), a_r,
+                       reinterpret_cast<float*>(ws + pl.off_bc), a_blocks);
+  }
+}
+
+}  // namespace
+
+bool supported(const Problem& p) {
+  const bool s_ok = p.S == 2 || p.S == 3 || p.S == 4 || p.S == 8;
+  return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 &&
+         (p.x_dt == DT_BF16 || p.x_dt == DT_F32);
+}
+
+size_t forward_workspace(const Problem& p) { return plan(p, false).total; }
+size_t backward_workspace(const Problem& p) { return plan(p, true).total; }
+
+void forward(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,
+             void* workspace, hipStream_t st) {
+  const Plan pl = plan(p, false);
+  char* ws = static_cast<char*>(workspace);
+  launch_prep(p, pl, alpha, basis, ws, st);
+  const void* a_c = ws + pl.off_ac;
+  const void* b_c = ws + pl.off_bc;
+  switch (p.S) {
+    case 2: launch_fwd<2>(p, x, a_c, b_c, y, st); break;
+    case 3: launch_fwd<3>(p, x, a_c, b_c, y, st); break;
+    case 4: launch_fwd<4>(p, x, a_c, b_c, y, st); break;
+    case 8: launch_fwd<8>(p, x, a_c, b_c, y, st); break;
+    default: break;
+  }
+}
+
+void backward(const Problem& p, const void* x, const void* alpha, const void* basis,
+              const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+              hipStream_t st) {
+  const Plan pl = plan(p, true);
+  char* ws = static_cast<char*>(workspace);
+  launch_prep(p, pl, alpha, basis, ws, st);
+  const void* a_c = ws + pl.off_ac;
+  const void* b_c = ws + pl.off_bc;
+  float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
+  float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
+  switch (p.S) {
+    case 2: launch_bwd<2>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 3: launch_bwd<3>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 4: launch_bwd<4>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    default: break;
+  }
+  const int64_t da_blocks = cdiv(p.n_tokens, 256);
+  const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
+  const float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<const float*>(ws + pl.off_ar)
+                                                : nullptr;
+  const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
+  if (pl.KP == 16) {
+    hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda,
+                       static_cast<int64_t>(pl.bg.gx), pdb, static_cast<int64_t>(pl.bg.gy), a_r,
+                       dalpha, p.a_dt, p.routing, dbasis, p.b_dt, p.n_tokens,
+                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
+  } else {
+    hipLaunchKernelGGL(stage2_kernel<2>, grid, dim3(256), 0, st, pda,
+                       static_cast<int64_t>(pl.bg.gx), pdb, static_cast<int64_t>(pl.bg.gy), a_r,
+                       dalpha, p.a_dt, p.routing, dbasis, p.b_dt, p.n_tokens,
+                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
+  }
+}
+
+}  // namespace mfma
+}  // namespace moc

@@ -1,0 +1,123 @@
+// Host-side launch of the MFMA kernels, templated on the kernel size S.  Each
+// moc_mfma_s<S>.hip instantiates launch_fwd<S> / launch_bwd<S>; the rest of the
+// library sees them through the extern declarations at the bottom.
+#pragma once
+
+#include "moc_kernels.h"
+#include "moc_mfma.h"
+
+namespace moc {
+namespace mfma {
+
+// Tile shapes (see moc_mfma.h): forward NB x NC blocks per wave, 4 waves per
+// workgroup; backward NB x NC per wave, kBwdWPG waves per workgroup.
+constexpr int kFwdNB = 2, kFwdNC = 4;
+constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
+// Resident workgroups the grids are sized for (256 CUs).
+constexpr int64_t kFwdTargetWG = 2048;
+constexpr int64_t kBwdTargetWG = 512;
+
+struct Grid2 {
+  unsigned gx, gy;
+  int n_sb;
+};
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline Grid2 fwd_grid(int64_t N, int64_t D) {
+  const int64_t gx = cdiv(D, 4 * 16 * kFwdNC);
+  const int64_t n_super = cdiv(N, 16 * kFwdNB);
+  int64_t gy_target = kFwdTargetWG / gx;
+  if (gy_target < 1) gy_target = 1;
+  const int64_t n_sb = cdiv(n_super, gy_target);
+  return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
+               static_cast<int>(n_sb)};
+}
+
+inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S) {
+  const int64_t gx = cdiv(D, kBwdWPG * 16 * kBwdNC);
+  const int64_t eown = 16 * kBwdNB - (S - 1);
+  const int64_t n_super = cdiv(N, eown);
+  int64_t gy_target = kBwdTargetWG / gx;
+  if (gy_target < 1) gy_target = 1;
+  const int64_t n_sb = cdiv(n_super, gy_target);
+  return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
+               static_cast<int>(n_sb)};
+}
+
+template <int S, int KC, bool ACT, bool BF>
+void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
+             hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const Grid2 g = fwd_grid(p.n_tokens, p.D);
+  hipLaunchKernelGGL((fwd_kernel<S, KC, kFwdNB, kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256), 0,
+                     st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq, p.D,
+                     g.n_sb);
+}
+
+template <int S, int KC, bool ACT, bool BF>
+void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
+             void* dx, float* part_da, float* part_db, hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
+  hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF>), dim3(g.gx, g.gy),
+                     dim3(64 * kBwdWPG), 0, st, x, dy, static_cast<const E*>(a_c),
+                     static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D, g.n_sb);
+}
+
+// Dispatch over (KC, activation, dtype) for one S.
+template <int S>
+void launch_fwd(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
+                hipStream_t st) {
+  const int kc = static_cast<int>((p.K + 15) / 16);
+  const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
+#define MOC_FWD(KC_)                                              \
+  if (kc == KC_) {                                                \
+    if (bf) {                                                     \
+      if (act) fwd_one<S, KC_, true, true>(p, x, a_c, b_c, y, st); \
+      else fwd_one<S, KC_, false, true>(p, x, a_c, b_c, y, st);   \
+    } else {                                                      \
+      if (act) fwd_one<S, KC_, true, false>(p, x, a_c, b_c, y, st); \
+      else fwd_one<S, KC_, false, false>(p, x, a_c, b_c, y, st);  \
+    }                                                             \
+    return;                                                       \
+  }
+  MOC_FWD(1)
+  MOC_FWD(2)
+#undef MOC_FWD
+}
+
+template <int S>
+void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
+                void* dx, float* part_da, float* part_db, hipStream_t st) {
+  const int kc = static_cast<int>((p.K + 15) / 16);
+  const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
+#define MOC_BWD(KC_)                                                                          \
+  if (kc == KC_) {                                                                            \
+    if (bf) {                                                                                 \
+      if (act) bwd_one<S, KC_, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);     \
+      else bwd_one<S, KC_, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);        \
+    } else {                                                                                  \
+      if (act) bwd_one<S, KC_, true, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);    \
+      else bwd_one<S, KC_, false, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);       \
+    }                                                                                         \
+    return;                                                                                   \
+  }
+  MOC_BWD(1)
+  MOC_BWD(2)
+#undef MOC_BWD
+}
+
+#define MOC_DECLARE_S(S_)                                                                     \
+  extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
+                                      void*, hipStream_t);                                    \
+  extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
+                                      const void*, void*, float*, float*, hipStream_t);
+MOC_DECLARE_S(2)
+MOC_DECLARE_S(3)
+MOC_DECLARE_S(4)
+MOC_DECLARE_S(8)
+#undef MOC_DECLARE_S
+
+}  // namespace mfma
+}  // namespace moc

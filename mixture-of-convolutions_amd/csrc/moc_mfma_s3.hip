@@ -1,0 +1,13 @@
+// MFMA forward / backward kernels instantiated for kernel size S = 3.
+#include "moc_mfma_launch.h"
+
+namespace moc {
+namespace mfma {
+
+template void launch_fwd<3>(const Problem&, const void*, const void*, const void*, void*,
+                             hipStream_t);
+template void launch_bwd<3>(const Problem&, const void*, const void*, const void*, const void*,
+                             void*, float*, float*, hipStream_t);
+
+}  // namespace mfma
+}  // namespace moc

@@ -1,0 +1,206 @@
+"""GPU parity at the BASELINE.json configurations.
+
+At these sizes the oracle (oracle/moc_oracle.py, plain torch) runs in fp32 on
+the GPU itself; it is the same restatement the CPU tests pin.  Every HIP result
+is also compared with the other kernel family (MFMA vs generic VALU kernels,
+selected with MOC_HIP_PATH), and the decode loop is checked against the full
+forward with the cache compared bit for bit.  Tolerances: tests/_parity.py.
+"""
+from __future__ import annotations
+
+import itertools
+import os
+
+import pytest
+import torch
+
+import moc
+from moc import MoC, moc_triton
+from oracle import moc_oracle as O
+from tests._parity import assert_close, gen, randn, round_like
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _layer(D, Z, K, S, act, route, init_std, dtype, seed=0):
+    torch.manual_seed(seed)
+    m = MoC(D, Z, S, K, activation=act, init_std=init_std, router_activation=route)
+    g = gen(seed + 1)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.02))
+    return m.to(DEV, dtype), g
+
+
+def _oracle_layer(m, x, z, dy, route, act, cu=None):
+    """fp32 oracle on the GPU for the layer: returns y and grads (x, z, router, basis)."""
+    dtype = x.dtype
+    rx = x.detach().float().requires_grad_()
+    rz = z.detach().float().requires_grad_()
+    rr = m.router.detach().float().requires_grad_()
+    rb = m.conv_bases.detach().float().requires_grad_()
+    logits = round_like(torch.nn.functional.linear(rz, rr), dtype)
+    alpha = round_like(O.route(logits, route), dtype)
+    if cu is None:
+        y = O.moc_ref(rx, alpha, rb, act)
+    else:
+        y = O.moc_varlen_ref(rx, alpha, rb, cu, act)
+    y.backward(dy.float())
+    return y.detach(), rx.grad, rz.grad, rr.grad, rb.grad
+
+
+def _hip_layer(m, x, z, dy, **kw):
+    m.zero_grad(set_to_none=True)
+    x = x.detach().requires_grad_()
+    z = z.detach().requires_grad_()
+    y, _ = m(x, z, **kw)
+    y.backward(dy)
+    return y.detach(), x.grad, z.grad, m.router.grad.clone(), m.conv_bases.grad.clone()
+
+
+def _with_path(path, fn):
+    old = os.environ.get("MOC_HIP_PATH")
+    os.environ["MOC_HIP_PATH"] = path
+    try:
+        return fn()
+    finally:
+        if old is None:
+            del os.environ["MOC_HIP_PATH"]
+        else:
+            os.environ["MOC_HIP_PATH"] = old
+
+
+NAMES = ("y", "dx", "dz", "drouter", "dbasis")
+
+
+def test_config1_cpu_reference_shape_fp32():
+    """B2 T512 D256 Z256 K4 S4 fp32, softmax, no SiLU (oracle on CPU)."""
+    m, g = _layer(256, 256, 4, 4, None, "softmax", None, torch.float32)
+    with torch.no_grad():
+        m.conv_bases.copy_(randn(g, 4, 4, 256, scale=0.002))
+    x = randn(g, 2, 512, 256).to(DEV)
+    z = randn(g, 2, 512, 256).to(DEV)
+    dy = randn(g, 2, 512, 256).to(DEV)
+    got = _hip_layer(m, x, z, dy)
+    m_cpu = MoC(256, 256, 4, 4)
+    m_cpu.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()})
+    ref = _oracle_layer(m_cpu, x.cpu(), z.cpu(), dy.cpu(), "softmax", None)
+    for n, a, b in zip(NAMES, got, ref):
+        assert_close(n, a, b, torch.float32)
+
+
+def test_config2_headline_layer():
+    """B4 T4096 D2048 Z2048 K16 S4 bf16, softmax, SiLU, loss = y.sum()."""
+    m, g = _layer(2048, 2048, 16, 4, "silu", "softmax", 0.002, torch.bfloat16)
+    x = randn(g, 4, 4096, 2048).to(DEV, torch.bfloat16)
+    z = randn(g, 4, 4096, 2048).to(DEV, torch.bfloat16)
+    dy = torch.ones_like(x)
+    got = _hip_layer(m, x, z, dy)
+    ref = _oracle_layer(m, x, z, dy, "softmax", "silu")
+    for n, a, b in zip(NAMES, got, ref):
+        assert_close(n, a, b, torch.bfloat16)
+    other = _with_path("generic", lambda: _hip_layer(m, x, z, dy))
+    for n, a, b in zip(NAMES, got, other):
+        assert_close(n + " (mfma vs generic)", a, b, torch.bfloat16)
+
+
+def _varlen_lengths(total, lo, hi, seed=0):
+    g = gen(seed)
+    lengths = []
+    while sum(lengths) < total:
+        lengths.append(int(torch.randint(lo, hi + 1, (1,), generator=g)))
+    lengths[-1] -= sum(lengths) - total
+    return [n for n in lengths if n > 0]
+
+
+def test_config3_varlen_layer():
+    """32768 packed tokens, lengths U[16, 4096], D4096 Z2048 K16 S4 bf16, exp."""
+    lengths = _varlen_lengths(32768, 16, 4096)
+    cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int32, device=DEV)
+    m, g = _layer(4096, 2048, 16, 4, None, "exp", 0.002, torch.bfloat16)
+    x = randn(g, 32768, 4096).to(DEV, torch.bfloat16)
+    z = randn(g, 32768, 2048).to(DEV, torch.bfloat16)
+    dy = randn(g, 32768, 4096).to(DEV, torch.bfloat16)
+    kw = dict(cu_seqlens=cu, max_seqlen=max(lengths))
+    got = _hip_layer(m, x, z, dy, **kw)
+    ref = _oracle_layer(m, x, z, dy, "exp", None, cu=cu.cpu())
+    for n, a, b in zip(NAMES, got, ref):
+        assert_close(n, a, b, torch.bfloat16)
+
+
+def test_config5_qkv_triple():
+    """q/k/v MoC layers routed by one x_norm, K32 S8, fan-in init,
+    exp for q/k and softmax for v; loss = sum of the three outputs."""
+    B, T, Dm = 2, 2048, 4096  # T reduced from 8192 to bound the fp32 oracle's memory
+    g = gen(7)
+    xn = randn(g, B, T, Dm).to(DEV, torch.bfloat16)
+    for dim, route in ((4096, "exp"), (1024, "exp"), (1024, "softmax")):
+        m, g2 = _layer(dim, Dm, 32, 8, None, route, None, torch.bfloat16, seed=dim)
+        v = randn(g2, B, T, dim).to(DEV, torch.bfloat16)
+        dy = torch.ones_like(v)
+        got = _hip_layer(m, v, xn, dy)
+        ref = _oracle_layer(m, v, xn, dy, route, None)
+        for n, a, b in zip(NAMES, got, ref):
+            assert_close(f"{n} ({dim}, {route})", a, b, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 32), (8, 32), (8, 5)])
+def test_mfma_matches_generic(dtype, S, K):
+    """Mid-size problems through both kernel families, fixed and packed."""
+    g = gen(S * 100 + K)
+    D, Bt, T = 192, 3, 333
+    x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
+    a = torch.softmax(randn(g, Bt, T, K), -1).to(DEV, dtype)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
+    dy = randn(g, Bt, T, D).to(DEV, dtype)
+
+    def run(**kw):
+        xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
+        if "cu_seqlens" in kw:
+            y, _ = moc_triton(xx.view(-1, D), aa.view(-1, K), bb, activation="silu", **kw)
+            y.backward(dy.view(-1, D))
+        else:
+            y, _ = moc_triton(xx, aa, bb, activation="silu")
+            y.backward(dy)
+        return y.detach().reshape(x.shape), xx.grad, aa.grad, bb.grad
+
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), "silu")
+    got = run()
+    other = _with_path("generic", run)
+    for n, u, v, r in zip(("y", "dx", "dalpha", "dbasis"), got, other, ref):
+        assert_close(n, u, r, dtype)
+        assert_close(n + " (mfma vs generic)", u, v, dtype)
+    lengths = [1, 2, 70, 3, 200, 17, 400, 5, 301]
+    cu = torch.tensor([0, *itertools.accumulate(lengths)], device=DEV, dtype=torch.int64)
+    assert cu[-1] == Bt * T
+    gv = run(cu_seqlens=cu, max_seqlen=400)
+    refv = O.moc_varlen_grads_ref(rx.detach().view(-1, D), ra.detach().view(-1, K), rb.detach(),
+                                  cu.cpu(), dy.float().cpu().view(-1, D), "silu")
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), gv, refv):
+        assert_close("varlen " + n, u.reshape(r.shape), r, dtype)
+
+
+def test_config4_decode():
+    """prefill a 1024-token prompt, then single-token steps; y against the
+    full forward (rows subsampled), cache bit-exact."""
+    B, D, Z, K, S, P, steps = 256, 2048, 2048, 16, 4, 1024, 64
+    m, g = _layer(D, Z, K, S, "silu", "softmax", None, torch.bfloat16)
+    x = randn(g, B, P + steps, D).to(DEV, torch.bfloat16)
+    z = randn(g, B, P + steps, Z).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        _, cache = m(x[:, :P], z[:, :P], output_final_state=True)
+        outs = []
+        for t in range(P, P + steps):
+            y, cache = m.step(x[:, t:t + 1], z[:, t:t + 1], cache=cache, output_final_state=True)
+            outs.append(y)
+        y_steps = torch.cat(outs, 1)
+    assert torch.equal(cache, x[:, -S:].transpose(1, 2))
+    rows = torch.arange(0, B, 37, device=DEV)
+    with torch.no_grad():
+        rx = x[rows].float()
+        logits = torch.nn.functional.linear(z[rows].float(), m.router.float()).bfloat16().float()
+        alpha = O.route(logits, "softmax").bfloat16().float()
+        full = O.moc_ref(rx, alpha, m.conv_bases.float(), "silu")
+    assert_close("decode y", y_steps[rows], full[:, P:], torch.bfloat16)
