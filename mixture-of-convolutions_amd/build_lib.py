@@ -37,9 +37,9 @@ COMMON_FLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, extra: tuple[str, ...] = (), build_dir: Path = BUILD) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     msgs = [ln for ln in (res.stdout + res.stderr).splitlines()
             if "packed-fp32-ops' is not a recognized feature" not in ln]
@@ -50,26 +50,35 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
+def build(jobs: int | None = None, verbose: bool = True, defines: tuple[str, ...] = (),
+          out: Path = LIB) -> Path:
+    """Compile csrc/*.hip and link ``out``; ``defines`` are extra -D flags."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    BUILD.mkdir(parents=True, exist_ok=True)
+    build_dir = BUILD if not defines else BUILD / ("_".join(defines).replace("=", "-"))
+    build_dir.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)))
+    extra = tuple(f"-D{d}" for d in defines)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda src: _compile(src, extra, build_dir), sources))
+    LIB_OUT = Path(out)
+    tmp = LIB_OUT.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stdout + res.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, LIB_OUT)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
-    return LIB
+        print(f"built {LIB_OUT} from {len(sources)} sources")
+    return LIB_OUT
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
-    build(ap.parse_args().jobs)
+    ap.add_argument("-D", dest="defines", action="append", default=[],
+                    help="extra preprocessor define, e.g. -D MOC_BWD_MIN_WAVES=2")
+    ap.add_argument("--out", default=str(LIB))
+    a = ap.parse_args()
+    build(a.jobs, defines=tuple(a.defines), out=Path(a.out))

@@ -70,7 +70,12 @@ struct SeqLayout {
 
   __device__ __forceinline__ void bounds(int64_t t, int64_t& lo, int64_t& hi) const {
     if (cu == nullptr) {
-      lo = (t / seq_len) * seq_len;
+      if (((t | seq_len) >> 32) == 0) {  // 32-bit division where it suffices
+        const uint32_t q = static_cast<uint32_t>(t) / static_cast<uint32_t>(seq_len);
+        lo = static_cast<int64_t>(q) * seq_len;
+      } else {
+        lo = (t / seq_len) * seq_len;
+      }
       hi = lo + seq_len;
       if (hi > n_tokens) hi = n_tokens;
       return;

@@ -114,7 +114,9 @@ __device__ __forceinline__ uint32_t tap_bits(const SeqLayout& seq, int64_t t) {
 
 // ---------------------------------------------------------------------------
 // Forward.  Grid: x = channel groups of 4 waves (4 * CW channels), y = token
-// ranges of n_sb super-blocks.  No LDS, no barriers.
+// ranges of n_sb super-blocks.  No LDS, no barriers: every wave walks its
+// super-blocks on its own, loading the rows of super-block i+1 (x window and
+// routing weights, raw) before it computes super-block i.
 template <int S, int KC, int NB, int NC, bool ACT, bool BF>
 __global__ void __launch_bounds__(256)
 fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict__ a_c,
@@ -123,6 +125,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
+  using XV = Vec<E, NC>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
   const E* __restrict__ x = static_cast<const E*>(xv);
   E* __restrict__ y = static_cast<E*>(yv);
@@ -145,7 +148,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * kc + 4 * q + v;
         if (ch_ok) {
-          Vec<E, NC>::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
+          XV::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
         } else {
 #pragma unroll
           for (int c = 0; c < NC; ++c) rows[v][c] = E(0);
@@ -156,37 +159,51 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
     }
   }
 
-  const int64_t tbase = static_cast<int64_t>(blockIdx.y) * n_sb * TB;
-  for (int sb = 0; sb < n_sb; ++sb) {
-    const int64_t t0 = tbase + static_cast<int64_t>(sb) * TB;
-    if (t0 >= N) break;
+  // raw rows of one super-block: x window (trun-(S-1) .. trun+R-1) and the
+  // alpha A operands (row i = j of block b is token t0 + R*(j/4) + 4b + j%4)
+  E xr[W][NC];
+  Op ar[NB][KC];
+  auto fetch = [&](int64_t t0) {
     const int64_t trun = t0 + R * q;
-
-    // x window: rows trun-(S-1) .. trun+R-1
-    float xw[W][NC];
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       const int64_t t = trun - (S - 1) + w;
-      E e[NC];
       if (ch_ok && t >= 0 && t < N) {
-        Vec<E, NC>::load(x + t * D + dl, e);
+        XV::load(x + t * D + dl, xr[w]);
       } else {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) e[c] = E(0);
+        for (int c = 0; c < NC; ++c) xr[w][c] = E(0);
       }
-#pragma unroll
-      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(e[c]);
     }
-    // alpha A operands: row i = j of block b is token t0 + R*(j/4) + 4b + j%4
-    Op aop[NB][KC];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t tok = t0 + R * (j >> 2) + 4 * b + (j & 3);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        aop[b][kc] = (tok < N) ? *reinterpret_cast<const Op*>(a_c + tok * KP + 16 * kc + 4 * q)
-                               : C::zero();
+        ar[b][kc] = (tok < N) ? *reinterpret_cast<const Op*>(a_c + tok * KP + 16 * kc + 4 * q)
+                              : C::zero();
     }
+  };
+
+  const int64_t tbase = static_cast<int64_t>(blockIdx.y) * n_sb * TB;
+  if (tbase < N) fetch(tbase);
+  for (int sb = 0; sb < n_sb; ++sb) {
+    const int64_t t0 = tbase + static_cast<int64_t>(sb) * TB;
+    if (t0 >= N) break;
+    const int64_t trun = t0 + R * q;
+
+    float xw[W][NC];
+#pragma unroll
+    for (int w = 0; w < W; ++w)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
+    Op aop[NB][KC];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) aop[b][kc] = ar[b][kc];
+    // issue the next super-block's loads before computing this one
+    if (sb + 1 < n_sb && t0 + TB < N) fetch(t0 + TB);
 
     bool interior = true;
     if (trun < N) {
@@ -208,24 +225,17 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        f32x4 w[NB][NC];
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            f32x4 w = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) t = C::mma(aop[b][kc], bop[c][s][kc], t);
-            w[b][c] = t;
-          }
+            for (int kc = 0; kc < KC; ++kc) w = C::mma(aop[b][kc], bop[c][s][kc], w);
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = 4 * b + v;
-            if (!MASK || ((ok[r] >> s) & 1u)) {
-#pragma unroll
-              for (int c = 0; c < NC; ++c) acc[r][c] = fmaf(xw[r + s][c], w[b][c][v], acc[r][c]);
+            for (int v = 0; v < 4; ++v) {
+              const int r = 4 * b + v;
+              if (!MASK || ((ok[r] >> s) & 1u)) acc[r][c] = fmaf(xw[r + s][c], w[v], acc[r][c]);
             }
           }
       }
@@ -236,7 +246,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
           E o[NC];
 #pragma unroll
           for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
-          Vec<E, NC>::store(y + t * D + dl, o);
+          XV::store(y + t * D + dl, o);
         }
       }
     };
@@ -246,22 +256,64 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// m = g * x as an MFMA operand.  With bf16 operands m is split into a bf16 high
+// part (its upper 16 bits) and a bf16 low part (round(m - high)), so that the
+// products of the dalpha / dbasis MFMAs keep about 16 significant bits of m
+// instead of 8: dbasis sums m over all tokens, and when g is close to constant
+// (loss = y.sum(), small kernels) the part of m that varies with g is below
+// bf16 resolution.  With fp32 operands m is used as is.
+template <bool BF>
+struct MSplit;
+
+template <>
+struct MSplit<true> {
+  static constexpr int kParts = 2;
+  static __device__ __forceinline__ void split(float m, uint16_t (&e)[2]) {
+    const uint32_t u = __float_as_uint(m);
+    e[0] = static_cast<uint16_t>(u >> 16);
+    e[1] = f32_to_bf16(m - __uint_as_float(u & 0xffff0000u));
+  }
+};
+
+template <>
+struct MSplit<false> {
+  static constexpr int kParts = 1;
+  static __device__ __forceinline__ void split(float m, float (&e)[1]) { e[0] = m; }
+};
+
+// Wave-local ordering of LDS traffic: LDS operations of one wave complete in
+// issue order; this keeps the compiler from moving them across the point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Backward, stage 1.  A workgroup of WPG waves covers WPG * CW channels and a
-// range of n_sb super-blocks; all its waves walk the same super-blocks.
-// Super-block i covers rows [t0, t0 + TB) with t0 = i * EOWN, EOWN = TB - (S-1):
-// its first EOWN rows are its own, the last S-1 rows only provide the future
-// g / W the own rows' dx needs (they are recomputed as own rows of block i+1).
-// Per super-block and lane:
+// range of n_sb super-blocks; all its waves walk the same super-blocks, one
+// workgroup barrier per super-block.  Super-block i covers rows [t0, t0 + TB)
+// with t0 = i * EOWN, EOWN = TB - (S-1): its first EOWN rows are its own, the
+// last S-1 rows only provide the later g / W the own rows' dx needs (they are
+// recomputed as own rows of block i+1).  Per super-block and lane:
 //   P (SiLU only) from MFMA W and the register window; g = dy * silu'(P);
-//   dx[u] = sum_s g[u+S-1-s] W_s[u+S-1-s]: W at the later token comes from an
-//     MFMA on alpha rows shifted by S-1-s, g of the next lane group's first
-//     S-1 rows by a cross-lane read;
-//   m_s = g * x_shift_s  ->  dbasis MFMA (m^T . alpha, accumulated over the
-//     whole range in registers) and, through LDS, dalpha MFMA (m . basis^T);
-//   the WPG waves' dalpha tiles are summed in LDS in wave order.
+//   dx[u] = sum_s g[u+S-1-s] W_s[u+S-1-s]: W at the later token from an MFMA on
+//     alpha rows shifted by S-1-s, g of the next lane group's first S-1 rows by
+//     a cross-lane read;
+//   per tap s: m_s = g * x_shift_s -> dbasis MFMA (m^T . alpha, accumulated over
+//     the whole range in registers) and, through a wave-private LDS tile, the
+//     dalpha MFMA (m . basis^T) accumulated over taps;
+//   the WPG waves' dalpha tiles are summed in LDS in wave order after the barrier.
+// Routing weights of the super-block (TB + S - 1 rows) are staged in LDS,
+// double buffered; x / dy rows of the next super-block are loaded before the
+// current one is computed.
 // Outputs: dx (own rows), part_da[blockIdx.x][t][KP], part_db[blockIdx.y][KP][S][D].
+// Minimum waves per SIMD the backward is compiled for (register budget 512 / n).
+#ifndef MOC_BWD_MIN_WAVES
+#define MOC_BWD_MIN_WAVES 1
+#endif
+
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
-__global__ void __launch_bounds__(64 * WPG)
+__global__ void __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(MOC_BWD_MIN_WAVES)))
 bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
@@ -270,13 +322,18 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
+  using XV = Vec<E, NC>;
+  using MS = MSplit<BF>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
   constexpr int EOWN = TB - (S - 1);
-  constexpr int MROW = S * CW + 4;  // padded LDS row: 8 / 16-byte aligned operand reads
+  constexpr int NP = MS::kParts;
+  constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
+  constexpr int MROW = CW + 4;        // padded LDS row of one m tile (elements)
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
 
-  __shared__ E m_lds[WPG][TB][MROW];
-  __shared__ float da_lds[WPG][NB][KC][16][17];
+  __shared__ E a_lds[2][AROWS][KP];
+  __shared__ E m_lds[WPG][NP][TB][MROW];
+  __shared__ float da_lds[2][WPG][NB][KC][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
   const E* __restrict__ dy = static_cast<const E*>(dyv);
@@ -303,7 +360,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * kc + 4 * q + v;
         if (ch_ok) {
-          Vec<E, NC>::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
+          XV::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
         } else {
 #pragma unroll
           for (int c = 0; c < NC; ++c) rows[v][c] = E(0);
@@ -334,67 +391,89 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) dbacc[c][s][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // raw rows of one super-block for this lane: x window, dy rows; alpha rows
+  // (AROWS x KP elements, spread over the workgroup's threads) for LDS
+  constexpr int AVEC = 4;                                  // elements per alpha load
+  constexpr int ACHUNKS = AROWS * KP / AVEC;
+  constexpr int APER = (ACHUNKS + 64 * WPG - 1) / (64 * WPG);
+  E xr[W][NC];
+  E dr[R][NC];
+  E arw[APER][AVEC];
+  auto fetch = [&](int64_t t0) {
+    const int64_t trun = t0 + R * q;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const int64_t t = trun - (S - 1) + w;
+      if (ch_ok && t >= 0 && t < N) {
+        XV::load(x + t * D + dl, xr[w]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) xr[w][c] = E(0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t t = trun + r;
+      if (ch_ok && t < N) {
+        XV::load(dy + t * D + dl, dr[r]);
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) dr[r][c] = E(0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < APER; ++i) {
+      const int chunk = tid + i * 64 * WPG;
+      const int64_t tok = t0 + chunk / (KP / AVEC);
+      if (chunk < ACHUNKS && tok < N) {
+        Vec<E, AVEC>::load(a_c + tok * KP + (chunk % (KP / AVEC)) * AVEC, arw[i]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < AVEC; ++v) arw[i][v] = E(0);
+      }
+    }
+  };
+  auto stage_alpha = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < APER; ++i) {
+      const int chunk = tid + i * 64 * WPG;
+      if (chunk < ACHUNKS)
+        Vec<E, AVEC>::store(&a_lds[buf][chunk / (KP / AVEC)][(chunk % (KP / AVEC)) * AVEC], arw[i]);
+    }
+  };
+
+  const int64_t first = static_cast<int64_t>(blockIdx.y) * n_sb * EOWN;
+  if (first < N) {
+    fetch(first);
+    stage_alpha(0);
+  }
+  __syncthreads();
+
   for (int sb = 0; sb < n_sb; ++sb) {
-    const int64_t t0 = (static_cast<int64_t>(blockIdx.y) * n_sb + sb) * EOWN;
+    const int64_t t0 = first + static_cast<int64_t>(sb) * EOWN;
     if (t0 >= N) break;  // uniform over the workgroup
+    const int buf = sb & 1;
     const int64_t own_end = (t0 + EOWN < N) ? t0 + EOWN : N;
     const int64_t trun = t0 + R * q;
 
     float xw[W][NC];
     float g[R][NC];
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int64_t t = trun - (S - 1) + w;
-      E e[NC];
-      if (ch_ok && t >= 0 && t < N) {
-        Vec<E, NC>::load(x + t * D + dl, e);
-      } else {
+    for (int w = 0; w < W; ++w)
 #pragma unroll
-        for (int c = 0; c < NC; ++c) e[c] = E(0);
-      }
+      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(e[c]);
-    }
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t t = trun + r;
-      E e[NC];
-      if (ch_ok && t < N) {
-        Vec<E, NC>::load(dy + t * D + dl, e);
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) e[c] = E(0);
-      }
-#pragma unroll
-      for (int c = 0; c < NC; ++c) g[r][c] = C::to_f(e[c]);
-    }
-    // alpha A operands, rows shifted by e = 0..S-1 tokens
-    Op aop[S][NB][KC];
-#pragma unroll
-    for (int e = 0; e < S; ++e)
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int64_t tok = t0 + R * (j >> 2) + 4 * b + (j & 3) + e;
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-          aop[e][b][kc] = (tok < N) ? *reinterpret_cast<const Op*>(a_c + tok * KP + 16 * kc + 4 * q)
-                                    : C::zero();
-      }
-    // alpha^T B operands of the dbasis MFMA: at[b][kc][v] = alpha[trun + 4b + v, 16kc + j],
-    // zero for rows that are not this super-block's own
-    Op at[NB][KC];
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        E e4[4];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t tok = trun + 4 * b + v;
-          e4[v] = (tok < own_end) ? a_c[tok * KP + 16 * kc + j] : E(0);
-        }
-        at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
-      }
+      for (int c = 0; c < NC; ++c) g[r][c] = C::to_f(dr[r][c]);
+    const bool more = (sb + 1 < n_sb) && (t0 + EOWN < N);
+    if (more) fetch(t0 + EOWN);
+
+    // alpha operand of token-row block b shifted by e rows (row i = j)
+    auto aop = [&](int e, int b, int kc) -> Op {
+      return *reinterpret_cast<const Op*>(
+          &a_lds[buf][R * (j >> 2) + 4 * b + (j & 3) + e][16 * kc + 4 * q]);
+    };
 
     bool interior = true;
     if (trun < N) {
@@ -403,6 +482,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       const int64_t last = (trun + W < N ? trun + W : N);
       interior = (trun - lo >= S - 1) && (last <= hi);
     }
+
+    f32x4 dacc[NB][KC];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) dacc[b][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto body = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
@@ -425,7 +510,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int c = 0; c < NC; ++c) {
               f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop[0][b][kc], bop[c][s][kc], w4);
+              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
 #pragma unroll
               for (int v = 0; v < 4; ++v) {
                 const int r = 4 * b + v;
@@ -467,7 +552,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int c = 0; c < NC; ++c) {
               f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop[off][b][kc], bop[c][s][kc], w4);
+              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(off, b, kc), bop[c][s][kc], w4);
 #pragma unroll
               for (int v = 0; v < 4; ++v) {
                 const int r = 4 * b + v;
@@ -484,63 +569,88 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             E o[NC];
 #pragma unroll
             for (int c = 0; c < NC; ++c) o[c] = C::from_f(dxa[r][c]);
-            Vec<E, NC>::store(dx + t * D + dl, o);
+            XV::store(dx + t * D + dl, o);
           }
         }
       }
 
-      // m_s = g * x[t-(S-1-s)]: dbasis MFMA and the LDS copy for dalpha
+      // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
 #pragma unroll
       for (int s = 0; s < S; ++s) {
+        // alpha^T operands (zero for rows that are not this super-block's own)
+        Op at[NB][KC];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc) {
+            E e4[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int row = R * q + 4 * b + v;
+              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
+            }
+            at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+          }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          E mv[4][NC];
+          E mv[NP][4][NC];
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int r = 4 * b + v;
             const bool on = !MASK || ((ok[r] >> s) & 1u);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) mv[v][c] = C::from_f(on ? g[r][c] * xw[r + s][c] : 0.f);
-            Vec<E, NC>::store(&m_lds[wave][R * q + r][s * CW + NC * j], mv[v]);
+            for (int c = 0; c < NC; ++c) {
+              E parts[NP];
+              MS::split(on ? g[r][c] * xw[r + s][c] : 0.f, parts);
+#pragma unroll
+              for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
+            }
+#pragma unroll
+            for (int h = 0; h < NP; ++h) XV::store(&m_lds[wave][h][R * q + r][NC * j], mv[h][v]);
           }
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const Op am = C::make(mv[0][c], mv[1][c], mv[2][c], mv[3][c]);
+          for (int h = 0; h < NP; ++h)
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) dbacc[c][s][kc] = C::mma(am, at[b][kc], dbacc[c][s][kc]);
-          }
+            for (int c = 0; c < NC; ++c) {
+              const Op am = C::make(mv[h][0][c], mv[h][1][c], mv[h][2][c], mv[h][3][c]);
+#pragma unroll
+              for (int kc = 0; kc < KC; ++kc) dbacc[c][s][kc] = C::mma(am, at[b][kc], dbacc[c][s][kc]);
+            }
         }
+        wave_lds_sync();
+        // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+          for (int h = 0; h < NP; ++h)
+#pragma unroll
+            for (int cg = 0; cg < NC; ++cg) {
+              const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][h][16 * rb + j][16 * cg + 4 * q]);
+#pragma unroll
+              for (int kc = 0; kc < KC; ++kc) dacc[rb][kc] = C::mma(am, bda[s][cg][kc], dacc[rb][kc]);
+            }
+        wave_lds_sync();
       }
     };
     if (__all(interior)) body(std::false_type{});
     else body(std::true_type{});
 
-    __syncthreads();
-    // dalpha over this wave's channels: D[t][k] = sum_(s,ch) m[t][(s,ch)] basis[k][(s,ch)]
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-          for (int cg = 0; cg < NC; ++cg) {
-            const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][16 * rb + j][s * CW + 16 * cg + 4 * q]);
-            acc = C::mma(am, bda[s][cg][kc], acc);
-          }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) da_lds[wave][rb][kc][4 * q + v][j] = acc[v];
-      }
+        for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kc][4 * q + v][j] = dacc[rb][kc][v];
+    if (more) stage_alpha(buf ^ 1);
     __syncthreads();
-    // sum the WPG waves' tiles in wave order; own rows only
+    // sum the WPG waves' dalpha tiles in wave order; own rows only
     for (int idx = tid; idx < NB * KC * 256; idx += 64 * WPG) {
       const int rb = idx / (KC * 256);
       const int kc = (idx / 256) % KC;
       const int row = (idx >> 4) & 15, col = idx & 15;
       float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < WPG; ++w) sum += da_lds[w][rb][kc][row][col];
+      for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kc][row][col];
       const int64_t t = t0 + 16 * rb + row;
       if (t < own_end) part_da[(static_cast<int64_t>(blockIdx.x) * N + t) * KP + 16 * kc + col] = sum;
     }

@@ -6,56 +6,77 @@ namespace mfma {
 
 // ---------------------------------------------------------------------------
 // Operand preparation (one launch):
-//   blocks [0, a_blocks): one lane per token; a_c[t, k] = alpha in the compute
-//     dtype, K padded to KP with zeros; with routing, alpha = softmax / exp of
-//     the logits rounded to the logits' dtype (what torch's router activation
-//     returns), and a_r[t, k] keeps that value in fp32 for the backward's
-//     activation gradient;
+//   blocks [0, a_blocks): 16 lanes per token, lane i holding k = i + 16 kc;
+//     a_c[t, k] = alpha in the compute dtype, K padded to KP with zeros; with
+//     routing, alpha = softmax / exp of the logits rounded to the logits' dtype
+//     (what torch's router activation returns), and a_r[t, k] keeps that value
+//     in fp32 for the backward's activation gradient;
 //   other blocks: b_c[k, s, d] = basis in the compute dtype, rows k >= K zero.
-template <bool BF>
+template <bool BF, int KC>
 __global__ void __launch_bounds__(256)
 prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* __restrict__ basis,
-            int b_dt, int64_t N, int K, int KP, int S, int64_t D,
-            typename CT<BF>::elem* __restrict__ a_c, float* __restrict__ a_r,
-            typename CT<BF>::elem* __restrict__ b_c, int64_t a_blocks) {
+            int b_dt, int64_t N, int K, int S, int64_t D, typename CT<BF>::elem* __restrict__ a_c,
+            float* __restrict__ a_r, typename CT<BF>::elem* __restrict__ b_c, int64_t a_blocks) {
   using C = CT<BF>;
   using E = typename C::elem;
+  constexpr int KP = 16 * KC;
   if (static_cast<int64_t>(blockIdx.x) < a_blocks) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= N) return;
-    const int64_t base = t * K;
-    float m = -INFINITY, inv = 1.f;
-    if (routing == ROUTE_SOFTMAX) {
-      for (int k = 0; k < K; ++k) m = fmaxf(m, load_any(alpha, a_dt, base + k));
-      float sum = 0.f;
-      for (int k = 0; k < K; ++k) sum += __expf(load_any(alpha, a_dt, base + k) - m);
-      inv = 1.0f / sum;
+    const int64_t t = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+    const int i = threadIdx.x & 15;
+    const bool live = t < N;
+    float l[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = i + 16 * kc;
+      l[kc] = (live && k < K) ? load_any(alpha, a_dt, t * K + k) : -INFINITY;
     }
-    for (int k = 0; k < KP; ++k) {
-      float v = 0.f;
-      if (k < K) {
-        const float l = load_any(alpha, a_dt, base + k);
-        if (routing == ROUTE_SOFTMAX) v = round_to(__expf(l - m) * inv, a_dt);
-        else if (routing == ROUTE_EXP) v = round_to(__expf(l), a_dt);
-        else v = l;
-        if (routing != ROUTE_ALPHA) a_r[base + k] = v;
+    float v[KC];
+    if (routing == ROUTE_SOFTMAX) {
+      float m = l[0];
+#pragma unroll
+      for (int kc = 1; kc < KC; ++kc) m = fmaxf(m, l[kc]);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+      float e[KC], sum = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        e[kc] = (i + 16 * kc < K) ? __expf(l[kc] - m) : 0.f;
+        sum += e[kc];
       }
-      a_c[t * KP + k] = C::from_f(v);
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+      const float inv = 1.0f / sum;
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) v[kc] = round_to(e[kc] * inv, a_dt);
+    } else if (routing == ROUTE_EXP) {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) v[kc] = (i + 16 * kc < K) ? round_to(__expf(l[kc]), a_dt) : 0.f;
+    } else {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) v[kc] = (i + 16 * kc < K) ? l[kc] : 0.f;
+    }
+    if (!live) return;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = i + 16 * kc;
+      a_c[t * KP + k] = C::from_f(v[kc]);
+      if (routing != ROUTE_ALPHA && k < K) a_r[t * K + k] = v[kc];
     }
   } else {
-    const int64_t i = (static_cast<int64_t>(blockIdx.x) - a_blocks) * 256 + threadIdx.x;
+    const int64_t idx = (static_cast<int64_t>(blockIdx.x) - a_blocks) * 256 + threadIdx.x;
     const int64_t sd = static_cast<int64_t>(S) * D;
-    if (i >= KP * sd) return;
-    const int64_t k = i / sd;
-    b_c[i] = (k < K) ? C::from_f(load_any(basis, b_dt, i)) : E(0);
+    if (idx >= KP * sd) return;
+    const int64_t k = idx / sd;
+    b_c[idx] = (k < K) ? C::from_f(load_any(basis, b_dt, idx)) : E(0);
   }
 }
 
 // ---------------------------------------------------------------------------
 // Backward stage 2 (one launch):
-//   blocks [0, da_blocks): one lane per token; dalpha = sum of the n_da channel
-//     partials in order, then the router activation gradient
-//     (softmax: a (da - <a, da>), exp: a da), stored in the alpha dtype;
+//   blocks [0, da_blocks): 16 lanes per token, lane i holding k = i + 16 kc;
+//     dalpha = sum of the n_da channel partials in order, then the router
+//     activation gradient (softmax: a (da - <a, da>), exp: a da), stored in the
+//     alpha dtype;
 //   other blocks: one lane per basis element; dbasis = sum of the n_db token
 //     partials in order, stored in the basis dtype.
 template <int KC>
@@ -66,45 +87,52 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
               int64_t D, int64_t da_blocks) {
   constexpr int KP = 16 * KC;
   if (static_cast<int64_t>(blockIdx.x) < da_blocks) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= N) return;
-    float da[KP];
+    const int64_t t = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+    const int i = threadIdx.x & 15;
+    const bool live = t < N;
+    float da[KC], a[KC];
 #pragma unroll
-    for (int k = 0; k < KP; ++k) da[k] = 0.f;
-    for (int64_t p = 0; p < n_da; ++p) {
-      const float4* src = reinterpret_cast<const float4*>(part_da + (p * N + t) * KP);
+    for (int kc = 0; kc < KC; ++kc) {
+      da[kc] = 0.f;
+      a[kc] = 0.f;
+    }
+    if (live) {
+      for (int64_t p = 0; p < n_da; ++p) {
 #pragma unroll
-      for (int i = 0; i < KP / 4; ++i) {
-        const float4 v = src[i];
-        da[4 * i + 0] += v.x;
-        da[4 * i + 1] += v.y;
-        da[4 * i + 2] += v.z;
-        da[4 * i + 3] += v.w;
+        for (int kc = 0; kc < KC; ++kc) da[kc] += part_da[(p * N + t) * KP + i + 16 * kc];
+      }
+      if (routing != ROUTE_ALPHA) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+          if (i + 16 * kc < K) a[kc] = a_r[t * K + i + 16 * kc];
       }
     }
     float dot = 0.f;
     if (routing == ROUTE_SOFTMAX) {
 #pragma unroll
-      for (int k = 0; k < KP; ++k)
-        if (k < K) dot = fmaf(a_r[t * K + k], da[k], dot);
-    }
+      for (int kc = 0; kc < KC; ++kc) dot = fmaf(a[kc], da[kc], dot);
 #pragma unroll
-    for (int k = 0; k < KP; ++k) {
+      for (int o = 8; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 16);
+    }
+    if (!live) return;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = i + 16 * kc;
       if (k < K) {
-        float v = da[k];
-        if (routing == ROUTE_SOFTMAX) v = a_r[t * K + k] * (v - dot);
-        else if (routing == ROUTE_EXP) v = a_r[t * K + k] * v;
+        float v = da[kc];
+        if (routing == ROUTE_SOFTMAX) v = a[kc] * (v - dot);
+        else if (routing == ROUTE_EXP) v = a[kc] * v;
         store_any(dalpha, a_dt, t * K + k, v);
       }
     }
   } else {
-    const int64_t i = (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x;
+    const int64_t idx = (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x;
     const int64_t sd = static_cast<int64_t>(S) * D;
-    if (i >= static_cast<int64_t>(K) * sd) return;
-    const int64_t k = i / sd, rest = i - k * sd;
+    if (idx >= static_cast<int64_t>(K) * sd) return;
+    const int64_t k = idx / sd, rest = idx - k * sd;
     float acc = 0.f;
     for (int64_t p = 0; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
-    store_any(dbasis, b_dt, i, acc);
+    store_any(dbasis, b_dt, idx, acc);
   }
 }
 
@@ -145,22 +173,29 @@ Plan plan(const Problem& p, bool backward) {
   return pl;
 }
 
-void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
-                 hipStream_t st) {
-  const int64_t a_blocks = cdiv(p.n_tokens, 256);
+template <bool BF, int KC>
+void prep_one(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
+              hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const int64_t a_blocks = cdiv(p.n_tokens * 16, 256);
   const int64_t b_blocks = cdiv(static_cast<int64_t>(pl.KP) * p.S * p.D, 256);
   float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<float*>(ws + pl.off_ar) : nullptr;
-  const dim3 grid(static_cast<unsigned>(a_blocks + b_blocks));
-  if (p.x_dt == DT_BF16) {
-    hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(256), 0, st, alpha, p.a_dt, p.routing, basis,
-                       p.b_dt, p.n_tokens, static_cast<int>(p.K), pl.KP, static_cast<int>(p.S),
-                       p.D, reinterpret_cast<uint16_t*>(ws + pl.off_ac), a_r,
-                       reinterpret_cast<uint16_t*>(ws + pl.off_bc), a_blocks);
+  hipLaunchKernelGGL((prep_kernel<BF, KC>), dim3(static_cast<unsigned>(a_blocks + b_blocks)),
+                     dim3(256), 0, st, alpha, p.a_dt, p.routing, basis, p.b_dt, p.n_tokens,
+                     static_cast<int>(p.K), static_cast<int>(p.S), p.D,
+                     reinterpret_cast<E*>(ws + pl.off_ac), a_r, reinterpret_cast<E*>(ws + pl.off_bc),
+                     a_blocks);
+}
+
+void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
+                 hipStream_t st) {
+  const bool bf = p.x_dt == DT_BF16;
+  if (pl.KP == 16) {
+    if (bf) prep_one<true, 1>(p, pl, alpha, basis, ws, st);
+    else prep_one<false, 1>(p, pl, alpha, basis, ws, st);
   } else {
-    hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(256), 0, st, alpha, p.a_dt, p.routing, basis,
-                       p.b_dt, p.n_tokens, static_cast<int>(p.K), pl.KP, static_cast<int>(p.S),
-                       p.D, reinterpret_cast<float*>(ws + pl.off_ac), a_r,
-                       reinterpret_cast<float*>(ws + pl.off_bc), a_blocks);
+    if (bf) prep_one<true, 2>(p, pl, alpha, basis, ws, st);
+    else prep_one<false, 2>(p, pl, alpha, basis, ws, st);
   }
 }
 
@@ -208,7 +243,7 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     default: break;
   }
-  const int64_t da_blocks = cdiv(p.n_tokens, 256);
+  const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
   const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
   const float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<const float*>(ws + pl.off_ar)
                                                 : nullptr;

@@ -6,12 +6,14 @@ fallback: if it is missing or fails to load, every MoC op raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
+# MOC_HIP_LIB selects another build of the library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("MOC_HIP_LIB") or Path(__file__).resolve().parent / "libmoc_hip.so")
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2

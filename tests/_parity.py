@@ -44,6 +44,24 @@ def round_like(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t + (t.detach().to(dtype).to(t.dtype) - t.detach())
 
 
+class _RoundGrad(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, t, dtype):
+        ctx.dtype = dtype
+        return t.view_as(t)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dtype).to(g.dtype), None
+
+
+def round_grad_like(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Identity whose incoming gradient is rounded to ``dtype``: models a tensor
+    of that dtype in the graph (e.g. bf16 router logits, whose gradient torch
+    holds in bf16 before the router GEMM's backward)."""
+    return _RoundGrad.apply(t, dtype)
+
+
 def gen(seed: int = 0) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
 

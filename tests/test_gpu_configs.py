@@ -17,7 +17,7 @@ import torch
 import moc
 from moc import MoC, moc_triton
 from oracle import moc_oracle as O
-from tests._parity import assert_close, gen, randn, round_like
+from tests._parity import assert_close, gen, randn, round_grad_like, round_like
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -39,7 +39,7 @@ def _oracle_layer(m, x, z, dy, route, act, cu=None):
     rz = z.detach().float().requires_grad_()
     rr = m.router.detach().float().requires_grad_()
     rb = m.conv_bases.detach().float().requires_grad_()
-    logits = round_like(torch.nn.functional.linear(rz, rr), dtype)
+    logits = round_grad_like(round_like(torch.nn.functional.linear(rz, rr), dtype), dtype)
     alpha = round_like(O.route(logits, route), dtype)
     if cu is None:
         y = O.moc_ref(rx, alpha, rb, act)

@@ -18,7 +18,7 @@ import torch
 import moc
 from moc import MoC, moc_triton
 from oracle import moc_oracle as O
-from tests._parity import assert_close, gen, randn, round_like
+from tests._parity import assert_close, gen, randn, round_grad_like, round_like
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -165,7 +165,7 @@ def test_module_routed_fwd_bwd(route, act, dtype):
     rb = m.conv_bases.detach().float().cpu().requires_grad_()
     # torch's GPU router GEMM returns logits in the module dtype, and the router
     # activation output has the logits' dtype: round both, keep the gradients
-    logits = round_like(torch.nn.functional.linear(rz, rr), dtype)
+    logits = round_grad_like(round_like(torch.nn.functional.linear(rz, rr), dtype), dtype)
     alpha = round_like(O.route(logits, route), dtype)
     ry = O.moc_ref(rx, alpha, rb, act)
     ry.backward(dy.float().cpu())
@@ -348,3 +348,27 @@ def test_module_varlen_routed():
 
 def test_moc_triton_name_is_hip_path():
     assert moc.moc_triton is moc.moc_hip
+
+
+@pytest.mark.parametrize("route", ["softmax", "exp"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_routed_function_dlogits(route, dtype):
+    """The logits-input autograd function directly: y, dx, d(logits), dbasis."""
+    from moc import api
+    g = gen(21)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, dtype)
+    lg = randn(g, B, T, K).to(DEV, dtype)
+    b = randn(g, K, 4, D, scale=0.1).to(DEV, dtype)
+    dy = randn(g, B, T, D).to(DEV, dtype)
+    xx, ll, bb = (t.clone().requires_grad_() for t in (x, lg, b))
+    y = api._MoCRoutedFunction.apply(xx, ll, bb, "silu", route, None, None, None, None)
+    y.backward(dy)
+    rx = x.float().cpu().requires_grad_()
+    rl = lg.float().cpu().requires_grad_()
+    rb = b.float().cpu().requires_grad_()
+    ry = O.moc_ref(rx, round_like(O.route(rl, route), dtype), rb, "silu")
+    ry.backward(dy.float().cpu())
+    assert_close("y", y, ry, dtype)
+    assert_close("dx", xx.grad, rx.grad, dtype)
+    assert_close("dlogits", ll.grad, rl.grad, dtype)
+    assert_close("dbasis", bb.grad, rb.grad, dtype)
