@@ -63,9 +63,12 @@ struct SeqLayout {
   int64_t seq_len;
   int64_t n_tokens;
 
+  // cu_seqlens is read-only for a kernel's lifetime: read it through the
+  // constant address space so that wave-uniform reads become scalar loads.
+  typedef const __attribute__((address_space(4))) int32_t c_i32;
+  typedef const __attribute__((address_space(4))) int64_t c_i64;
   __device__ __forceinline__ int64_t cu_at(int64_t j) const {
-    return cu64 ? static_cast<const int64_t*>(cu)[j]
-                : static_cast<int64_t>(static_cast<const int32_t*>(cu)[j]);
+    return cu64 ? ((c_i64*)cu)[j] : static_cast<int64_t>(((c_i32*)cu)[j]);
   }
 
   __device__ __forceinline__ void bounds(int64_t t, int64_t& lo, int64_t& hi) const {
@@ -98,6 +101,28 @@ struct SeqLayout {
     if (lo > t) lo = t;
     if (hi > n_tokens) hi = n_tokens;
     if (hi <= t) hi = t + 1;
+  }
+
+  // Smallest segment start >= lo (segment starts: 0, the cu entries, in order),
+  // or n_tokens if there is none below n_tokens.  Called with wave-uniform
+  // arguments, so its loads are scalar.
+  __device__ __forceinline__ int64_t next_start(int64_t lo) const {
+    if (lo <= 0) return 0;
+    if (lo >= n_tokens) return n_tokens;
+    if (cu == nullptr) {
+      const int64_t k = (lo + seq_len - 1) / seq_len;
+      const int64_t b = k * seq_len;
+      return b < n_tokens ? b : n_tokens;
+    }
+    // first j in [0, n_seqs] with cu[j] >= lo
+    int64_t a = 0, e = n_seqs + 1;
+    while (a < e) {
+      const int64_t m = (a + e) >> 1;
+      if (cu_at(m) < lo) a = m + 1; else e = m;
+    }
+    if (a > n_seqs) return n_tokens;
+    const int64_t b = cu_at(a);
+    return (b < n_tokens && b >= lo) ? b : n_tokens;
   }
 };
 

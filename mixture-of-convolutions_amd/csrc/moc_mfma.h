@@ -97,19 +97,94 @@ struct Vec {
   }
 };
 
+// Raw buffer resource over a byte range [base, base + bytes) (< 2 GiB).  Loads at
+// offsets outside the range return zeros and stores there are dropped by the
+// hardware, so rows before a sequence's first token, past the token axis or
+// past the channel axis need no branches: they get an out-of-range offset.
+constexpr uint32_t kOffNone = 0x80000000u;  // an offset no range here reaches
+
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Buf(const void* base, int64_t bytes) {
+    r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                          static_cast<int>(bytes > 0 ? bytes : 0), 0x00020000);
+  }
+  template <int BYTES>
+  __device__ __forceinline__ void load(uint32_t off, void* dst) const {
+    if constexpr (BYTES == 2) {
+      const uint16_t v = __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
+      __builtin_memcpy(dst, &v, 2);
+    } else if constexpr (BYTES == 4) {
+      const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0);
+      __builtin_memcpy(dst, &v, 4);
+    } else if constexpr (BYTES == 8) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(off), 0, 0);
+      __builtin_memcpy(dst, &v, 8);
+    } else {
+      static_assert(BYTES == 16, "buffer load width");
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+      __builtin_memcpy(dst, &v, 16);
+    }
+  }
+  template <int BYTES>
+  __device__ __forceinline__ void store(uint32_t off, const void* src) const {
+    if constexpr (BYTES == 4) {
+      uint32_t v;
+      __builtin_memcpy(&v, src, 4);
+      __builtin_amdgcn_raw_buffer_store_b32(v, r, static_cast<int>(off), 0, 0);
+    } else if constexpr (BYTES == 8) {
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      u32x2 v;
+      __builtin_memcpy(&v, src, 8);
+      __builtin_amdgcn_raw_buffer_store_b64(v, r, static_cast<int>(off), 0, 0);
+    } else {
+      static_assert(BYTES == 16, "buffer store width");
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      u32x4 v;
+      __builtin_memcpy(&v, src, 16);
+      __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(off), 0, 0);
+    }
+  }
+};
+
+// Byte offset of (row t, byte column col) relative to row `lo` of a row-major
+// buffer, or kOffNone when `on` is false.  Negative rows give offsets >= 2^31.
+__device__ __forceinline__ uint32_t row_off(int64_t t, int64_t lo, uint32_t row_bytes,
+                                            uint32_t col, bool on = true) {
+  const uint32_t o = static_cast<uint32_t>(static_cast<int32_t>(t - lo)) * row_bytes + col;
+  return on ? o : kOffNone;
+}
+
 __device__ __forceinline__ float silu_f(float p) { return p * sigmoid_f(p); }
 
-// Bit s set <=> tap s of token t reads a token of t's own sequence,
-// i.e. S-1-s <= t - lo(t).  Tokens at or past n_tokens get no taps.
-template <int S>
-__device__ __forceinline__ uint32_t tap_bits(const SeqLayout& seq, int64_t t) {
-  if (t >= seq.n_tokens || t < 0) return 0u;
-  int64_t lo, hi;
-  seq.bounds(t, lo, hi);
-  const int64_t pos = t - lo;
-  if (pos >= S - 1) return (1u << S) - 1u;
-  // taps s >= S-1-pos are valid
-  return ((1u << S) - 1u) & ~((1u << (S - 1 - pos)) - 1u);
+// Sequence starts near a super-block.  A tap s of token t is valid when its
+// source t-(S-1-s) is not before t's segment start.  All starts that can
+// invalidate a tap of the rows [r0, r1] lie in [r0 - (S-2), r1]; `starts_in`
+// tells (wave-uniformly) whether there is one, and `tap_bits_rows` gives the
+// valid-tap bits of rows row0 + r (r < NROWS) by walking those starts.
+__device__ __forceinline__ bool starts_in(const SeqLayout& seq, int64_t lo, int64_t hi) {
+  return seq.next_start(lo) <= hi;
+}
+
+template <int S, int NROWS>
+__device__ __forceinline__ void tap_bits_rows(const SeqLayout& seq, int64_t row0, int64_t w_lo,
+                                              int64_t w_hi, uint32_t (&ok)[NROWS]) {
+  int64_t last[NROWS];
+#pragma unroll
+  for (int r = 0; r < NROWS; ++r) last[r] = INT64_MIN / 2;
+  for (int64_t b = seq.next_start(w_lo); b <= w_hi && b < seq.n_tokens; b = seq.next_start(b + 1)) {
+#pragma unroll
+    for (int r = 0; r < NROWS; ++r)
+      if (b <= row0 + r) last[r] = b;
+  }
+#pragma unroll
+  for (int r = 0; r < NROWS; ++r) {
+    const int64_t t = row0 + r;
+    const int64_t pos = t - last[r];
+    uint32_t bits = (1u << S) - 1u;
+    if (pos < S - 1) bits &= ~((1u << (S - 1 - pos)) - 1u);  // taps s >= S-1-pos
+    ok[r] = (t < seq.n_tokens && t >= 0) ? bits : 0u;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -125,7 +200,6 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
-  using XV = Vec<E, NC>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
   const E* __restrict__ x = static_cast<const E*>(xv);
   E* __restrict__ y = static_cast<E*>(yv);
@@ -137,6 +211,18 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   const int64_t dl = d0 + NC * j;
   const bool ch_ok = dl < D;
 
+  constexpr int ESZ = static_cast<int>(sizeof(E));
+  const int64_t tbase = static_cast<int64_t>(blockIdx.y) * n_sb * TB;
+  // buffers over the rows this wave touches: x / y rows [row_lo, row_hi), alpha rows [tbase, row_hi)
+  const int64_t row_lo = (tbase - (S - 1) > 0) ? tbase - (S - 1) : 0;
+  const int64_t row_hi = (tbase + static_cast<int64_t>(n_sb) * TB < N) ? tbase + static_cast<int64_t>(n_sb) * TB : N;
+  const uint32_t rb = static_cast<uint32_t>(D * ESZ);
+  const uint32_t col = static_cast<uint32_t>(dl * ESZ);
+  const Buf xb(x + row_lo * D, (row_hi - row_lo) * D * ESZ);
+  const Buf yb(y + row_lo * D, (row_hi - row_lo) * D * ESZ);
+  const Buf ab(a_c + tbase * KP, (row_hi - tbase) * KP * ESZ);
+  const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
+
   // basis B operands: bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c], v = 0..3
   Op bop[NC][S][KC];
 #pragma unroll
@@ -147,12 +233,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * kc + 4 * q + v;
-        if (ch_ok) {
-          XV::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) rows[v][c] = E(0);
-        }
+        bb.load<NC * ESZ>(row_off(k * S + s, 0, rb, col, ch_ok), rows[v]);
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) bop[c][s][kc] = C::make(rows[0][c], rows[1][c], rows[2][c], rows[3][c]);
@@ -166,26 +247,17 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   auto fetch = [&](int64_t t0) {
     const int64_t trun = t0 + R * q;
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int64_t t = trun - (S - 1) + w;
-      if (ch_ok && t >= 0 && t < N) {
-        XV::load(x + t * D + dl, xr[w]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) xr[w][c] = E(0);
-      }
-    }
+    for (int w = 0; w < W; ++w)
+      xb.load<NC * ESZ>(row_off(trun - (S - 1) + w, row_lo, rb, col, ch_ok), xr[w]);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       const int64_t tok = t0 + R * (j >> 2) + 4 * b + (j & 3);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        ar[b][kc] = (tok < N) ? *reinterpret_cast<const Op*>(a_c + tok * KP + 16 * kc + 4 * q)
-                              : C::zero();
+        ab.load<4 * ESZ>(row_off(tok, tbase, KP * ESZ, (16 * kc + 4 * q) * ESZ), &ar[b][kc]);
     }
   };
 
-  const int64_t tbase = static_cast<int64_t>(blockIdx.y) * n_sb * TB;
   if (tbase < N) fetch(tbase);
   for (int sb = 0; sb < n_sb; ++sb) {
     const int64_t t0 = tbase + static_cast<int64_t>(sb) * TB;
@@ -205,19 +277,19 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
     // issue the next super-block's loads before computing this one
     if (sb + 1 < n_sb && t0 + TB < N) fetch(t0 + TB);
 
-    bool interior = true;
-    if (trun < N) {
-      int64_t lo, hi;
-      seq.bounds(trun, lo, hi);
-      const int64_t last = (trun + R < N ? trun + R : N);
-      interior = (trun - lo >= S - 1) && (last <= hi);
-    }
+    // uniform over the wave: does a sequence start fall where it masks a tap?
+    const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB - 1;
+    const bool interior = !starts_in(seq, w_lo, w_hi);
 
     auto body = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
       uint32_t ok[R];
+      if (MASK) {
+        tap_bits_rows<S, R>(seq, trun, w_lo, w_hi, ok);
+      } else {
 #pragma unroll
-      for (int r = 0; r < R; ++r) ok[r] = MASK ? tap_bits<S>(seq, trun + r) : ((1u << S) - 1u);
+        for (int r = 0; r < R; ++r) ok[r] = (1u << S) - 1u;
+      }
       float acc[R][NC];
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -241,16 +313,13 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
       }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int64_t t = trun + r;
-        if (ch_ok && t < N) {
-          E o[NC];
+        E o[NC];
 #pragma unroll
-          for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
-          XV::store(y + t * D + dl, o);
-        }
+        for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
+        yb.store<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok), o);
       }
     };
-    if (__all(interior)) body(std::false_type{});
+    if (interior) body(std::false_type{});
     else body(std::true_type{});
   }
 }
@@ -347,6 +416,22 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const int64_t dl = d0 + NC * j;
   const bool ch_ok = wave_on && dl < D;
 
+  constexpr int ESZ = static_cast<int>(sizeof(E));
+  const int64_t first = static_cast<int64_t>(blockIdx.y) * n_sb * EOWN;
+  // buffers over the rows this workgroup touches: x / dy / dx rows [row_lo, row_hi),
+  // alpha rows [first, a_hi)
+  const int64_t last_t0 = first + static_cast<int64_t>(n_sb - 1) * EOWN;
+  const int64_t row_lo = (first - (S - 1) > 0) ? first - (S - 1) : 0;
+  const int64_t row_hi = (last_t0 + TB < N) ? last_t0 + TB : N;
+  const int64_t a_hi = (last_t0 + AROWS < N) ? last_t0 + AROWS : N;
+  const uint32_t rb = static_cast<uint32_t>(D * ESZ);
+  const uint32_t col = static_cast<uint32_t>(dl * ESZ);
+  const Buf xb(x + row_lo * D, (row_hi - row_lo) * D * ESZ);
+  const Buf dyb(dy + row_lo * D, (row_hi - row_lo) * D * ESZ);
+  const Buf dxb(dx + row_lo * D, (dx != nullptr ? row_hi - row_lo : 0) * D * ESZ);
+  const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
+  const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
+
   // W operands: bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
   Op bop[NC][S][KC];
   // dalpha B operands: bda[s][cg][kc] = basis[16kc + j, s, d0 + 16cg + 4q + v]
@@ -359,12 +444,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * kc + 4 * q + v;
-        if (ch_ok) {
-          XV::load(b_c + (static_cast<int64_t>(k) * S + s) * D + dl, rows[v]);
-        } else {
-#pragma unroll
-          for (int c = 0; c < NC; ++c) rows[v][c] = E(0);
-        }
+        bb.load<NC * ESZ>(row_off(k * S + s, 0, rb, col, ch_ok), rows[v]);
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) bop[c][s][kc] = C::make(rows[0][c], rows[1][c], rows[2][c], rows[3][c]);
@@ -372,12 +452,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       for (int cg = 0; cg < NC; ++cg) {
         const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
-        if (wave_on && ch < D) {
-          Vec<E, 4>::load(b_c + (static_cast<int64_t>(16 * kc + j) * S + s) * D + ch, e4);
-        } else {
-#pragma unroll
-          for (int v = 0; v < 4; ++v) e4[v] = E(0);
-        }
+        bb.load<4 * ESZ>(row_off((16 * kc + j) * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ),
+                                 wave_on && ch < D),
+                         e4);
         bda[s][cg][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
       }
     }
@@ -402,35 +479,17 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   auto fetch = [&](int64_t t0) {
     const int64_t trun = t0 + R * q;
 #pragma unroll
-    for (int w = 0; w < W; ++w) {
-      const int64_t t = trun - (S - 1) + w;
-      if (ch_ok && t >= 0 && t < N) {
-        XV::load(x + t * D + dl, xr[w]);
-      } else {
+    for (int w = 0; w < W; ++w)
+      xb.load<NC * ESZ>(row_off(trun - (S - 1) + w, row_lo, rb, col, ch_ok), xr[w]);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) xr[w][c] = E(0);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t t = trun + r;
-      if (ch_ok && t < N) {
-        XV::load(dy + t * D + dl, dr[r]);
-      } else {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) dr[r][c] = E(0);
-      }
-    }
+    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok), dr[r]);
 #pragma unroll
     for (int i = 0; i < APER; ++i) {
       const int chunk = tid + i * 64 * WPG;
       const int64_t tok = t0 + chunk / (KP / AVEC);
-      if (chunk < ACHUNKS && tok < N) {
-        Vec<E, AVEC>::load(a_c + tok * KP + (chunk % (KP / AVEC)) * AVEC, arw[i]);
-      } else {
-#pragma unroll
-        for (int v = 0; v < AVEC; ++v) arw[i][v] = E(0);
-      }
+      ab.load<AVEC * ESZ>(row_off(tok, first, KP * ESZ, (chunk % (KP / AVEC)) * AVEC * ESZ,
+                                  chunk < ACHUNKS),
+                          arw[i]);
     }
   };
   auto stage_alpha = [&](int buf) {
@@ -442,7 +501,6 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     }
   };
 
-  const int64_t first = static_cast<int64_t>(blockIdx.y) * n_sb * EOWN;
   if (first < N) {
     fetch(first);
     stage_alpha(0);
@@ -475,13 +533,10 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
           &a_lds[buf][R * (j >> 2) + 4 * b + (j & 3) + e][16 * kc + 4 * q]);
     };
 
-    bool interior = true;
-    if (trun < N) {
-      int64_t lo, hi;
-      seq.bounds(trun, lo, hi);
-      const int64_t last = (trun + W < N ? trun + W : N);
-      interior = (trun - lo >= S - 1) && (last <= hi);
-    }
+    // uniform: does a sequence start fall where it masks a tap of the rows
+    // [t0, t0 + TB + S - 1) (own rows, their later rows, the lanes' extended runs)?
+    const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB + S - 2;
+    const bool interior = !starts_in(seq, w_lo, w_hi);
 
     f32x4 dacc[NB][KC];
 #pragma unroll
@@ -493,8 +548,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       constexpr bool MASK = decltype(mask_tag)::value;
       // ok[r]: tap bits of row r of this lane's run extended by S-1 later rows
       uint32_t ok[R + S - 1];
+      if (MASK) {
+        tap_bits_rows<S, R + S - 1>(seq, trun, w_lo, w_hi, ok);
+      } else {
 #pragma unroll
-      for (int r = 0; r < R + S - 1; ++r) ok[r] = MASK ? tap_bits<S>(seq, trun + r) : ((1u << S) - 1u);
+        for (int r = 0; r < R + S - 1; ++r) ok[r] = (1u << S) - 1u;
+      }
 
       if (ACT) {
         float p[R][NC];
@@ -564,13 +623,10 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         }
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-          const int64_t t = trun + r;
-          if (ch_ok && t < own_end) {
-            E o[NC];
+          E o[NC];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) o[c] = C::from_f(dxa[r][c]);
-            XV::store(dx + t * D + dl, o);
-          }
+          for (int c = 0; c < NC; ++c) o[c] = C::from_f(dxa[r][c]);
+          dxb.store<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok && trun + r < own_end), o);
         }
       }
 
@@ -632,7 +688,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         wave_lds_sync();
       }
     };
-    if (__all(interior)) body(std::false_type{});
+    if (interior) body(std::false_type{});
     else body(std::true_type{});
 
 #pragma unroll
