@@ -31,6 +31,9 @@ COMMON_FLAGS = [
     "-fno-gpu-rdc",
     # packed FP32 VALU ops are kept out of the device code on this pool
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in VGPRs: the kernels read every result on VALU right away,
+    # and AGPR results would cost a v_accvgpr_read per value
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-command-line-argument",

@@ -378,7 +378,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Outputs: dx (own rows), part_da[blockIdx.x][t][KP], part_db[blockIdx.y][KP][S][D].
 // Minimum waves per SIMD the backward is compiled for (register budget 512 / n).
 #ifndef MOC_BWD_MIN_WAVES
-#define MOC_BWD_MIN_WAVES 1
+#define MOC_BWD_MIN_WAVES 2
 #endif
 
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
@@ -630,23 +630,24 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         }
       }
 
+      // alpha^T operands of the dbasis MFMA (zero for rows that are not this
+      // super-block's own): at[b][kc][v] = alpha[trun + 4b + v, 16kc + j]
+      Op at[NB][KC];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          E e4[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = R * q + 4 * b + v;
+            e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
+          }
+          at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+        }
       // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        // alpha^T operands (zero for rows that are not this super-block's own)
-        Op at[NB][KC];
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int kc = 0; kc < KC; ++kc) {
-            E e4[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              const int row = R * q + 4 * b + v;
-              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
-            }
-            at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
-          }
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           E mv[NP][4][NC];
@@ -688,8 +689,13 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         wave_lds_sync();
       }
     };
+#ifdef MOC_INSPECT_FAST_PATH_ONLY
+    (void)interior;
+    body(std::false_type{});
+#else
     if (interior) body(std::false_type{});
     else body(std::true_type{});
+#endif
 
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb)
