@@ -20,7 +20,8 @@ Functions and the reference lines they follow:
 
 * ``moc_ref``          - ``moc/reference.py:19-33`` (pad, unfold, einsum, sum, SiLU).
 * ``moc_varlen_ref``   - ``moc/reference.py:36-59`` (per-sequence loop over cu_seqlens).
-* ``route``            - ``moc/api.py:383-388`` (router softmax / exp).
+* ``route``            - ``moc/api.py:383-388`` (router softmax / exp; optionally
+                         rounded to the logits' dtype with torch's gradient rule).
 * ``final_state``      - ``moc/api.py:218-227`` (last S tokens as [B, D, S]).
 * ``moc_prefill_ref``  - ``moc/api.py:299-309`` (prepend the cache, drop its rows).
 * ``moc_step_ref``     - ``moc/kernels.py:487-550`` (decode: read slots 1..S-1 plus x,
@@ -97,13 +98,40 @@ def moc_varlen_ref(x: torch.Tensor, alpha: torch.Tensor, basis: torch.Tensor,
     return out[None] if batched else out
 
 
-def route(logits: torch.Tensor, router_activation: str) -> torch.Tensor:
-    """Router activation of moc/api.py:383-388 (softmax over K, or exp)."""
+class _RoundedRoute(torch.autograd.Function):
+    """Router activation whose output is rounded to ``dtype`` and whose
+    backward uses that rounded output, as torch's softmax / exp backward does
+    for a low-precision tensor (they differentiate through the saved result)."""
+
+    @staticmethod
+    def forward(ctx, logits, router_activation, dtype):
+        a = route(logits, router_activation).to(dtype).to(logits.dtype)
+        ctx.save_for_backward(a)
+        ctx.softmax = router_activation == "softmax"
+        return a
+
+    @staticmethod
+    def backward(ctx, g):
+        (a,) = ctx.saved_tensors
+        if ctx.softmax:
+            return a * (g - (a * g).sum(-1, keepdim=True)), None, None
+        return a * g, None, None
+
+
+def route(logits: torch.Tensor, router_activation: str,
+          out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Router activation of moc/api.py:383-388 (softmax over K, or exp).
+
+    With ``out_dtype`` the result is rounded to that dtype (the dtype the
+    router's logits have in the module) and the gradient is formed from the
+    rounded result, like torch's own softmax / exp on such a tensor."""
+    if router_activation not in ("softmax", "exp"):
+        raise ValueError(f"unsupported router activation: {router_activation}")
+    if out_dtype is not None:
+        return _RoundedRoute.apply(logits, router_activation, out_dtype)
     if router_activation == "softmax":
         return torch.softmax(logits, dim=-1)
-    if router_activation == "exp":
-        return torch.exp(logits)
-    raise ValueError(f"unsupported router activation: {router_activation}")
+    return torch.exp(logits)
 
 
 def final_state(x: torch.Tensor, cache: torch.Tensor | None, S: int) -> torch.Tensor:

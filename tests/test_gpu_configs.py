@@ -17,7 +17,7 @@ import torch
 import moc
 from moc import MoC, moc_triton
 from oracle import moc_oracle as O
-from tests._parity import assert_close, gen, randn, round_grad_like, round_like
+from tests._parity import assert_close, gen, randn
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -33,20 +33,23 @@ def _layer(D, Z, K, S, act, route, init_std, dtype, seed=0):
 
 
 def _oracle_layer(m, x, z, dy, route, act, cu=None):
-    """fp32 oracle on the GPU for the layer: returns y and grads (x, z, router, basis)."""
-    dtype = x.dtype
+    """The layer with the MoC op replaced by the fp32 oracle: the router GEMM is
+    the same torch op the module runs (module dtype, on the GPU), the router
+    activation is rounded to the logits' dtype with torch's gradient rule, and
+    the oracle's d(logits) is cast back to that dtype for the GEMM's backward.
+    Returns y and the gradients of x, z, router, basis."""
+    lz = z.detach().requires_grad_()
+    lr = m.router.detach().requires_grad_()
+    logits = torch.nn.functional.linear(lz, lr)
     rx = x.detach().float().requires_grad_()
-    rz = z.detach().float().requires_grad_()
-    rr = m.router.detach().float().requires_grad_()
     rb = m.conv_bases.detach().float().requires_grad_()
-    logits = round_grad_like(round_like(torch.nn.functional.linear(rz, rr), dtype), dtype)
-    alpha = round_like(O.route(logits, route), dtype)
+    alpha = O.route(logits.float(), route, out_dtype=logits.dtype)
     if cu is None:
         y = O.moc_ref(rx, alpha, rb, act)
     else:
         y = O.moc_varlen_ref(rx, alpha, rb, cu, act)
     y.backward(dy.float())
-    return y.detach(), rx.grad, rz.grad, rr.grad, rb.grad
+    return y.detach(), rx.grad, lz.grad, lr.grad, rb.grad
 
 
 def _hip_layer(m, x, z, dy, **kw):
@@ -82,9 +85,7 @@ def test_config1_cpu_reference_shape_fp32():
     z = randn(g, 2, 512, 256).to(DEV)
     dy = randn(g, 2, 512, 256).to(DEV)
     got = _hip_layer(m, x, z, dy)
-    m_cpu = MoC(256, 256, 4, 4)
-    m_cpu.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()})
-    ref = _oracle_layer(m_cpu, x.cpu(), z.cpu(), dy.cpu(), "softmax", None)
+    ref = _oracle_layer(m, x, z, dy, "softmax", None)
     for n, a, b in zip(NAMES, got, ref):
         assert_close(n, a, b, torch.float32)
 
@@ -123,7 +124,7 @@ def test_config3_varlen_layer():
     dy = randn(g, 32768, 4096).to(DEV, torch.bfloat16)
     kw = dict(cu_seqlens=cu, max_seqlen=max(lengths))
     got = _hip_layer(m, x, z, dy, **kw)
-    ref = _oracle_layer(m, x, z, dy, "exp", None, cu=cu.cpu())
+    ref = _oracle_layer(m, x, z, dy, "exp", None, cu=cu)
     for n, a, b in zip(NAMES, got, ref):
         assert_close(n, a, b, torch.bfloat16)
 
@@ -199,8 +200,7 @@ def test_config4_decode():
     assert torch.equal(cache, x[:, -S:].transpose(1, 2))
     rows = torch.arange(0, B, 37, device=DEV)
     with torch.no_grad():
-        rx = x[rows].float()
-        logits = torch.nn.functional.linear(z[rows].float(), m.router.float()).bfloat16().float()
-        alpha = O.route(logits, "softmax").bfloat16().float()
-        full = O.moc_ref(rx, alpha, m.conv_bases.float(), "silu")
+        logits = torch.nn.functional.linear(z[rows], m.router)
+        alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
+        full = O.moc_ref(x[rows].float(), alpha, m.conv_bases.float(), "silu")
     assert_close("decode y", y_steps[rows], full[:, P:], torch.bfloat16)

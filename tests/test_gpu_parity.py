@@ -18,7 +18,7 @@ import torch
 import moc
 from moc import MoC, moc_triton
 from oracle import moc_oracle as O
-from tests._parity import assert_close, gen, randn, round_grad_like, round_like
+from tests._parity import assert_close, gen, randn
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -159,16 +159,17 @@ def test_module_routed_fwd_bwd(route, act, dtype):
     y, _ = m(x, z)
     y.backward(dy)
 
+    # oracle layer: the module's own router GEMM (same dtype, on the GPU), the
+    # router activation rounded like torch's, the MoC op by the CPU oracle
+    lz = z.detach().requires_grad_()
+    lr = m.router.detach().requires_grad_()
+    logits = torch.nn.functional.linear(lz, lr)
     rx = x.detach().float().cpu().requires_grad_()
-    rz = z.detach().float().cpu().requires_grad_()
-    rr = m.router.detach().float().cpu().requires_grad_()
     rb = m.conv_bases.detach().float().cpu().requires_grad_()
-    # torch's GPU router GEMM returns logits in the module dtype, and the router
-    # activation output has the logits' dtype: round both, keep the gradients
-    logits = round_grad_like(round_like(torch.nn.functional.linear(rz, rr), dtype), dtype)
-    alpha = round_like(O.route(logits, route), dtype)
+    alpha = O.route(logits.float().cpu(), route, out_dtype=dtype)
     ry = O.moc_ref(rx, alpha, rb, act)
     ry.backward(dy.float().cpu())
+    rz, rr = lz, lr
     assert_close("y", y, ry, dtype)
     assert_close("dx", x.grad, rx.grad, dtype)
     assert_close("dz", z.grad, rz.grad, dtype)
@@ -334,10 +335,10 @@ def test_module_varlen_routed():
     y, st = m(x, z, cu_seqlens=cu, max_seqlen=31)
     assert st is None
     y.sum().backward()
+    rz = z.detach().requires_grad_()
+    rr = m.router.detach().requires_grad_()
     rx = x.detach().cpu().requires_grad_()
-    rz = z.detach().cpu().requires_grad_()
-    rr = m.router.detach().cpu().requires_grad_()
-    ry = O.moc_varlen_ref(rx, O.route(torch.nn.functional.linear(rz, rr), "exp"),
+    ry = O.moc_varlen_ref(rx, O.route(torch.nn.functional.linear(rz, rr).cpu(), "exp"),
                           m.conv_bases.detach().cpu(), cu.cpu())
     ry.sum().backward()
     assert_close("y", y, ry, torch.float32)
@@ -366,7 +367,7 @@ def test_routed_function_dlogits(route, dtype):
     rx = x.float().cpu().requires_grad_()
     rl = lg.float().cpu().requires_grad_()
     rb = b.float().cpu().requires_grad_()
-    ry = O.moc_ref(rx, round_like(O.route(rl, route), dtype), rb, "silu")
+    ry = O.moc_ref(rx, O.route(rl, route, out_dtype=dtype), rb, "silu")
     ry.backward(dy.float().cpu())
     assert_close("y", y, ry, dtype)
     assert_close("dx", xx.grad, rx.grad, dtype)

@@ -177,6 +177,26 @@ def test_route():
         O.route(lg, "relu")
 
 
+@pytest.mark.parametrize("act", ["softmax", "exp"])
+def test_rounded_route_matches_torch_low_precision_autograd(act):
+    # torch's own softmax / exp on a bf16 tensor: bf16 output, gradient formed
+    # from that output; the oracle's rounded route must reproduce both.
+    lg = _rand(6, 8, seed=47, dtype=torch.float32, scale=2.0)
+    g = _rand(6, 8, seed=48, dtype=torch.float32)
+    lb = lg.bfloat16().requires_grad_()
+    ab = torch.softmax(lb, -1) if act == "softmax" else torch.exp(lb)
+    ab.backward(g.bfloat16())
+    lf = lg.bfloat16().float().requires_grad_()
+    af = O.route(lf, act, out_dtype=torch.bfloat16)
+    af.backward(g.bfloat16().float())
+    torch.testing.assert_close(af, ab.float(), rtol=2 ** -7, atol=1e-6)
+    torch.testing.assert_close(lf.grad, lb.grad.float(), rtol=2 ** -6, atol=1e-3 * lf.grad.abs().max().item())
+    # in fp32 the rounded route is the plain route, gradient included
+    l64 = _rand(5, 7, seed=49).requires_grad_()
+    assert torch.autograd.gradcheck(lambda t: O.route(t, act, out_dtype=torch.float64), (l64,))
+    torch.testing.assert_close(O.route(l64, act, out_dtype=torch.float64), O.route(l64, act))
+
+
 @pytest.mark.parametrize("S", [1, 2, 4])
 def test_decode_steps_match_full_forward_and_cache_is_last_inputs(S):
     B, T, D, K = 2, 9, 5, 3
