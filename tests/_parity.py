@@ -17,9 +17,11 @@ TOL = {
 }
 
 
-def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype) -> None:
+def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.dtype,
+                 extra: torch.Tensor | None = None) -> None:
     """Check ``got`` against the fp32 oracle result ``ref``.  ``dtype`` is the
-    compute (x) dtype; a result stored in a 16-bit dtype is held to the bf16 rule."""
+    compute (x) dtype; a result stored in a 16-bit dtype is held to the bf16 rule.
+    ``extra`` adds an elementwise absolute allowance (see ``ulp_allowance``)."""
     if got.dtype in (torch.bfloat16, torch.float16):
         dtype = torch.bfloat16
     got = got.detach().float().cpu()
@@ -30,6 +32,8 @@ def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.d
     rms = ref.pow(2).mean().sqrt().item() if ref.numel() else 0.0
     err = (got - ref).abs()
     bound = a_rms * rms + r_rel * ref.abs() + 1e-30
+    if extra is not None:
+        bound = bound + extra.detach().float().cpu().reshape(bound.shape)
     bad = err > bound
     if bad.any():
         i = int(torch.argmax((err / bound).flatten()))
@@ -37,6 +41,22 @@ def assert_close(name: str, got: torch.Tensor, ref: torch.Tensor, dtype: torch.d
             f"{name} ({dtype}): {int(bad.sum())}/{err.numel()} elements out of tolerance; "
             f"worst at flat {i}: got {got.flatten()[i].item():.6g} ref {ref.flatten()[i].item():.6g} "
             f"(max abs err {err.max().item():.3g}, rms(ref) {rms:.3g})")
+
+
+def bf16_ulp(t: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |t| (8 significant bits)."""
+    _, e = torch.frexp(t.float())
+    return torch.where(t == 0, torch.zeros_like(t, dtype=torch.float32),
+                       torch.ldexp(torch.ones_like(t, dtype=torch.float32), e - 8))
+
+
+def ulp_allowance(d_inter: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """Allowance for a result formed as (bf16 intermediate) @ weight, where the
+    kernel's and the oracle's intermediate may round to neighbouring bf16
+    values: one ulp of each intermediate entry, propagated through |weight|.
+    d_inter [..., K] (the oracle's fp32 intermediate), weight [K, M]."""
+    u = bf16_ulp(d_inter.detach()).reshape(-1, d_inter.shape[-1])
+    return (u @ weight.detach().float().abs()).reshape(*d_inter.shape[:-1], weight.shape[-1])
 
 
 def round_like(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
