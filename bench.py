@@ -35,6 +35,10 @@ import torch  # noqa: E402
 METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/step"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
+# HBM bytes per launch of the backward stage-1 kernel at CFG, from rocprofv3
+# FETCH_SIZE + WRITE_SIZE runs scaled by a copy kernel of known size; None until
+# measured for the current kernel
+TRAFFIC_BWD = None
 DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
 
 
@@ -93,8 +97,60 @@ def bench_layer(dev, steps, warmup):
     return time_region(step, steps, warmup)
 
 
+class _HipEvents:
+    """hipEvent_t pairs from libamdhip64 (ctypes), for the profiling hook of
+    libmoc_hip.so (moc_profile_events): times one kernel on its own stream."""
+
+    def __init__(self, n):
+        import ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float),
+                                                 ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.pairs = []
+        for _ in range(n):
+            a, b = ctypes.c_void_p(), ctypes.c_void_p()
+            assert self.hip.hipEventCreate(ctypes.byref(a)) == 0
+            assert self.hip.hipEventCreate(ctypes.byref(b)) == 0
+            self.pairs.append((a, b))
+
+    def total_ms(self):
+        import ctypes
+        tot = 0.0
+        for a, b in self.pairs:
+            ms = ctypes.c_float()
+            assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+            tot += ms.value
+        return tot
+
+    def close(self):
+        for a, b in self.pairs:
+            self.hip.hipEventDestroy(a)
+            self.hip.hipEventDestroy(b)
+
+
+def time_kernel(fn, steps, warmup):
+    """Average duration (ms) of the main kernel of the C-ABI call fn()."""
+    from moc import _lib
+    L = _lib.lib()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = _HipEvents(steps)
+    for a, b in ev.pairs:
+        L.moc_profile_events(a, b)
+        fn()
+    L.moc_profile_events(None, None)
+    torch.cuda.synchronize()
+    ms = ev.total_ms() / steps
+    ev.close()
+    return ms
+
+
 def bench_entries(dev, steps, warmup):
-    """Forward and backward C-ABI entries alone, on the layer's logits."""
+    """Forward and backward C-ABI entries alone, on the layer's logits:
+    (entry ms fwd, entry ms bwd, main-kernel ms fwd, main-kernel ms bwd)."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX
     m, x, z = build_layer(dev)
@@ -107,7 +163,8 @@ def bench_entries(dev, steps, warmup):
                                      routing=ROUTE_SOFTMAX)
     bwd = lambda: ops.launch_backward(xd, logits, basis, dy, activation_flag=1,  # noqa: E731
                                       need_x=True, routing=ROUTE_SOFTMAX)
-    return time_region(fwd, steps, warmup), time_region(bwd, steps, warmup)
+    return (time_region(fwd, steps, warmup), time_region(bwd, steps, warmup),
+            time_kernel(fwd, steps, warmup), time_kernel(bwd, steps, warmup))
 
 
 def bench_decode(dev):
@@ -224,11 +281,15 @@ def main():
     D, K, S = CFG["D"], CFG["K"], CFG["S"]
 
     ms = bench_layer(dev, args.steps, args.warmup)
-    t_fwd, t_bwd = bench_entries(dev, args.steps, args.warmup)
+    t_fwd, t_bwd, k_fwd, k_bwd = bench_entries(dev, args.steps, args.warmup)
     fb, bb = bytes_fwd(N, D, K, S), bytes_bwd(N, D, K, S)
     roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / 2.5e15)
                + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / 2.5e15)) * 1e6
-    achieved = bb / (t_bwd * 1e-3)
+    # dominant kernel: the fused backward stage 1; its algorithmic bytes are x, dy
+    # and dx, the routing weights and the basis (dalpha / dbasis leave it as
+    # partial sums that the stage-2 reduction turns into the outputs)
+    kb = 3 * N * D * 2 + N * K * 2 + K * S * D * 2
+    achieved = kb / (k_bwd * 1e-3)
     out = {
         "metric": METRIC,
         "value": round(N / (ms * 1e-3) / 1e6, 3),
@@ -245,11 +306,14 @@ def main():
         "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[1]", "B": CFG["B"],
                    "T": CFG["T"], "D": D, "z_dim": CFG["Z"], "K": K, "S": S,
                    "activation": "silu", "routing": "softmax", "loss": "y.sum()"},
-        "roofline": {"bound": "hbm", "kernel": "moc_backward",
+        "roofline": {"bound": "hbm", "kernel": "moc::mfma::bwd_kernel (fused backward stage 1)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
-                     "traffic": None, "algorithmic_bytes": bb},
+                     "traffic": TRAFFIC_BWD, "algorithmic_bytes": kb,
+                     "kernel_us": round(k_bwd * 1e3, 2)},
         "kernel_scope": {"fwd_us": round(t_fwd * 1e3, 2), "bwd_us": round(t_bwd * 1e3, 2),
+                         "fwd_kernel_us": round(k_fwd * 1e3, 2),
+                         "fwd_kernel_GBps": round(fb / (k_fwd * 1e-3) / 1e9, 1),
                          "mtok_s": round(N / ((t_fwd + t_bwd) * 1e-3) / 1e6, 3),
                          "fwd_GBps": round(fb / (t_fwd * 1e-3) / 1e9, 1),
                          "bwd_GBps": round(bb / (t_bwd * 1e-3) / 1e9, 1),

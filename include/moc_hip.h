@@ -132,6 +132,16 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
                int x_dtype, int alpha_dtype, int basis_dtype,
                int activation, int routing, void* stream);
 
+/*
+ * Profiling aid; it has no counterpart in the reference.  While set (non-NULL
+ * hipEvent_t handles), moc_forward / moc_backward record `start_event` right
+ * before and `stop_event` right after their main kernel (the fused forward,
+ * resp. the fused backward stage 1) on their stream, so a caller can time that
+ * kernel alone with hipEventElapsedTime.  NULL, NULL switches it off.
+ * Thread-local; returns 0.
+ */
+int moc_profile_events(void* start_event, void* stop_event);
+
 #ifdef __cplusplus
 }
 #endif

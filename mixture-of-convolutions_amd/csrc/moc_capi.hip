@@ -13,6 +13,8 @@
 namespace {
 
 thread_local char g_err[512] = "";
+thread_local hipEvent_t g_prof_start = nullptr;
+thread_local hipEvent_t g_prof_stop = nullptr;
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -95,6 +97,8 @@ moc::Problem make_problem(const void* cu, int cu64, int64_t n_seqs, int64_t n_to
   p.b_dt = b_dt;
   p.activation = activation;
   p.routing = routing;
+  p.prof_start = g_prof_start;
+  p.prof_stop = g_prof_stop;
   return p;
 }
 
@@ -137,6 +141,12 @@ int moc_abi_version(void) { return 1; }
 
 const char* moc_last_error(void) { return g_err; }
 
+int moc_profile_events(void* start_event, void* stop_event) {
+  g_prof_start = static_cast<hipEvent_t>(start_event);
+  g_prof_stop = static_cast<hipEvent_t>(stop_event);
+  return MOC_OK;
+}
+
 size_t moc_forward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                    int64_t kernel_size, int x_dtype, int routing) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
@@ -172,7 +182,9 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
   float* a_r = cv.take<float>(size_t(n_tokens * k));
   float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
   moc::launch_prep(p, alpha, basis, a_r, basis_c, st);
+  moc::prof_begin(p, st);
   moc::launch_forward_generic(p, x, a_r, basis_c, y, st);
+  moc::prof_end(p, st);
   return hip_status("moc_forward launch");
 }
 
@@ -216,7 +228,9 @@ int moc_backward(const void* x, const void* alpha, const void* basis, const void
   float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
   float* scratch = cv.take<float>(moc::generic_bwd_scratch_floats(p));
   moc::launch_prep(p, alpha, basis, a_r, basis_c, st);
+  moc::prof_begin(p, st);
   moc::launch_backward_generic(p, x, dy, dx, dalpha, dbasis, a_r, basis_c, scratch, st);
+  moc::prof_end(p, st);
   return hip_status("moc_backward launch");
 }
 

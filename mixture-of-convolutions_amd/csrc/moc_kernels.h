@@ -16,7 +16,17 @@ struct Problem {
   int x_dt, a_dt, b_dt;
   int activation;    // 0 = none, 1 = SiLU
   int routing;       // Route
+  hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set
+  hipEvent_t prof_stop = nullptr;
 };
+
+// Record p.prof_start / p.prof_stop around the main kernel of a call.
+inline void prof_begin(const Problem& p, hipStream_t st) {
+  if (p.prof_start) (void)hipEventRecord(p.prof_start, st);
+}
+inline void prof_end(const Problem& p, hipStream_t st) {
+  if (p.prof_stop) (void)hipEventRecord(p.prof_stop, st);
+}
 
 // generic path (moc_generic.hip)
 void launch_prep(const Problem& p, const void* alpha, const void* basis, float* a_r,

@@ -217,6 +217,7 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
   launch_prep(p, pl, alpha, basis, ws, st);
   const void* a_c = ws + pl.off_ac;
   const void* b_c = ws + pl.off_bc;
+  prof_begin(p, st);
   switch (p.S) {
     case 2: launch_fwd<2>(p, x, a_c, b_c, y, st); break;
     case 3: launch_fwd<3>(p, x, a_c, b_c, y, st); break;
@@ -224,6 +225,7 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
     case 8: launch_fwd<8>(p, x, a_c, b_c, y, st); break;
     default: break;
   }
+  prof_end(p, st);
 }
 
 void backward(const Problem& p, const void* x, const void* alpha, const void* basis,
@@ -236,6 +238,7 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
   const void* b_c = ws + pl.off_bc;
   float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
   float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
+  prof_begin(p, st);
   switch (p.S) {
     case 2: launch_bwd<2>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     case 3: launch_bwd<3>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
@@ -243,6 +246,7 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     default: break;
   }
+  prof_end(p, st);
   const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
   const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
   const float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<const float*>(ws + pl.off_ar)

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "moc_backward_workspace_bytes",
     "moc_backward",
     "moc_update",
+    "moc_profile_events",
 )
 
 _lock = threading.Lock()
@@ -78,6 +79,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i, _i, _p,                # activation, routing, stream
     ]
     lib.moc_update.restype = _i
+    lib.moc_profile_events.argtypes = [_p, _p]
+    lib.moc_profile_events.restype = _i
 
 
 def lib() -> ctypes.CDLL:
