@@ -35,10 +35,12 @@ import torch  # noqa: E402
 METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/step"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
-# HBM bytes per launch of the backward stage-1 kernel at CFG, from rocprofv3
-# FETCH_SIZE + WRITE_SIZE runs scaled by a copy kernel of known size; None until
-# measured for the current kernel
-TRAFFIC_BWD = None
+# HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
+# FETCH_SIZE (69153 KiB) and WRITE_SIZE (98378 KiB) per dispatch of
+# `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
+# 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
+# 131072 KiB -> factor 1.0)
+TRAFFIC_BWD = 242_338_988
 DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
 
 
@@ -148,9 +150,9 @@ def time_kernel(fn, steps, warmup):
     return ms
 
 
-def bench_entries(dev, steps, warmup):
-    """Forward and backward C-ABI entries alone, on the layer's logits:
-    (entry ms fwd, entry ms bwd, main-kernel ms fwd, main-kernel ms bwd)."""
+def entry_calls(dev):
+    """The forward and backward C-ABI entries on the layer's logits, as two
+    zero-argument callables (fwd, bwd)."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX
     m, x, z = build_layer(dev)
@@ -163,8 +165,34 @@ def bench_entries(dev, steps, warmup):
                                      routing=ROUTE_SOFTMAX)
     bwd = lambda: ops.launch_backward(xd, logits, basis, dy, activation_flag=1,  # noqa: E731
                                       need_x=True, routing=ROUTE_SOFTMAX)
+    return fwd, bwd
+
+
+def bench_entries(dev, steps, warmup):
+    """Forward and backward C-ABI entries alone, on the layer's logits:
+    (entry ms fwd, entry ms bwd, main-kernel ms fwd, main-kernel ms bwd)."""
+    fwd, bwd = entry_calls(dev)
     return (time_region(fwd, steps, warmup), time_region(bwd, steps, warmup),
             time_kernel(fwd, steps, warmup), time_kernel(bwd, steps, warmup))
+
+
+def counter_run(dev, which, reps=3):
+    """A short program for hardware-counter passes (rocprofv3 --pmc): `reps`
+    calls of one entry at the headline config, or of a bf16 copy of 128 MiB
+    (`copy`), the kernel of known traffic that calibrates FETCH_SIZE and
+    WRITE_SIZE."""
+    if which == "copy":
+        a = torch.randn(64 * 1024 * 1024, device=dev).bfloat16()
+        b = torch.empty_like(a)
+        fn = lambda: b.copy_(a)  # noqa: E731
+    else:
+        fwd, bwd = entry_calls(dev)
+        fn = fwd if which == "fwd" else bwd
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    print(f"counter run: {reps} x {which}", flush=True)
 
 
 def bench_decode(dev):
@@ -268,6 +296,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--counters", choices=("fwd", "bwd", "copy"), default=None,
+                    help="only run 3 calls of one entry (or the calibration copy) "
+                         "for a rocprofv3 --pmc pass; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -277,6 +308,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.counters:
+        counter_run(dev, args.counters)
+        return
     N = CFG["B"] * CFG["T"]
     D, K, S = CFG["D"], CFG["K"], CFG["S"]
 
