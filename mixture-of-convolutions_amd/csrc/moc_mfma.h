@@ -350,6 +350,59 @@ struct MSplit<false> {
   static __device__ __forceinline__ void split(float m, float (&e)[1]) { e[0] = m; }
 };
 
+// Four bf16 in MFMA operand order from the upper halves of four fp32 bit patterns
+// (v_perm_b32 picks bytes 2-3 of each source).
+__device__ __forceinline__ s16x4 pack4_hi(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 w = {__builtin_amdgcn_perm(b, a, 0x07060302u), __builtin_amdgcn_perm(d, c, 0x07060302u)};
+  return __builtin_bit_cast(s16x4, w);
+}
+
+// Four fp32 rounded to bf16 (nearest even) in MFMA operand order.
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+__device__ __forceinline__ s16x4 pack4_bf16(float a, float b, float c, float d) {
+  typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 w = {pack2_bf16(a, b), pack2_bf16(c, d)};
+  return __builtin_bit_cast(s16x4, w);
+}
+
+// Transposable LDS tile of one wave's m values for the dalpha MFMA (bf16).
+//
+// The writer lane (j, q) holds, per token block b and channel c, the 4 values of
+// channel NC j + c at the super-block tokens 4 g + {0..3}, g = NB q + b: the
+// dbasis operand, stored as one 8-byte slot.  The dalpha A operand wants, in
+// lane i + 16 q', the 4 channels 16 cg + 4 q' + {0..3} of token 16 rb + i.
+// ds_read_b64_tr_b16 returns, in lane i of each 16-lane group, element i % 4 of
+// the slots read by lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4 of the group,
+// so reader lane 4 e + a of group q' reads the slot of channel 16 cg + 4 q' + e,
+// token group 4 rb + a.
+// Slot (channel NC jj + c, token group g) lives at (c GB + g) * 32 + jj + 2 c +
+// 4 (g & 3): within each 16-lane group both the writer (16 channels) and the
+// reader (4 channels x 4 token groups) touch 16 distinct slots modulo 32, and
+// both addresses are a per-lane base plus a compile-time offset.
+template <int NB, int NC>
+struct TrTile {
+  static_assert(NC == 2, "slot layout written for two channels per lane");
+  static constexpr int GB = 4 * NB;          // token groups of 4 per super-block
+  static constexpr int kSlots = NC * GB * 32;
+  static __device__ __forceinline__ int wslot(int j, int q, int b, int c) {
+    return (NB * q) * 32 + j + 4 * ((NB * q) & 3) + (c * GB + b) * 32 + 2 * c + 4 * b;
+  }
+  static __device__ __forceinline__ int rslot(int i, int q, int rb, int cg) {
+    const int e = i >> 2, a = i & 3, c = e & 1;
+    return (c * GB + a) * 32 + 2 * q + (e >> 1) + 2 * c + 4 * a + 4 * rb * 32 + 8 * cg;
+  }
+  template <typename T>
+  static __device__ __forceinline__ s16x4 read(const T* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(const_cast<T*>(p)));
+  }
+};
+
 // Wave-local ordering of LDS traffic: LDS operations of one wave complete in
 // issue order; this keeps the compiler from moving them across the point.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -400,8 +453,13 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   constexpr int MROW = CW + 4;        // padded LDS row of one m tile (elements)
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
 
-  __shared__ E a_lds[2][AROWS][KP];
-  __shared__ E m_lds[WPG][NP][TB][MROW];
+  // m tiles for the dalpha product.  fp32: [token][channel] tiles read as rows.
+  // bf16: the dbasis operand of a (token group of 4, channel) is stored as is
+  // (8 bytes) and read back transposed with ds_read_b64_tr_b16 (see TrTile).
+  using TT = TrTile<NB, NC>;
+  __shared__ __align__(16) E a_lds[2][AROWS][KP];
+  __shared__ __align__(16) E m_lds[BF ? 1 : WPG][NP][BF ? 1 : TB][BF ? 1 : MROW];
+  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][NP][BF ? TT::kSlots : 1];
   __shared__ float da_lds[2][WPG][NB][KC][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
@@ -633,19 +691,79 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       // alpha^T operands of the dbasis MFMA (zero for rows that are not this
       // super-block's own): at[b][kc][v] = alpha[trun + 4b + v, 16kc + j]
       Op at[NB][KC];
+      if constexpr (BF) {
+        // transposed read: supplier lane 4e + a of each 16-lane group holds the
+        // 4 routing weights 16kc + 4a.. of row R q + 4b + e (ds_read_b64_tr_b16)
+        const int own_rows = static_cast<int>(own_end - t0);
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
+        for (int b = 0; b < NB; ++b) {
+          const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
+          const uint64_t keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          E e4[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int row = R * q + 4 * b + v;
-            e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
+          for (int kc = 0; kc < KC; ++kc) {
+            const Op v = TT::read(&a_lds[buf][R * q + 4 * b + (j >> 2)][16 * kc + 4 * (j & 3)]);
+            at[b][kc] = __builtin_bit_cast(Op, __builtin_bit_cast(uint64_t, v) & keep);
           }
-          at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
         }
+      } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc) {
+            E e4[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              const int row = R * q + 4 * b + v;
+              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
+            }
+            at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+          }
+      }
       // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
+      if constexpr (BF) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+              // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
+              uint32_t hb[4];
+              float lo[4];
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int r = 4 * b + v;
+                const bool on = !MASK || ((ok[r] >> s) & 1u);
+                const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                hb[v] = __float_as_uint(mval) & 0xffff0000u;
+                lo[v] = mval - __uint_as_float(hb[v]);
+              }
+              const Op mh = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
+              const Op ml = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
+              m_tr[wave][0][TT::wslot(j, q, b, c)] = mh;
+              m_tr[wave][1][TT::wslot(j, q, b, c)] = ml;
+#pragma unroll
+              for (int kc = 0; kc < KC; ++kc) {
+                dbacc[c][s][kc] = C::mma(mh, at[b][kc], dbacc[c][s][kc]);
+                dbacc[c][s][kc] = C::mma(ml, at[b][kc], dbacc[c][s][kc]);
+              }
+            }
+          }
+          wave_lds_sync();
+          // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
+#pragma unroll
+          for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+            for (int h = 0; h < NP; ++h)
+#pragma unroll
+              for (int cg = 0; cg < NC; ++cg) {
+                const Op am = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
+#pragma unroll
+                for (int kc = 0; kc < KC; ++kc) dacc[rb][kc] = C::mma(am, bda[s][cg][kc], dacc[rb][kc]);
+              }
+          wave_lds_sync();
+        }
+      } else {
 #pragma unroll
       for (int s = 0; s < S; ++s) {
 #pragma unroll
@@ -687,6 +805,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
               for (int kc = 0; kc < KC; ++kc) dacc[rb][kc] = C::mma(am, bda[s][cg][kc], dacc[rb][kc]);
             }
         wave_lds_sync();
+      }
       }
     };
 #ifdef MOC_INSPECT_FAST_PATH_ONLY
