@@ -370,6 +370,17 @@ __device__ __forceinline__ s16x4 pack4_bf16(float a, float b, float c, float d) 
   return __builtin_bit_cast(s16x4, w);
 }
 
+// v_mfma_f32_16x16x32_bf16 on operand pairs: lane entries a0 ++ a1 against
+// b0 ++ b1, i.e. two 16x16x16 products over disjoint halves of the contraction.
+__device__ __forceinline__ f32x4 mma32(s16x4 a0, s16x4 a1, s16x4 b0, s16x4 b1, f32x4 c) {
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+  const s16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
 // Transposable LDS tile of one wave's m values for the dalpha MFMA (bf16).
 //
 // The writer lane (j, q) holds, per token block b and channel c, the 4 values of
@@ -380,21 +391,22 @@ __device__ __forceinline__ s16x4 pack4_bf16(float a, float b, float c, float d) 
 // the slots read by lanes i / 4, 4 + i / 4, 8 + i / 4, 12 + i / 4 of the group,
 // so reader lane 4 e + a of group q' reads the slot of channel 16 cg + 4 q' + e,
 // token group 4 rb + a.
-// Slot (channel NC jj + c, token group g) lives at (c GB + g) * 32 + jj + 2 c +
-// 4 (g & 3): within each 16-lane group both the writer (16 channels) and the
-// reader (4 channels x 4 token groups) touch 16 distinct slots modulo 32, and
-// both addresses are a per-lane base plus a compile-time offset.
+// Slot (channel NC jj + c, token group g) lives at (c GB + g) * 16 +
+// (jj ^ (2 c + 4 (g & 3))): 16 slots (128 bytes) per (c, g), and the 16 lanes
+// of a writer group (16 channels) or of a reader group (4 channels x 4 token
+// groups) touch 16 distinct slots modulo 16.
 template <int NB, int NC>
 struct TrTile {
   static_assert(NC == 2, "slot layout written for two channels per lane");
   static constexpr int GB = 4 * NB;          // token groups of 4 per super-block
-  static constexpr int kSlots = NC * GB * 32;
+  static constexpr int kSlots = NC * GB * 16;
   static __device__ __forceinline__ int wslot(int j, int q, int b, int c) {
-    return (NB * q) * 32 + j + 4 * ((NB * q) & 3) + (c * GB + b) * 32 + 2 * c + 4 * b;
+    const int g = NB * q + b;
+    return (c * GB + g) * 16 + (j ^ (2 * c + 4 * (g & 3)));
   }
   static __device__ __forceinline__ int rslot(int i, int q, int rb, int cg) {
     const int e = i >> 2, a = i & 3, c = e & 1;
-    return (c * GB + a) * 32 + 2 * q + (e >> 1) + 2 * c + 4 * a + 4 * rb * 32 + 8 * cg;
+    return (c * GB + a) * 16 + ((8 * cg + 2 * q + (e >> 1)) ^ (2 * c + 4 * a)) + 64 * rb;
   }
   template <typename T>
   static __device__ __forceinline__ s16x4 read(const T* p) {
@@ -402,6 +414,9 @@ struct TrTile {
         (__attribute__((address_space(3))) s16x4*)(const_cast<T*>(p)));
   }
 };
+
+// MFMA jobs issued ahead of the FMAs that consume them.
+constexpr int kLead = 2;
 
 // Wave-local ordering of LDS traffic: LDS operations of one wave complete in
 // issue order; this keeps the compiler from moving them across the point.
@@ -457,9 +472,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   // bf16: the dbasis operand of a (token group of 4, channel) is stored as is
   // (8 bytes) and read back transposed with ds_read_b64_tr_b16 (see TrTile).
   using TT = TrTile<NB, NC>;
-  __shared__ __align__(16) E a_lds[2][AROWS][KP];
+  // routing-weight rows padded by 4 bf16 (40-byte rows) so that the W operand
+  // reads of the 16 lanes of a group spread over the banks
+  constexpr int AP = BF ? KP + 4 : KP;
+  __shared__ __align__(16) E a_lds[2][AROWS][AP];
   __shared__ __align__(16) E m_lds[BF ? 1 : WPG][NP][BF ? 1 : TB][BF ? 1 : MROW];
-  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][NP][BF ? TT::kSlots : 1];
+  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][2][NP][BF ? TT::kSlots : 1];
   __shared__ float da_lds[2][WPG][NB][KC][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
@@ -486,7 +504,6 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const uint32_t col = static_cast<uint32_t>(dl * ESZ);
   const Buf xb(x + row_lo * D, (row_hi - row_lo) * D * ESZ);
   const Buf dyb(dy + row_lo * D, (row_hi - row_lo) * D * ESZ);
-  const Buf dxb(dx + row_lo * D, (dx != nullptr ? row_hi - row_lo : 0) * D * ESZ);
   const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
 
@@ -535,12 +552,13 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   E dr[R][NC];
   E arw[APER][AVEC];
   auto fetch = [&](int64_t t0) {
-    const int64_t trun = t0 + R * q;
+    // offset of window row w = base + w rb: rows before row_lo wrap to >= 2^31
+    // and load zeros; a lane past the channel axis starts at kOffNone
+    const uint32_t base = row_off(t0 + R * q - (S - 1), row_lo, rb, col, ch_ok);
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      xb.load<NC * ESZ>(row_off(trun - (S - 1) + w, row_lo, rb, col, ch_ok), xr[w]);
+    for (int w = 0; w < W; ++w) xb.load<NC * ESZ>(base + w * rb, xr[w]);
 #pragma unroll
-    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok), dr[r]);
+    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(base + (r + S - 1) * rb, dr[r]);
 #pragma unroll
     for (int i = 0; i < APER; ++i) {
       const int chunk = tid + i * 64 * WPG;
@@ -619,21 +637,28 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int c = 0; c < NC; ++c) p[r][c] = 0.f;
+        // jobs (s, b, c): W block by MFMA, then its 4 FMAs; the MFMA of job
+        // i + kLead is issued before the FMAs of job i to cover its latency
+        constexpr int NJ = S * NB * NC;
+        f32x4 wq[NJ];
+        auto issue = [&](int jb) {
+          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
+          f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
+          for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
+          wq[jb] = w4;
+        };
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
+        for (int jb = 0; jb < kLead && jb < NJ; ++jb) issue(jb);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
+        for (int jb = 0; jb < NJ; ++jb) {
+          if (jb + kLead < NJ) issue(jb + kLead);
+          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
-#pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                const int r = 4 * b + v;
-                if (!MASK || ((ok[r] >> s) & 1u)) p[r][c] = fmaf(xw[r + s][c], w4[v], p[r][c]);
-              }
-            }
+          for (int v = 0; v < 4; ++v) {
+            const int r = 4 * b + v;
+            if (!MASK || ((ok[r] >> s) & 1u)) p[r][c] = fmaf(xw[r + s][c], wq[jb][v], p[r][c]);
+          }
         }
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -660,31 +685,44 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int c = 0; c < NC; ++c) dxa[r][c] = 0.f;
+        constexpr int NJ = S * NB * NC;
+        f32x4 wq[NJ];
+        auto issue = [&](int jb) {
+          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
+          f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
+          for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(S - 1 - s, b, kc), bop[c][s][kc], w4);
+          wq[jb] = w4;
+        };
+#pragma unroll
+        for (int jb = 0; jb < kLead && jb < NJ; ++jb) issue(jb);
+#pragma unroll
+        for (int jb = 0; jb < NJ; ++jb) {
+          if (jb + kLead < NJ) issue(jb + kLead);
+          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           const int off = S - 1 - s;
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(off, b, kc), bop[c][s][kc], w4);
-#pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                const int r = 4 * b + v;
-                const int src = r + off;
-                const float gs = (src < R) ? g[src < R ? src : 0][c] : gf[src >= R ? src - R : 0][c];
-                if (!MASK || ((ok[src] >> s) & 1u)) dxa[r][c] = fmaf(gs, w4[v], dxa[r][c]);
-              }
-            }
+          for (int v = 0; v < 4; ++v) {
+            const int r = 4 * b + v;
+            const int src = r + off;
+            const float gs = (src < R) ? g[src < R ? src : 0][c] : gf[src >= R ? src - R : 0][c];
+            if (!MASK || ((ok[src] >> s) & 1u)) dxa[r][c] = fmaf(gs, wq[jb][v], dxa[r][c]);
+          }
         }
+        // the buffer ends at this super-block's last own row: later rows drop
+        const Buf dxb(dx + row_lo * D, (own_end - row_lo) * D * ESZ);
+        const uint32_t base = row_off(trun, row_lo, rb, col, ch_ok);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           E o[NC];
+          if constexpr (BF && NC == 2) {
+            const uint32_t pk = pack2_bf16(dxa[r][0], dxa[r][1]);
+            __builtin_memcpy(o, &pk, 4);
+          } else {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) o[c] = C::from_f(dxa[r][c]);
-          dxb.store<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok && trun + r < own_end), o);
+            for (int c = 0; c < NC; ++c) o[c] = C::from_f(dxa[r][c]);
+          }
+          dxb.store<NC * ESZ>(base + r * rb, o);
         }
       }
 
@@ -721,48 +759,75 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       }
       // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
       if constexpr (BF) {
+        // both products contract 32 entries per v_mfma_f32_16x16x32_bf16: dbasis
+        // the 8 rows of this lane's run (token blocks b, b+1), dalpha the 32
+        // channels of the wave (channel groups 0, 1); A and B operands list
+        // their entries in the same order
+        static_assert(NB % 2 == 0 && NC == 2, "16x16x32 pairing");
+        // tap s: m_s -> bf16 hi / lo operands -> LDS tile (buffer s & 1) and the
+        // dbasis MFMAs; the dalpha reads of tap s are issued before the m values
+        // of tap s + 1 are computed, so that VALU work covers the LDS latency
+        auto stage_m = [&](int s) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
+          for (int c = 0; c < NC; ++c) {
 #pragma unroll
-          for (int b = 0; b < NB; ++b) {
+            for (int b2 = 0; b2 < NB; b2 += 2) {
+              Op mh[2], ml[2];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
-              uint32_t hb[4];
-              float lo[4];
+              for (int bb = 0; bb < 2; ++bb) {
+                const int b = b2 + bb;
+                // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
+                uint32_t hb[4];
+                float lo[4];
 #pragma unroll
-              for (int v = 0; v < 4; ++v) {
-                const int r = 4 * b + v;
-                const bool on = !MASK || ((ok[r] >> s) & 1u);
-                const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
-                hb[v] = __float_as_uint(mval) & 0xffff0000u;
-                lo[v] = mval - __uint_as_float(hb[v]);
+                for (int v = 0; v < 4; ++v) {
+                  const int r = 4 * b + v;
+                  const bool on = !MASK || ((ok[r] >> s) & 1u);
+                  const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                  hb[v] = __float_as_uint(mval) & 0xffff0000u;
+                  lo[v] = mval - __uint_as_float(hb[v]);
+                }
+                mh[bb] = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
+                ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
+                m_tr[wave][s & 1][0][TT::wslot(j, q, b, c)] = mh[bb];
+                m_tr[wave][s & 1][1][TT::wslot(j, q, b, c)] = ml[bb];
               }
-              const Op mh = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
-              const Op ml = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
-              m_tr[wave][0][TT::wslot(j, q, b, c)] = mh;
-              m_tr[wave][1][TT::wslot(j, q, b, c)] = ml;
 #pragma unroll
               for (int kc = 0; kc < KC; ++kc) {
-                dbacc[c][s][kc] = C::mma(mh, at[b][kc], dbacc[c][s][kc]);
-                dbacc[c][s][kc] = C::mma(ml, at[b][kc], dbacc[c][s][kc]);
+                dbacc[c][s][kc] = mma32(mh[0], mh[1], at[b2][kc], at[b2 + 1][kc], dbacc[c][s][kc]);
+                dbacc[c][s][kc] = mma32(ml[0], ml[1], at[b2][kc], at[b2 + 1][kc], dbacc[c][s][kc]);
               }
             }
           }
+        };
+        stage_m(0);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          // LDS operations of a wave complete in order: the tile of tap s is
+          // written before these reads, and the reads of tap s - 1 from the other
+          // buffer are done before stage_m(s + 1) overwrites it
           wave_lds_sync();
+          Op ra[NB][NP][2];
+#pragma unroll
+          for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+            for (int h = 0; h < NP; ++h)
+#pragma unroll
+              for (int cg = 0; cg < 2; ++cg)
+                ra[rb][h][cg] = TT::read(&m_tr[wave][s & 1][h][TT::rslot(j, q, rb, cg)]);
+          // keep the reads ahead of the next tap's VALU work
+          __builtin_amdgcn_sched_barrier(0);
+          if (s + 1 < S) stage_m(s + 1);
           // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
 #pragma unroll
           for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
             for (int h = 0; h < NP; ++h)
 #pragma unroll
-              for (int cg = 0; cg < NC; ++cg) {
-                const Op am = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
-#pragma unroll
-                for (int kc = 0; kc < KC; ++kc) dacc[rb][kc] = C::mma(am, bda[s][cg][kc], dacc[rb][kc]);
-              }
-          wave_lds_sync();
+              for (int kc = 0; kc < KC; ++kc)
+                dacc[rb][kc] = mma32(ra[rb][h][0], ra[rb][h][1], bda[s][0][kc], bda[s][1][kc], dacc[rb][kc]);
         }
+        wave_lds_sync();
       } else {
 #pragma unroll
       for (int s = 0; s < S; ++s) {
