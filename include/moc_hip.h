@@ -133,6 +133,33 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
                int activation, int routing, void* stream);
 
 /*
+ * Router of the MoC layer: logits = z . router^T, the F.linear(z, router) of
+ * MoC.forward (moc/api.py:383-388) that the reference runs as a library GEMM,
+ * and its backward.  bf16 only; k % 4 == 0, k <= 32, z_dim % 64 == 0 and
+ * n_tokens * z_dim * 2 < 2^31 (moc_router_supported returns 1 for such shapes).
+ *   z      : [n_tokens, z_dim] contiguous
+ *   router : [k, z_dim] contiguous
+ *   logits : [n_tokens, k] (output of the forward)
+ * Accumulation is fp32; each result is rounded to bf16 once.
+ */
+int moc_router_supported(int64_t n_tokens, int64_t z_dim, int64_t k, int dtype);
+int moc_router_forward(const void* z, const void* router, void* logits, int64_t n_tokens,
+                       int64_t z_dim, int64_t k, int dtype, void* stream);
+
+/* Workspace bytes moc_router_backward needs when drouter is requested. */
+size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,
+                                           int dtype);
+
+/*
+ * dz = dlogits . router ([n_tokens, z_dim]) and drouter = dlogits^T . z
+ * ([k, z_dim]); either output may be NULL to skip it.  drouter is reduced in a
+ * fixed order (bitwise reproducible).
+ */
+int moc_router_backward(const void* z, const void* router, const void* dlogits, void* dz,
+                        void* drouter, int64_t n_tokens, int64_t z_dim, int64_t k, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Profiling aid; it has no counterpart in the reference.  While set (non-NULL
  * hipEvent_t handles), moc_forward / moc_backward record `start_event` right
  * before and `stop_event` right after their main kernel (the fused forward,

@@ -250,4 +250,47 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   return hip_status("moc_update launch");
 }
 
+int moc_router_supported(int64_t n_tokens, int64_t z_dim, int64_t k, int dtype) {
+  return moc::router_supported(n_tokens, z_dim, k, dtype) ? 1 : 0;
+}
+
+int moc_router_forward(const void* z, const void* router, void* logits, int64_t n_tokens,
+                       int64_t z_dim, int64_t k, int dtype, void* stream) {
+  g_err[0] = '\0';
+  if (!moc::router_supported(n_tokens, z_dim, k, dtype))
+    return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
+                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
+  if (!z || !router || !logits) return fail(MOC_ERR_ARG, "null tensor pointer");
+  if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
+  moc::router_forward(z, router, logits, n_tokens, z_dim, k, static_cast<hipStream_t>(stream));
+  return hip_status("moc_router_forward launch");
+}
+
+size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,
+                                           int dtype) {
+  if (!moc::router_supported(n_tokens, z_dim, k, dtype)) return 0;
+  return moc::router_backward_workspace(n_tokens, z_dim, k);
+}
+
+int moc_router_backward(const void* z, const void* router, const void* dlogits, void* dz,
+                        void* drouter, int64_t n_tokens, int64_t z_dim, int64_t k, int dtype,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  if (!moc::router_supported(n_tokens, z_dim, k, dtype))
+    return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
+                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
+  if (!router || !dlogits || (drouter && !z)) return fail(MOC_ERR_ARG, "null tensor pointer");
+  if (drouter) {
+    const size_t need = moc::router_backward_workspace(n_tokens, z_dim, k);
+    if (workspace_bytes < need || !workspace)
+      return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                  workspace_bytes);
+  }
+  moc::router_backward(z, router, dlogits, dz, drouter, n_tokens, z_dim, k, workspace,
+                       static_cast<hipStream_t>(stream));
+  return hip_status("moc_router_backward launch");
+}
+
 }  // extern "C"

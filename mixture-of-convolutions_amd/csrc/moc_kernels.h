@@ -54,4 +54,12 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
               hipStream_t st);
 }  // namespace mfma
 
+// router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 32, Z % 64 == 0
+bool router_supported(int64_t N, int64_t Z, int64_t K, int dt);
+size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K);
+void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
+                    hipStream_t st);
+void router_backward(const void* z, const void* r, const void* dl, void* dz, void* dr,
+                     int64_t N, int64_t Z, int64_t K, void* workspace, hipStream_t st);
+
 }  // namespace moc

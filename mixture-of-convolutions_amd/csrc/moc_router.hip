@@ -1,0 +1,345 @@
+// Router GEMMs of the MoC layer (moc/api.py:383-388 of the reference: logits =
+// F.linear(z, router) and its autograd): logits = z . router^T, and in the
+// backward dz = dlogits . router and drouter = dlogits^T . z.
+//
+// All three products have the K (<= 32) routes on one side and the [N, Z]
+// routing input on the other, so they are bound by streaming z (or writing dz)
+// through HBM once.  The kernels read and write [N, Z] with 16-byte accesses and
+// run the products on the matrix cores (v_mfma_f32_16x16x32_bf16, 16x16x16 for
+// dz with K = 16); accumulation is fp32, results are rounded to bf16 once.
+// drouter is reduced in a fixed order (per-range partials, then one sum), so it
+// is bitwise reproducible.  bf16 data only; K % 4 == 0, K <= 32, Z % 64 == 0.
+#include "moc_kernels.h"
+#include "moc_mfma.h"
+
+namespace moc {
+namespace router {
+
+using mfma::Buf;
+using mfma::f32x4;
+using mfma::kOffNone;
+using mfma::s16x4;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x4 load16(const Buf& b, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(b.r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ u32x2 load8(const Buf& b, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(b.r, static_cast<int>(off), 0, 0);
+}
+
+// 16 x 16 x 32 product of 8-element bf16 operands held as 16 bytes.
+__device__ __forceinline__ f32x4 mma8(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// Transposed LDS read (ds_read_b64_tr_b16): lane i of each 16-lane group gets
+// element i % 4 of the 8-byte rows read by lanes i / 4 + {0, 4, 8, 12}.
+__device__ __forceinline__ s16x4 tr_read(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(p)));
+}
+
+// ---------------------------------------------------------------------------
+// logits[t, k] = sum_z z[t, z] router[k, z].  Workgroup: 16 tokens, 4 waves.
+// Wave w sums the 64-wide z chunks c = w, w + 4, ...: lane (i, qq) loads the 16
+// columns 64 c + 16 qq + [0, 16) of token t0 + i (A operand) and of route
+// 16 kc + i (B operand), two MFMAs per chunk.  The 4 partial 16 x KP tiles are
+// summed in LDS in wave order.
+template <int KC>
+__global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restrict__ z,
+                                                         const uint16_t* __restrict__ r,
+                                                         uint16_t* __restrict__ logits,
+                                                         int64_t N, int Z, int K) {
+  constexpr int KP = 16 * KC;
+  __shared__ float red[4][KP][17];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, qq = lane >> 4;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 16;
+  const int64_t rows = (N - t0 < 16) ? N - t0 : 16;
+  // rows past N and routes past K lie outside the buffers and load zeros
+  const Buf zb(z + t0 * Z, rows * Z * 2);
+  const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
+  const uint32_t zrow = static_cast<uint32_t>(i * Z * 2);
+  f32x4 acc[KC];
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc) acc[kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nchunk = Z / 64;
+  // four chunks per step, so that 8 (+ 8 KC) loads per lane are in flight
+  for (int c0 = w; c0 < nchunk; c0 += 16) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c0 + 4 * u;
+      if (c < nchunk) {
+        const uint32_t col = static_cast<uint32_t>((64 * c + 16 * qq) * 2);
+        const u32x4 z0 = load16(zb, zrow + col), z1 = load16(zb, zrow + col + 16);
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
+          const u32x4 r0 = load16(rb, rrow + col), r1 = load16(rb, rrow + col + 16);
+          acc[kc] = mma8(z0, r0, acc[kc]);
+          acc[kc] = mma8(z1, r1, acc[kc]);
+        }
+      }
+    }
+  }
+  // D lane (j, q): route 16 kc + j, tokens 4 q + v
+#pragma unroll
+  for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[w][16 * kc + i][4 * qq + v] = acc[kc][v];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * KP; idx += 256) {
+    const int tok = idx / KP, k = idx % KP;
+    const float s = ((red[0][k][tok] + red[1][k][tok]) + red[2][k][tok]) + red[3][k][tok];
+    if (k < K && tok < rows) logits[(t0 + tok) * K + k] = f32_to_bf16(s);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dz[t, zc] = sum_k dl[t, k] router[k, zc].  A wave owns 64 columns (4 tiles
+// of 16) and walks `bpw` blocks of 16 tokens.  D[zc][t] = router^T . dl^T:
+// A lane (i, qq) holds router[16 kc + 4 qq + {0..3}][zc_i] (kept in registers),
+// B lane (j, qq) holds dl[t_j][16 kc + 4 qq + {0..3}]; the result lane (j, q)
+// holds columns 4 q + {0..3} of token t_j: one 8-byte store.
+template <int KC>
+__global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restrict__ dl,
+                                                        const uint16_t* __restrict__ r,
+                                                        uint16_t* __restrict__ dz, int64_t N,
+                                                        int Z, int K, int bpw) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, qq = lane >> 4;
+  const int zs = (blockIdx.x * 4 + w) * 64;
+  if (zs >= Z) return;  // whole wave; the kernel has no barrier
+  const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
+  const Buf db(dl, N * K * 2);
+  const Buf ob(dz, N * Z * 2);
+  s16x4 aop[4][KC];
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      uint16_t e[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * kc + 4 * qq + v;
+        const uint32_t off = static_cast<uint32_t>((k * Z + zs + 16 * tl + i) * 2);
+        e[v] = __builtin_amdgcn_raw_buffer_load_b16(rb.r, static_cast<int>(off), 0, 0);
+      }
+      aop[tl][kc] = s16x4{static_cast<short>(e[0]), static_cast<short>(e[1]),
+                          static_cast<short>(e[2]), static_cast<short>(e[3])};
+    }
+  const int64_t blk0 = static_cast<int64_t>(blockIdx.y) * bpw;
+  for (int b = 0; b < bpw; ++b) {
+    const int64_t t0 = (blk0 + b) * 16;
+    if (t0 >= N) break;
+    const int64_t t = t0 + i;
+    s16x4 bop[KC];
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = 16 * kc + 4 * qq;
+      const uint32_t off = (k < K) ? static_cast<uint32_t>((t * K + k) * 2) : kOffNone;
+      bop[kc] = __builtin_bit_cast(s16x4, load8(db, off));
+    }
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl) {
+      f32x4 acc;
+      if constexpr (KC == 1) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bop[0],
+                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+      } else {
+        acc = mfma::mma32(aop[tl][0], aop[tl][1], bop[0], bop[1], f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+      const u32x2 pk = {mfma::pack2_bf16(acc[0], acc[1]), mfma::pack2_bf16(acc[2], acc[3])};
+      const uint32_t off = static_cast<uint32_t>((t * Z + zs + 16 * tl + 4 * qq) * 2);
+      __builtin_amdgcn_raw_buffer_store_b64(pk, ob.r, static_cast<int>(off), 0, 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Partial drouter over a token range: D[k][zc] = sum_t dl[t][k] z[t][zc].
+// Workgroup: 64 columns and one token range, 4 waves taking 32-token blocks in
+// turn.  Each block of z (32 x 64) and of dl (32 x KP) is loaded with 16- and
+// 8-byte accesses into a wave-private LDS tile and read back transposed: A lane
+// (i, qq) = dl[8 qq + {0..7}][16 kc + i], B lane (j, qq) = z[8 qq + {0..7}][16 tl
+// + j].  The waves' tiles are summed in LDS in wave order and written as
+// part[range][k][zc] (fp32).
+constexpr int kZRow = 64 + 8;   // padded LDS row of a z tile (bf16)
+
+template <int KC>
+__global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restrict__ dl,
+                                                        const uint16_t* __restrict__ z,
+                                                        float* __restrict__ part, int64_t N,
+                                                        int Z, int K, int blocks_per_range) {
+  constexpr int KP = 16 * KC;
+  constexpr int KROW = KP + 4;  // padded LDS row of a dl tile (bf16)
+  __shared__ __align__(16) uint16_t zt[4][32][kZRow];
+  __shared__ __align__(16) uint16_t dt[4][32][KROW];
+  __shared__ float red[4][KP][65];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int i = lane & 15, qq = lane >> 4;
+  const int zs = blockIdx.x * 64;
+  const Buf zb(z, N * Z * 2);
+  const Buf db(dl, N * K * 2);
+  f32x4 acc[4][KC];
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) acc[tl][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t blk0 = static_cast<int64_t>(blockIdx.y) * blocks_per_range;
+  for (int b = w; b < blocks_per_range; b += 4) {
+    const int64_t t0 = (blk0 + b) * 32;
+    if (t0 >= N) break;  // per wave; the waves meet again only after the loop
+    // z rows t0 + lane / 8 + 8 ld, columns zs + 8 (lane % 8) .. + 7
+#pragma unroll
+    for (int ld = 0; ld < 4; ++ld) {
+      const int row = lane / 8 + 8 * ld;
+      const uint32_t off = static_cast<uint32_t>(((t0 + row) * Z + zs + 8 * (lane % 8)) * 2);
+      const u32x4 v = load16(zb, off);
+      *reinterpret_cast<u32x4*>(&zt[w][row][8 * (lane % 8)]) = v;
+    }
+    // dl rows of the block: KP / 4 chunks of 4 routes per row
+#pragma unroll
+    for (int ld = 0; ld < KP / 8; ++ld) {
+      const int chunk = lane + 64 * ld;
+      const int row = chunk / (KP / 4), k = 4 * (chunk % (KP / 4));
+      const uint32_t off = (k < K) ? static_cast<uint32_t>(((t0 + row) * K + k) * 2) : kOffNone;
+      const u32x2 v = load8(db, off);
+      *reinterpret_cast<u32x2*>(&dt[w][row][k]) = v;
+    }
+    mfma::wave_lds_sync();
+    // supplier lane 4 e + a of group qq reads row 8 qq + 4 h + e, columns 4 a..
+    const int e = i >> 2, a = i & 3;
+    s16x4 bz[4][2], ad[KC][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 8 * qq + 4 * h + e;
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) bz[tl][h] = tr_read(&zt[w][row][16 * tl + 4 * a]);
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) ad[kc][h] = tr_read(&dt[w][row][16 * kc + 4 * a]);
+    }
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        acc[tl][kc] = mfma::mma32(ad[kc][0], ad[kc][1], bz[tl][0], bz[tl][1], acc[tl][kc]);
+    mfma::wave_lds_sync();
+  }
+  // D lane (j, q): column 16 tl + j, routes 16 kc + 4 q + v
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[w][16 * kc + 4 * qq + v][16 * tl + i] = acc[tl][kc][v];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < K * 64; idx += 256) {
+    const int k = idx / 64, col = idx % 64;
+    const float s = ((red[0][k][col] + red[1][k][col]) + red[2][k][col]) + red[3][k][col];
+    part[(static_cast<int64_t>(blockIdx.y) * K + k) * Z + zs + col] = s;
+  }
+}
+
+// drouter[k, zc] = sum over ranges of part[range][k][zc], in range order.
+__global__ void __launch_bounds__(256) router_dr_reduce_kernel(const float* __restrict__ part,
+                                                               uint16_t* __restrict__ dr,
+                                                               int64_t KZ, int n_ranges) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= KZ) return;
+  float s = 0.f;
+  for (int p = 0; p < n_ranges; ++p) s += part[p * KZ + idx];
+  dr[idx] = f32_to_bf16(s);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct BwdPlan {
+  int64_t ranges, blocks_per_range;
+};
+
+BwdPlan bwd_plan(int64_t N, int64_t Z) {
+  const int64_t nblk = cdiv(N, 32);
+  const int64_t slices = Z / 64;
+  int64_t ranges = cdiv(512, slices);  // about 512 workgroups
+  if (ranges > cdiv(nblk, 4)) ranges = cdiv(nblk, 4);
+  if (ranges < 1) ranges = 1;
+  const int64_t bpr = cdiv(nblk, ranges);
+  return BwdPlan{cdiv(nblk, bpr), bpr};
+}
+
+}  // namespace router
+
+bool router_supported(int64_t N, int64_t Z, int64_t K, int dt) {
+  // buffer resources address [N, Z] bf16 with 32-bit byte offsets
+  return dt == DT_BF16 && K > 0 && K <= 32 && K % 4 == 0 && Z >= 64 && Z % 64 == 0 && N > 0 &&
+         N * Z * 2 < (int64_t(1) << 31);
+}
+
+size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
+  const router::BwdPlan pl = router::bwd_plan(N, Z);
+  return static_cast<size_t>(pl.ranges * K * Z) * 4;
+}
+
+void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
+                    hipStream_t st) {
+  const dim3 grid(static_cast<unsigned>(router::cdiv(N, 16)));
+  const auto* zp = static_cast<const uint16_t*>(z);
+  const auto* rp = static_cast<const uint16_t*>(r);
+  auto* lp = static_cast<uint16_t*>(logits);
+  if (K <= 16)
+    hipLaunchKernelGGL(router::router_fwd_kernel<1>, grid, dim3(256), 0, st, zp, rp, lp, N,
+                       static_cast<int>(Z), static_cast<int>(K));
+  else
+    hipLaunchKernelGGL(router::router_fwd_kernel<2>, grid, dim3(256), 0, st, zp, rp, lp, N,
+                       static_cast<int>(Z), static_cast<int>(K));
+}
+
+void router_backward(const void* z, const void* r, const void* dl, void* dz, void* dr,
+                     int64_t N, int64_t Z, int64_t K, void* workspace, hipStream_t st) {
+  const auto* zp = static_cast<const uint16_t*>(z);
+  const auto* rp = static_cast<const uint16_t*>(r);
+  const auto* dp = static_cast<const uint16_t*>(dl);
+  const int Zi = static_cast<int>(Z), Ki = static_cast<int>(K);
+  if (dz != nullptr) {
+    const int64_t nblk = router::cdiv(N, 16);
+    const int64_t waves_x = Z / 64;
+    int64_t bpw = router::cdiv(nblk * waves_x, 4096);
+    if (bpw < 1) bpw = 1;
+    const dim3 grid(static_cast<unsigned>(router::cdiv(waves_x, 4)),
+                    static_cast<unsigned>(router::cdiv(nblk, bpw)));
+    auto* op = static_cast<uint16_t*>(dz);
+    if (K <= 16)
+      hipLaunchKernelGGL(router::router_dz_kernel<1>, grid, dim3(256), 0, st, dp, rp, op, N, Zi,
+                         Ki, static_cast<int>(bpw));
+    else
+      hipLaunchKernelGGL(router::router_dz_kernel<2>, grid, dim3(256), 0, st, dp, rp, op, N, Zi,
+                         Ki, static_cast<int>(bpw));
+  }
+  if (dr != nullptr) {
+    const router::BwdPlan pl = router::bwd_plan(N, Z);
+    float* part = static_cast<float*>(workspace);
+    const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
+    if (K <= 16)
+      hipLaunchKernelGGL(router::router_dr_kernel<1>, grid, dim3(256), 0, st, dp, zp, part, N, Zi,
+                         Ki, static_cast<int>(pl.blocks_per_range));
+    else
+      hipLaunchKernelGGL(router::router_dr_kernel<2>, grid, dim3(256), 0, st, dp, zp, part, N, Zi,
+                         Ki, static_cast<int>(pl.blocks_per_range));
+    const int64_t KZ = K * Z;
+    hipLaunchKernelGGL(router::router_dr_reduce_kernel, dim3(static_cast<unsigned>(router::cdiv(KZ, 256))),
+                       dim3(256), 0, st, part, static_cast<uint16_t*>(dr), KZ,
+                       static_cast<int>(pl.ranges));
+  }
+}
+
+}  // namespace moc

@@ -29,6 +29,10 @@ EXPORTED_SYMBOLS = (
     "moc_backward",
     "moc_update",
     "moc_profile_events",
+    "moc_router_supported",
+    "moc_router_forward",
+    "moc_router_backward_workspace_bytes",
+    "moc_router_backward",
 )
 
 _lock = threading.Lock()
@@ -81,6 +85,14 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_update.restype = _i
     lib.moc_profile_events.argtypes = [_p, _p]
     lib.moc_profile_events.restype = _i
+    lib.moc_router_supported.argtypes = [_l, _l, _l, _i]
+    lib.moc_router_supported.restype = _i
+    lib.moc_router_forward.argtypes = [_p, _p, _p, _l, _l, _l, _i, _p]
+    lib.moc_router_forward.restype = _i
+    lib.moc_router_backward_workspace_bytes.argtypes = [_l, _l, _l, _i]
+    lib.moc_router_backward_workspace_bytes.restype = _z
+    lib.moc_router_backward.argtypes = [_p, _p, _p, _p, _p, _l, _l, _l, _i, _p, _z, _p]
+    lib.moc_router_backward.restype = _i
 
 
 def lib() -> ctypes.CDLL:

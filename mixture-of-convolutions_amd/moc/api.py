@@ -9,7 +9,10 @@ the gfx950 HIP kernels of libmoc_hip.so through ``ops`` and
   re-running the forward (moc/api.py:176-183);
 * ``MoC.forward`` / ``MoC.step`` hand the router *logits* to the kernels, which
   apply softmax / exp themselves and return d(logits) directly, so the router
-  activation and its gradient cost no separate kernels (moc/api.py:383-388).
+  activation and its gradient cost no separate kernels (moc/api.py:383-388);
+* the router GEMM logits = z . router^T and its backward run on the library's
+  skinny-GEMM kernels for bf16 layers (``router_linear``), torch's F.linear
+  otherwise.
 """
 from __future__ import annotations
 
@@ -217,6 +220,33 @@ class _MoCRoutedFunction(torch.autograd.Function):
         return dx, dlogits, dbasis, None, None, None, None, None, None
 
 
+class _RouterLinear(torch.autograd.Function):
+    """logits = z . router^T on the library's router kernels, with their
+    backward (dz = dlogits . router, drouter = dlogits^T . z)."""
+
+    @staticmethod
+    def forward(ctx, z, router):
+        ctx.save_for_backward(z, router)
+        return ops.router_forward(z, router)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dlogits):
+        z, router = ctx.saved_tensors
+        dz, dr = ops.router_backward(z, router, dlogits, ctx.needs_input_grad[0],
+                                     ctx.needs_input_grad[1])
+        return dz, dr
+
+
+def router_linear(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
+    """``F.linear(z, router)`` of ``MoC.forward`` (moc/api.py:383): the router
+    kernels of the HIP library where they apply (bf16, k % 4 == 0, k <= 32,
+    z_dim % 64 == 0), torch's GEMM otherwise."""
+    if ops.router_supported(z, router):
+        return _RouterLinear.apply(z, router)
+    return F.linear(z, router)
+
+
 def _apply(x, a, basis, activation, router_activation, cu_seqlens=None, max_seqlen=None,
            cu_seqlens_cpu=None, chunk_indices=None):
     if router_activation is None:
@@ -327,7 +357,7 @@ class MoC(nn.Module):
                 max_seqlen: Optional[int] = None, cu_seqlens_cpu: Optional[torch.Tensor] = None,
                 chunk_indices: Optional[torch.Tensor] = None
                 ) -> tuple[torch.Tensor, torch.Tensor | None]:
-        logits = F.linear(z, self.router)
+        logits = router_linear(z, self.router)
         return _dispatch(x, logits, self.conv_bases, cache, output_final_state,
                          self.activation, self.router_activation, cu_seqlens, max_seqlen,
                          cu_seqlens_cpu, chunk_indices)
@@ -347,4 +377,4 @@ class MoC(nn.Module):
         return self.dim * self.kernel_size
 
 
-__all__ = ["MoC", "moc_triton", "moc_hip"]
+__all__ = ["MoC", "moc_triton", "moc_hip", "router_linear"]

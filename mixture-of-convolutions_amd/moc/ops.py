@@ -240,3 +240,55 @@ def launch_update(
         )
     _lib.check(rc, "moc_update")
     return out
+
+
+def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
+    """Whether the router GEMM of ``MoC.forward`` runs on the library's kernels
+    (bf16 z and router on a GPU, k % 4 == 0, k <= 32, z_dim % 64 == 0)."""
+    if not (z.is_cuda and router.is_cuda) or z.dtype != torch.bfloat16 or router.dtype != z.dtype:
+        return False
+    K, Z = router.shape
+    if z.shape[-1] != Z or z.numel() == 0:
+        return False
+    return bool(_lib.lib().moc_router_supported(z.numel() // Z, Z, K, _lib.DT_BF16))
+
+
+def router_forward(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
+    """logits = z . router^T (the F.linear(z, router) of moc/api.py:383-388)."""
+    L = _lib.lib()
+    z = z.contiguous()
+    r = router.contiguous()
+    K, Z = r.shape
+    N = z.numel() // Z
+    out = torch.empty(*z.shape[:-1], K, dtype=z.dtype, device=z.device)
+    with torch.cuda.device(z.device):
+        rc = L.moc_router_forward(z.data_ptr(), r.data_ptr(), out.data_ptr(), N, Z, K,
+                                  _lib.DT_BF16, _lib.stream_ptr(z.device))
+    _lib.check(rc, "moc_router_forward")
+    return out
+
+
+def router_backward(z: torch.Tensor, router: torch.Tensor, dlogits: torch.Tensor,
+                    need_z: bool, need_router: bool
+                    ) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """(dz, drouter) = (dlogits . router, dlogits^T . z); either may be skipped."""
+    L = _lib.lib()
+    z = z.contiguous()
+    r = router.contiguous()
+    dl = dlogits.contiguous()
+    if dl.dtype != z.dtype:
+        dl = dl.to(z.dtype)
+    K, Z = r.shape
+    N = z.numel() // Z
+    dz = torch.empty_like(z) if need_z else None
+    dr = torch.empty_like(r) if need_router else None
+    nbytes = L.moc_router_backward_workspace_bytes(N, Z, K, _lib.DT_BF16) if need_router else 0
+    ws = _workspace(nbytes, z.device)
+    with torch.cuda.device(z.device):
+        rc = L.moc_router_backward(
+            z.data_ptr(), r.data_ptr(), dl.data_ptr(),
+            None if dz is None else dz.data_ptr(), None if dr is None else dr.data_ptr(),
+            N, Z, K, _lib.DT_BF16, ws.data_ptr() if nbytes else None, nbytes,
+            _lib.stream_ptr(z.device))
+    _lib.check(rc, "moc_router_backward")
+    return dz, dr

@@ -33,27 +33,31 @@ def _layer(D, Z, K, S, act, route, init_std, dtype, seed=0):
 
 
 def _oracle_layer(m, x, z, dy, route, act, cu=None):
-    """The layer with the MoC op replaced by the fp32 oracle: the router GEMM is
-    the same torch op the module runs (module dtype, on the GPU), the router
-    activation is rounded to the logits' dtype with torch's gradient rule, and
-    the oracle's d(logits) is cast back to that dtype for the GEMM's backward.
-    Returns y and the gradients of x, z, router, basis."""
-    lz = z.detach().requires_grad_()
-    lr = m.router.detach().requires_grad_()
-    logits = torch.nn.functional.linear(lz, lr)
+    """The layer with the MoC op replaced by the fp32 oracle.  The logits are
+    the module's own router GEMM (moc.router_linear, on the GPU), so the
+    oracle and the module route identically; the router activation is rounded
+    to the logits' dtype with torch's gradient rule; dz and drouter are fp32
+    products of the oracle's d(logits) rounded to the logits' dtype, the value
+    the module's router backward consumes.  Returns y and the gradients of x,
+    z, router, basis."""
+    with torch.no_grad():
+        logits = moc.router_linear(z, m.router)
+    lf = logits.float().requires_grad_()
     rx = x.detach().float().requires_grad_()
     rb = m.conv_bases.detach().float().requires_grad_()
-    lf = logits.float()
-    seen = {}
-    lf.register_hook(lambda gr: seen.__setitem__("dlogits", gr))
     alpha = O.route(lf, route, out_dtype=logits.dtype)
     if cu is None:
         y = O.moc_ref(rx, alpha, rb, act)
     else:
         y = O.moc_varlen_ref(rx, alpha, rb, cu, act)
     y.backward(dy.float())
-    _oracle_layer.last_dlogits = seen["dlogits"]
-    return y.detach(), rx.grad, lz.grad, lr.grad, rb.grad
+    dl = lf.grad
+    _oracle_layer.last_dlogits = dl
+    K, Z = m.router.shape
+    dlr = dl.to(logits.dtype).float().reshape(-1, K)
+    dz = (dlr @ m.router.detach().float()).reshape(z.shape)
+    drouter = dlr.T @ z.detach().float().reshape(-1, Z)
+    return y.detach(), rx.grad, dz, drouter, rb.grad
 
 
 def _check_layer(label, m, got, ref, dtype):
@@ -209,7 +213,7 @@ def test_config4_decode():
     assert torch.equal(cache, x[:, -S:].transpose(1, 2))
     rows = torch.arange(0, B, 37, device=DEV)
     with torch.no_grad():
-        logits = torch.nn.functional.linear(z[rows], m.router)
+        logits = moc.router_linear(z[rows], m.router)
         alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
         full = O.moc_ref(x[rows].float(), alpha, m.conv_bases.float(), "silu")
     assert_close("decode y", y_steps[rows], full[:, P:], torch.bfloat16)
