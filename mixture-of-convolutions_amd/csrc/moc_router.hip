@@ -45,72 +45,100 @@ __device__ __forceinline__ s16x4 tr_read(const void* p) {
 }
 
 // ---------------------------------------------------------------------------
-// logits[t, k] = sum_z z[t, z] router[k, z].  Workgroup: 16 tokens, 4 waves.
-// Wave w sums the 64-wide z chunks c = w, w + 4, ...: lane (i, qq) loads the 16
-// columns 64 c + 16 qq + [0, 16) of token t0 + i (A operand) and of route
-// 16 kc + i (B operand), two MFMAs per chunk.  The 4 partial 16 x KP tiles are
-// summed in LDS in wave order.
+// logits[t, k] = sum_z z[t, z] router[k, z].  Workgroup: 32 tokens (two blocks
+// of 16), 4 waves.  Wave w sums the 64-wide z chunks c = w, w + 4, ...: lane
+// (i, qq) loads columns 64 c + 8 qq + [0, 8) and 64 c + 32 + 8 qq + [0, 8) of
+// tokens t0 + i, t0 + 16 + i (A operands) and of route 16 kc + i (B operands),
+// so that each load instruction reads 64 contiguous bytes per row and the
+// router operands serve both token blocks.  The 4 partial tiles are summed in
+// LDS in wave order.
 template <int KC>
 __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restrict__ z,
                                                          const uint16_t* __restrict__ r,
                                                          uint16_t* __restrict__ logits,
                                                          int64_t N, int Z, int K) {
   constexpr int KP = 16 * KC;
-  __shared__ float red[4][KP][17];
+  __shared__ float red[4][2][KP][17];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i = lane & 15, qq = lane >> 4;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 16;
-  const int64_t rows = (N - t0 < 16) ? N - t0 : 16;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 32;
+  const int64_t rows = (N - t0 < 32) ? N - t0 : 32;
   // rows past N and routes past K lie outside the buffers and load zeros
   const Buf zb(z + t0 * Z, rows * Z * 2);
   const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
-  const uint32_t zrow = static_cast<uint32_t>(i * Z * 2);
-  f32x4 acc[KC];
+  f32x4 acc[2][KC];
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) acc[kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) acc[h][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int nchunk = Z / 64;
-  // four chunks per step, so that 8 (+ 8 KC) loads per lane are in flight
+  // four chunks per step with all their loads issued first (16 + 8 KC per lane);
+  // chunks past the row end load zeros instead of branching
   for (int c0 = w; c0 < nchunk; c0 += 16) {
+    u32x4 za[4][2][2], ra[4][KC][2];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int c = c0 + 4 * u;
-      if (c < nchunk) {
-        const uint32_t col = static_cast<uint32_t>((64 * c + 16 * qq) * 2);
-        const u32x4 z0 = load16(zb, zrow + col), z1 = load16(zb, zrow + col + 16);
+      const bool on = c < nchunk;
+      const uint32_t col0 = static_cast<uint32_t>((64 * c + 8 * qq) * 2), col1 = col0 + 64;
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
-          const u32x4 r0 = load16(rb, rrow + col), r1 = load16(rb, rrow + col + 16);
-          acc[kc] = mma8(z0, r0, acc[kc]);
-          acc[kc] = mma8(z1, r1, acc[kc]);
-        }
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t zrow = static_cast<uint32_t>((16 * h + i) * Z * 2);
+        za[u][h][0] = load16(zb, on ? zrow + col0 : kOffNone);
+        za[u][h][1] = load16(zb, on ? zrow + col1 : kOffNone);
+      }
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
+        ra[u][kc][0] = load16(rb, on ? rrow + col0 : kOffNone);
+        ra[u][kc][1] = load16(rb, on ? rrow + col1 : kOffNone);
       }
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          acc[h][kc] = mma8(za[u][h][0], ra[u][kc][0], acc[h][kc]);
+          acc[h][kc] = mma8(za[u][h][1], ra[u][kc][1], acc[h][kc]);
+        }
   }
-  // D lane (j, q): route 16 kc + j, tokens 4 q + v
+  // D lane (j, q): route 16 kc + j, tokens 16 h + 4 q + v
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[w][16 * kc + i][4 * qq + v] = acc[kc][v];
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[w][h][16 * kc + i][4 * qq + v] = acc[h][kc][v];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * KP; idx += 256) {
-    const int tok = idx / KP, k = idx % KP;
-    const float s = ((red[0][k][tok] + red[1][k][tok]) + red[2][k][tok]) + red[3][k][tok];
+  for (int idx = threadIdx.x; idx < 32 * KP; idx += 256) {
+    const int tok = idx / KP, k = idx % KP, h = tok >> 4, tr = tok & 15;
+    const float s = ((red[0][h][k][tr] + red[1][h][k][tr]) + red[2][h][k][tr]) + red[3][h][k][tr];
     if (k < K && tok < rows) logits[(t0 + tok) * K + k] = f32_to_bf16(s);
   }
 }
 
 // ---------------------------------------------------------------------------
-// dz[t, zc] = sum_k dl[t, k] router[k, zc].  A wave owns 64 columns (4 tiles
-// of 16) and walks `bpw` blocks of 16 tokens.  D[zc][t] = router^T . dl^T:
-// A lane (i, qq) holds router[16 kc + 4 qq + {0..3}][zc_i] (kept in registers),
-// B lane (j, qq) holds dl[t_j][16 kc + 4 qq + {0..3}]; the result lane (j, q)
-// holds columns 4 q + {0..3} of token t_j: one 8-byte store.
+// dz[t, zc] = sum_k dl[t, k] router[k, zc].  A wave owns 64 columns and kDzBlocks
+// blocks of 16 tokens.  D[zc][t] = router^T . dl^T with A lane (i, qq) holding
+// router[16 kc + 4 qq + {0..3}][zc] (kept in registers) and B lane (j, qq)
+// holding dl[t_j][16 kc + 4 qq + {0..3}].  Row r = 4 q + v of tile tl stands for
+// column zs + zcol(tl, r), zcol = 32 (tl >> 1) + 8 q + 4 (tl & 1) + v, so that
+// the result lane (j, q) holds columns 8 q + {0..7} (tiles 0, 1) and
+// 32 + 8 q + {0..7} (tiles 2, 3) of token t_j: two 16-byte stores, and each
+// store instruction writes 64 contiguous bytes of every token row.
+constexpr int kDzBlocks = 8;
+
+__device__ __forceinline__ int dz_col(int tl, int r) {
+  return 32 * (tl >> 1) + 8 * (r >> 2) + 4 * (tl & 1) + (r & 3);
+}
+
 template <int KC>
 __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restrict__ dl,
                                                         const uint16_t* __restrict__ r,
                                                         uint16_t* __restrict__ dz, int64_t N,
-                                                        int Z, int K, int bpw) {
+                                                        int Z, int K) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int i = lane & 15, qq = lane >> 4;
   const int zs = (blockIdx.x * 4 + w) * 64;
@@ -118,6 +146,18 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
   const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
   const Buf db(dl, N * K * 2);
   const Buf ob(dz, N * Z * 2);
+  const int64_t tb = static_cast<int64_t>(blockIdx.y) * kDzBlocks * 16;
+  // B operands of all blocks first: rows past N load zeros
+  s16x4 bop[kDzBlocks][KC];
+#pragma unroll
+  for (int b = 0; b < kDzBlocks; ++b)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = 16 * kc + 4 * qq;
+      const int64_t t = tb + 16 * b + i;
+      const uint32_t off = (k < K) ? static_cast<uint32_t>((t * K + k) * 2) : kOffNone;
+      bop[b][kc] = __builtin_bit_cast(s16x4, load8(db, off));
+    }
   s16x4 aop[4][KC];
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl)
@@ -127,36 +167,34 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int k = 16 * kc + 4 * qq + v;
-        const uint32_t off = static_cast<uint32_t>((k * Z + zs + 16 * tl + i) * 2);
+        const uint32_t off = static_cast<uint32_t>((k * Z + zs + dz_col(tl, i)) * 2);
         e[v] = __builtin_amdgcn_raw_buffer_load_b16(rb.r, static_cast<int>(off), 0, 0);
       }
       aop[tl][kc] = s16x4{static_cast<short>(e[0]), static_cast<short>(e[1]),
                           static_cast<short>(e[2]), static_cast<short>(e[3])};
     }
-  const int64_t blk0 = static_cast<int64_t>(blockIdx.y) * bpw;
-  for (int b = 0; b < bpw; ++b) {
-    const int64_t t0 = (blk0 + b) * 16;
-    if (t0 >= N) break;
-    const int64_t t = t0 + i;
-    s16x4 bop[KC];
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      const int k = 16 * kc + 4 * qq;
-      const uint32_t off = (k < K) ? static_cast<uint32_t>((t * K + k) * 2) : kOffNone;
-      bop[kc] = __builtin_bit_cast(s16x4, load8(db, off));
-    }
+  for (int b = 0; b < kDzBlocks; ++b) {
+    const int64_t t = tb + 16 * b + i;
+    f32x4 acc[4];
 #pragma unroll
     for (int tl = 0; tl < 4; ++tl) {
-      f32x4 acc;
       if constexpr (KC == 1) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bop[0],
-                                                        f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        acc[tl] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bop[b][0],
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
       } else {
-        acc = mfma::mma32(aop[tl][0], aop[tl][1], bop[0], bop[1], f32x4{0.f, 0.f, 0.f, 0.f});
+        acc[tl] = mfma::mma32(aop[tl][0], aop[tl][1], bop[b][0], bop[b][1],
+                              f32x4{0.f, 0.f, 0.f, 0.f});
       }
-      const u32x2 pk = {mfma::pack2_bf16(acc[0], acc[1]), mfma::pack2_bf16(acc[2], acc[3])};
-      const uint32_t off = static_cast<uint32_t>((t * Z + zs + 16 * tl + 4 * qq) * 2);
-      __builtin_amdgcn_raw_buffer_store_b64(pk, ob.r, static_cast<int>(off), 0, 0);
+    }
+    // rows past N lie outside the buffer: their stores are dropped
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const f32x4 a0 = acc[2 * half], a1 = acc[2 * half + 1];
+      const u32x4 pk = {mfma::pack2_bf16(a0[0], a0[1]), mfma::pack2_bf16(a0[2], a0[3]),
+                        mfma::pack2_bf16(a1[0], a1[1]), mfma::pack2_bf16(a1[2], a1[3])};
+      const uint32_t off = static_cast<uint32_t>((t * Z + zs + 32 * half + 8 * qq) * 2);
+      __builtin_amdgcn_raw_buffer_store_b128(pk, ob.r, static_cast<int>(off), 0, 0);
     }
   }
 }
@@ -193,25 +231,38 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
     for (int kc = 0; kc < KC; ++kc) acc[tl][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t blk0 = static_cast<int64_t>(blockIdx.y) * blocks_per_range;
-  for (int b = w; b < blocks_per_range; b += 4) {
-    const int64_t t0 = (blk0 + b) * 32;
-    if (t0 >= N) break;  // per wave; the waves meet again only after the loop
-    // z rows t0 + lane / 8 + 8 ld, columns zs + 8 (lane % 8) .. + 7
+  // registers of one block: z rows t0 + lane / 8 + 8 ld, columns zs + 8 (lane % 8)
+  // .. + 7; dl rows of the block in KP / 4 chunks of 4 routes.  Two register
+  // sets: the loads of blocks b + 4 and b + 8 are in flight while block b is
+  // multiplied.  Blocks past the range or past N load zeros (no branches).
+  struct Regs {
+    u32x4 z[4];
+    u32x2 d[KP / 8];
+  };
+  auto load_block = [&](Regs& rg, int bb) {
+    const int64_t t0 = (blk0 + bb) * 32;
+    const bool on = bb < blocks_per_range && t0 < N;
 #pragma unroll
     for (int ld = 0; ld < 4; ++ld) {
       const int row = lane / 8 + 8 * ld;
-      const uint32_t off = static_cast<uint32_t>(((t0 + row) * Z + zs + 8 * (lane % 8)) * 2);
-      const u32x4 v = load16(zb, off);
-      *reinterpret_cast<u32x4*>(&zt[w][row][8 * (lane % 8)]) = v;
+      rg.z[ld] = load16(zb, on ? static_cast<uint32_t>(((t0 + row) * Z + zs + 8 * (lane % 8)) * 2)
+                               : kOffNone);
     }
-    // dl rows of the block: KP / 4 chunks of 4 routes per row
 #pragma unroll
     for (int ld = 0; ld < KP / 8; ++ld) {
       const int chunk = lane + 64 * ld;
       const int row = chunk / (KP / 4), k = 4 * (chunk % (KP / 4));
-      const uint32_t off = (k < K) ? static_cast<uint32_t>(((t0 + row) * K + k) * 2) : kOffNone;
-      const u32x2 v = load8(db, off);
-      *reinterpret_cast<u32x2*>(&dt[w][row][k]) = v;
+      rg.d[ld] = load8(db, (on && k < K) ? static_cast<uint32_t>(((t0 + row) * K + k) * 2) : kOffNone);
+    }
+  };
+  auto mult_block = [&](const Regs& rg) {
+#pragma unroll
+    for (int ld = 0; ld < 4; ++ld)
+      *reinterpret_cast<u32x4*>(&zt[w][lane / 8 + 8 * ld][8 * (lane % 8)]) = rg.z[ld];
+#pragma unroll
+    for (int ld = 0; ld < KP / 8; ++ld) {
+      const int chunk = lane + 64 * ld;
+      *reinterpret_cast<u32x2*>(&dt[w][chunk / (KP / 4)][4 * (chunk % (KP / 4))]) = rg.d[ld];
     }
     mfma::wave_lds_sync();
     // supplier lane 4 e + a of group qq reads row 8 qq + 4 h + e, columns 4 a..
@@ -231,6 +282,16 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
       for (int kc = 0; kc < KC; ++kc)
         acc[tl][kc] = mfma::mma32(ad[kc][0], ad[kc][1], bz[tl][0], bz[tl][1], acc[tl][kc]);
     mfma::wave_lds_sync();
+  };
+  Regs ra, rb2;
+  load_block(ra, w);
+  load_block(rb2, w + 4);
+  for (int b = w; b < blocks_per_range; b += 8) {  // per wave; no barrier inside
+    mult_block(ra);
+    load_block(ra, b + 8);
+    if (b + 4 >= blocks_per_range) break;
+    mult_block(rb2);
+    load_block(rb2, b + 12);
   }
   // D lane (j, q): column 16 tl + j, routes 16 kc + 4 q + v
 #pragma unroll
@@ -253,8 +314,18 @@ __global__ void __launch_bounds__(256) router_dr_reduce_kernel(const float* __re
                                                                int64_t KZ, int n_ranges) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx >= KZ) return;
+  // loads four at a time, sums in range order
   float s = 0.f;
-  for (int p = 0; p < n_ranges; ++p) s += part[p * KZ + idx];
+  int p = 0;
+  for (; p + 4 <= n_ranges; p += 4) {
+    const float a = part[p * KZ + idx], b = part[(p + 1) * KZ + idx];
+    const float c = part[(p + 2) * KZ + idx], d = part[(p + 3) * KZ + idx];
+    s += a;
+    s += b;
+    s += c;
+    s += d;
+  }
+  for (; p < n_ranges; ++p) s += part[p * KZ + idx];
   dr[idx] = f32_to_bf16(s);
 }
 
@@ -292,7 +363,7 @@ size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
 
 void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
                     hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(router::cdiv(N, 16)));
+  const dim3 grid(static_cast<unsigned>(router::cdiv(N, 32)));
   const auto* zp = static_cast<const uint16_t*>(z);
   const auto* rp = static_cast<const uint16_t*>(r);
   auto* lp = static_cast<uint16_t*>(logits);
@@ -311,19 +382,14 @@ void router_backward(const void* z, const void* r, const void* dl, void* dz, voi
   const auto* dp = static_cast<const uint16_t*>(dl);
   const int Zi = static_cast<int>(Z), Ki = static_cast<int>(K);
   if (dz != nullptr) {
-    const int64_t nblk = router::cdiv(N, 16);
     const int64_t waves_x = Z / 64;
-    int64_t bpw = router::cdiv(nblk * waves_x, 4096);
-    if (bpw < 1) bpw = 1;
     const dim3 grid(static_cast<unsigned>(router::cdiv(waves_x, 4)),
-                    static_cast<unsigned>(router::cdiv(nblk, bpw)));
+                    static_cast<unsigned>(router::cdiv(N, 16 * router::kDzBlocks)));
     auto* op = static_cast<uint16_t*>(dz);
     if (K <= 16)
-      hipLaunchKernelGGL(router::router_dz_kernel<1>, grid, dim3(256), 0, st, dp, rp, op, N, Zi,
-                         Ki, static_cast<int>(bpw));
+      hipLaunchKernelGGL(router::router_dz_kernel<1>, grid, dim3(256), 0, st, dp, rp, op, N, Zi, Ki);
     else
-      hipLaunchKernelGGL(router::router_dz_kernel<2>, grid, dim3(256), 0, st, dp, rp, op, N, Zi,
-                         Ki, static_cast<int>(bpw));
+      hipLaunchKernelGGL(router::router_dz_kernel<2>, grid, dim3(256), 0, st, dp, rp, op, N, Zi, Ki);
   }
   if (dr != nullptr) {
     const router::BwdPlan pl = router::bwd_plan(N, Z);
