@@ -244,6 +244,15 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
   if (batch > kMaxBatch) return fail(MOC_ERR_ARG, "batch too large: %lld", (long long)batch);
   if (!x || !alpha || !basis || !cache || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
+  const char* env = std::getenv("MOC_HIP_PATH");
+  const bool force_generic = env != nullptr && std::strcmp(env, "generic") == 0;
+  if (!force_generic && moc::decode_supported(batch, dim, k, kernel_size, x_dtype, alpha_dtype,
+                                              basis_dtype, cache_stride_b, cache_stride_d,
+                                              cache_stride_s)) {
+    moc::launch_decode(x, alpha, routing, basis, cache, y, batch, dim, k, kernel_size, activation,
+                       static_cast<hipStream_t>(stream));
+    return hip_status("moc_update launch");
+  }
   moc::launch_update_generic(x, alpha, basis, cache, cache_stride_b, cache_stride_d,
                              cache_stride_s, y, batch, dim, k, kernel_size, x_dtype, alpha_dtype,
                              basis_dtype, activation, routing, static_cast<hipStream_t>(stream));

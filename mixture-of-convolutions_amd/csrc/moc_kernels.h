@@ -54,6 +54,15 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
               hipStream_t st);
 }  // namespace mfma
 
+// decode step on the matrix cores (moc_decode.hip): bf16 x, logits / weights
+// and basis, contiguous [B, D, S] cache, S in {2, 3, 4, 8}, K % 4 == 0, K <= 32,
+// D % 4 == 0
+bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
+                      int64_t cs_b, int64_t cs_d, int64_t cs_s);
+void launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+                   void* y, int64_t B, int64_t D, int64_t K, int64_t S, int activation,
+                   hipStream_t st);
+
 // router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 32, Z % 64 == 0
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt);
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K);

@@ -166,6 +166,17 @@ __device__ __forceinline__ bool starts_in(const SeqLayout& seq, int64_t lo, int6
   return seq.next_start(lo) <= hi;
 }
 
+// starts_in for windows that move forward: `ns` caches the smallest segment
+// start >= the previous window's lo and is searched again only once the
+// window has passed it (about once per sequence), not for every super-block.
+struct StartCursor {
+  int64_t ns = -1;
+  __device__ __forceinline__ bool starts_in(const SeqLayout& seq, int64_t lo, int64_t hi) {
+    if (ns < lo) ns = seq.next_start(lo);
+    return ns <= hi;
+  }
+};
+
 template <int S, int NROWS>
 __device__ __forceinline__ void tap_bits_rows(const SeqLayout& seq, int64_t row0, int64_t w_lo,
                                               int64_t w_hi, uint32_t (&ok)[NROWS]) {
@@ -259,6 +270,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   };
 
   if (tbase < N) fetch(tbase);
+  StartCursor cursor;
   for (int sb = 0; sb < n_sb; ++sb) {
     const int64_t t0 = tbase + static_cast<int64_t>(sb) * TB;
     if (t0 >= N) break;
@@ -279,7 +291,7 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
 
     // uniform over the wave: does a sequence start fall where it masks a tap?
     const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB - 1;
-    const bool interior = !starts_in(seq, w_lo, w_hi);
+    const bool interior = !cursor.starts_in(seq, w_lo, w_hi);
 
     auto body = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
@@ -477,7 +489,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   constexpr int AP = BF ? KP + 4 : KP;
   __shared__ __align__(16) E a_lds[2][AROWS][AP];
   __shared__ __align__(16) E m_lds[BF ? 1 : WPG][NP][BF ? 1 : TB][BF ? 1 : MROW];
-  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][2][NP][BF ? TT::kSlots : 1];
+  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][NP][BF ? TT::kSlots : 1];
+  // dalpha B operands of each wave's channels (bf16, one 16-route chunk): rows
+  // (k, s), CW channels; with more routes they stay in registers
+  constexpr bool kBdaLds = BF && KC == 1;
+  constexpr int BROW = CW + 4;
+  __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? KP * S : 1][kBdaLds ? BROW : 1];
   __shared__ float da_lds[2][WPG][NB][KC][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
@@ -530,7 +547,10 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         bb.load<4 * ESZ>(row_off((16 * kc + j) * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ),
                                  wave_on && ch < D),
                          e4);
-        bda[s][cg][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+        if constexpr (kBdaLds)  // read back per tap in the dalpha loop (wave-private rows)
+          Vec<E, 4>::store(&b_lds[wave][(16 * kc + j) * S + s][16 * cg + 4 * q], e4);
+        else
+          bda[s][cg][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
       }
     }
   }
@@ -583,6 +603,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   }
   __syncthreads();
 
+  StartCursor cursor;
   for (int sb = 0; sb < n_sb; ++sb) {
     const int64_t t0 = first + static_cast<int64_t>(sb) * EOWN;
     if (t0 >= N) break;  // uniform over the workgroup
@@ -612,7 +633,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     // uniform: does a sequence start fall where it masks a tap of the rows
     // [t0, t0 + TB + S - 1) (own rows, their later rows, the lanes' extended runs)?
     const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB + S - 2;
-    const bool interior = !starts_in(seq, w_lo, w_hi);
+    const bool interior = !cursor.starts_in(seq, w_lo, w_hi);
 
     f32x4 dacc[NB][KC];
 #pragma unroll
@@ -764,9 +785,11 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         // channels of the wave (channel groups 0, 1); A and B operands list
         // their entries in the same order
         static_assert(NB % 2 == 0 && NC == 2, "16x16x32 pairing");
-        // tap s: m_s -> bf16 hi / lo operands -> LDS tile (buffer s & 1) and the
+        // tap s: m_s -> bf16 hi / lo operands -> the wave's LDS tile and the
         // dbasis MFMAs; the dalpha reads of tap s are issued before the m values
-        // of tap s + 1 are computed, so that VALU work covers the LDS latency
+        // of tap s + 1 are computed and written, so that VALU work covers the
+        // LDS latency (one tile suffices: a wave's LDS operations complete in
+        // issue order, so the writes of tap s + 1 follow the reads of tap s)
         auto stage_m = [&](int s) {
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
@@ -789,8 +812,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
                 }
                 mh[bb] = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
                 ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
-                m_tr[wave][s & 1][0][TT::wslot(j, q, b, c)] = mh[bb];
-                m_tr[wave][s & 1][1][TT::wslot(j, q, b, c)] = ml[bb];
+                m_tr[wave][0][TT::wslot(j, q, b, c)] = mh[bb];
+                m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
               }
 #pragma unroll
               for (int kc = 0; kc < KC; ++kc) {
@@ -803,9 +826,6 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         stage_m(0);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          // LDS operations of a wave complete in order: the tile of tap s is
-          // written before these reads, and the reads of tap s - 1 from the other
-          // buffer are done before stage_m(s + 1) overwrites it
           wave_lds_sync();
           Op ra[NB][NP][2];
 #pragma unroll
@@ -814,7 +834,18 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int h = 0; h < NP; ++h)
 #pragma unroll
               for (int cg = 0; cg < 2; ++cg)
-                ra[rb][h][cg] = TT::read(&m_tr[wave][s & 1][h][TT::rslot(j, q, rb, cg)]);
+                ra[rb][h][cg] = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
+          // dalpha B operands of tap s: basis[16 kc + j][s][16 cg + 4 q + {0..3}]
+          Op bs[KC][2];
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+            for (int cg = 0; cg < 2; ++cg) {
+              if constexpr (kBdaLds)
+                bs[kc][cg] = *reinterpret_cast<const Op*>(&b_lds[wave][(16 * kc + j) * S + s][16 * cg + 4 * q]);
+              else
+                bs[kc][cg] = bda[s][cg][kc];
+            }
           // keep the reads ahead of the next tap's VALU work
           __builtin_amdgcn_sched_barrier(0);
           if (s + 1 < S) stage_m(s + 1);
@@ -825,7 +856,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int h = 0; h < NP; ++h)
 #pragma unroll
               for (int kc = 0; kc < KC; ++kc)
-                dacc[rb][kc] = mma32(ra[rb][h][0], ra[rb][h][1], bda[s][0][kc], bda[s][1][kc], dacc[rb][kc]);
+                dacc[rb][kc] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kc][0], bs[kc][1], dacc[rb][kc]);
         }
         wave_lds_sync();
       } else {

@@ -15,7 +15,10 @@ constexpr int kFwdNB = 2, kFwdNC = 2;
 constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
 // Resident workgroups the grids are sized for (256 CUs).
 constexpr int64_t kFwdTargetWG = 2048;
-constexpr int64_t kBwdTargetWG = 512;
+#ifndef MOC_BWD_TARGET_WG
+#define MOC_BWD_TARGET_WG 512
+#endif
+constexpr int64_t kBwdTargetWG = MOC_BWD_TARGET_WG;
 
 struct Grid2 {
   unsigned gx, gy;
