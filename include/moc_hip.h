@@ -133,6 +133,23 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
                int activation, int routing, void* stream);
 
 /*
+ * A whole decode step of the MoC layer in one launch: the router GEMM
+ * (logits = z . router^T, rounded to bf16), its softmax / exp (routing 1 / 2)
+ * and the step of moc_update, i.e. MoC.step (moc/api.py:403-425, which runs
+ * F.linear, the router activation and launch_update, moc/ops.py:341-362).
+ * All tensors bf16; cache [batch, dim, kernel_size] contiguous, updated in place.
+ *   z : [batch, z_dim], router : [k, z_dim], x, y : [batch, dim],
+ *   basis : [k, kernel_size, dim]
+ * Shapes: kernel_size in {2, 3, 4, 8}, k % 4 == 0, k <= 32, dim % 4 == 0,
+ * z_dim % 64 == 0 (moc_decode_step_supported returns 1 for such shapes).
+ */
+int moc_decode_step_supported(int64_t batch, int64_t z_dim, int64_t dim, int64_t k,
+                              int64_t kernel_size);
+int moc_decode_step(const void* z, const void* router, const void* x, const void* basis,
+                    void* cache, void* y, int64_t batch, int64_t z_dim, int64_t dim, int64_t k,
+                    int64_t kernel_size, int activation, int routing, void* stream);
+
+/*
  * Router of the MoC layer: logits = z . router^T, the F.linear(z, router) of
  * MoC.forward (moc/api.py:383-388) that the reference runs as a library GEMM,
  * and its backward.  bf16 only; k % 4 == 0, k <= 32, z_dim % 64 == 0 and

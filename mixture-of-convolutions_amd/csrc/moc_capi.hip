@@ -259,6 +259,33 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   return hip_status("moc_update launch");
 }
 
+int moc_decode_step_supported(int64_t batch, int64_t z_dim, int64_t dim, int64_t k,
+                              int64_t kernel_size) {
+  return moc::decode_step_supported(batch, dim, z_dim, k, kernel_size) ? 1 : 0;
+}
+
+int moc_decode_step(const void* z, const void* router, const void* x, const void* basis,
+                    void* cache, void* y, int64_t batch, int64_t z_dim, int64_t dim, int64_t k,
+                    int64_t kernel_size, int activation, int routing, void* stream) {
+  g_err[0] = '\0';
+  int rc;
+  if ((rc = check_dims(batch, dim, k, kernel_size)) != MOC_OK) return rc;
+  if (batch > kMaxBatch) return fail(MOC_ERR_ARG, "batch too large: %lld", (long long)batch);
+  if (activation != 0 && activation != 1)
+    return fail(MOC_ERR_ARG, "activation must be 0 or 1, got %d", activation);
+  if (routing != MOC_ROUTE_SOFTMAX && routing != MOC_ROUTE_EXP)
+    return fail(MOC_ERR_ARG, "routing must be softmax (1) or exp (2), got %d", routing);
+  if (!moc::decode_step_supported(batch, dim, z_dim, k, kernel_size))
+    return fail(MOC_ERR_ARG, "decode step shape not supported (batch %lld, z_dim %lld, dim %lld, "
+                             "k %lld, kernel_size %lld)",
+                (long long)batch, (long long)z_dim, (long long)dim, (long long)k,
+                (long long)kernel_size);
+  if (!z || !router || !x || !basis || !cache || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
+  moc::launch_decode_step(z, router, x, basis, cache, y, batch, z_dim, dim, k, kernel_size,
+                          activation, routing, static_cast<hipStream_t>(stream));
+  return hip_status("moc_decode_step launch");
+}
+
 int moc_router_supported(int64_t n_tokens, int64_t z_dim, int64_t k, int dtype) {
   return moc::router_supported(n_tokens, z_dim, k, dtype) ? 1 : 0;
 }

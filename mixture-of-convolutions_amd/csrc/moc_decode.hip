@@ -53,34 +53,41 @@ struct CacheRow {
   }
 };
 
-template <int S, int KC, bool ACT>
+// FUSED: the logits come from the router GEMM in the same kernel (z [B, Z],
+// router [K, Z]); otherwise `alpha` holds them (or the weights, ROUTE_ALPHA).
+template <int S, int KC, bool ACT, bool FUSED>
 __global__ void __launch_bounds__(256) decode_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ alpha, int routing,
     const uint16_t* __restrict__ basis, uint16_t* __restrict__ cache, uint16_t* __restrict__ y,
-    int64_t B, int64_t D, int K) {
+    int64_t B, int64_t D, int K, const uint16_t* __restrict__ z,
+    const uint16_t* __restrict__ router, int Z) {
   using C = CT<true>;
   constexpr int CW = 16 * kNC;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, qq = lane >> 4;
   const int64_t tb = static_cast<int64_t>(blockIdx.y) * 16;
   const int64_t d0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * CW;
-  if (d0 >= D) return;  // whole wave; the kernel has no barrier
+  const bool wave_on = d0 < D;
+  // without the router stage the kernel has no barrier and idle waves leave
+  if (!FUSED && !wave_on) return;
   const int64_t ta = tb + i;              // token of this lane's A-operand row
   const bool tok_ok = ta < B;
   const int64_t dl = d0 + kNC * i;        // first channel of this lane
-  const bool ch_ok = dl < D;              // D is even: both channels are in or out
+  const bool ch_ok = wave_on && dl < D;   // D is even: both channels are in or out
 
   // Every load of the step is issued first, without branches (out-of-range
   // offsets load zeros): logits, basis rows, x and cache rows.
   // logits of token ta, routes 16 kc + 4 qq + {0..3} (K % 4 == 0: whole words)
-  const Buf ab(alpha, B * K * 2);
   uint32_t lw[KC][2];
+  if constexpr (!FUSED) {
+    const Buf ab(alpha, B * K * 2);
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc) {
-    const int k = 16 * kc + 4 * qq;
-    const uint32_t off = (tok_ok && k < K) ? static_cast<uint32_t>((ta * K + k) * 2) : kOffNone;
-    lw[kc][0] = __builtin_amdgcn_raw_buffer_load_b32(ab.r, static_cast<int>(off), 0, 0);
-    lw[kc][1] = __builtin_amdgcn_raw_buffer_load_b32(ab.r, static_cast<int>(off == kOffNone ? off : off + 4), 0, 0);
+    for (int kc = 0; kc < KC; ++kc) {
+      const int k = 16 * kc + 4 * qq;
+      const uint32_t off = (tok_ok && k < K) ? static_cast<uint32_t>((ta * K + k) * 2) : kOffNone;
+      lw[kc][0] = __builtin_amdgcn_raw_buffer_load_b32(ab.r, static_cast<int>(off), 0, 0);
+      lw[kc][1] = __builtin_amdgcn_raw_buffer_load_b32(ab.r, static_cast<int>(off == kOffNone ? off : off + 4), 0, 0);
+    }
   }
   // basis row (k, s) at this lane's two channels: bw[s][kc][v], k = 16 kc + 4 qq + v
   const Buf bbuf(basis, static_cast<int64_t>(K) * S * D * 2);
@@ -114,14 +121,74 @@ __global__ void __launch_bounds__(256) decode_kernel(
   // routing weights in the A-operand layout, rounded as the forward path rounds
   // them (softmax / exp in fp32, then to bf16)
   float l[KC][4];
+  if constexpr (FUSED) {
+    // logits of tokens tb..tb+15 = z . router^T (bf16-rounded, as the router
+    // GEMM's output): wave w sums the 64-wide z chunks c = w, w + 4, ... of all
+    // 16 tokens (lane (i, qq): columns 64 c + 8 qq + [0, 8) and 64 c + 32 + 8 qq
+    // + [0, 8) of token tb + i and route 16 kc + i); the 4 partial tiles are
+    // summed in LDS in wave order
+    __shared__ float red[4][16 * KC][17];
+    const int64_t rows = (B - tb < 16) ? B - tb : 16;
+    const Buf zb(z + tb * Z, rows * Z * 2);
+    const Buf rb(router, static_cast<int64_t>(K) * Z * 2);
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    f32x4 acc[KC];
 #pragma unroll
-  for (int kc = 0; kc < KC; ++kc)
+    for (int kc = 0; kc < KC; ++kc) acc[kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int nchunk = Z / 64;
+    const uint32_t zrow = static_cast<uint32_t>(i * Z * 2);
+    for (int c0 = wave; c0 < nchunk; c0 += 16) {
+      u32x4 za[4][2], ra[4][KC][2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int k = 16 * kc + 4 * qq + v;
-      l[kc][v] = (tok_ok && k < K) ? bf16_to_f32(static_cast<uint16_t>(lw[kc][v >> 1] >> (16 * (v & 1))))
-                                   : -INFINITY;
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + 4 * u;
+        const bool on = c < nchunk;
+        const uint32_t col0 = static_cast<uint32_t>((64 * c + 8 * qq) * 2), col1 = col0 + 64;
+        za[u][0] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col0 : kOffNone), 0, 0);
+        za[u][1] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col1 : kOffNone), 0, 0);
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+          const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
+          ra[u][kc][0] = __builtin_amdgcn_raw_buffer_load_b128(rb.r, static_cast<int>(on ? rrow + col0 : kOffNone), 0, 0);
+          ra[u][kc][1] = __builtin_amdgcn_raw_buffer_load_b128(rb.r, static_cast<int>(on ? rrow + col1 : kOffNone), 0, 0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            acc[kc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, za[u][h]),
+                                                              __builtin_bit_cast(bf16x8, ra[u][kc][h]),
+                                                              acc[kc], 0, 0, 0);
     }
+    // result lane (j, q): route 16 kc + j, tokens 4 q + v
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][16 * kc + i][4 * qq + v] = acc[kc][v];
+    __syncthreads();
+    if (!wave_on) return;  // no barrier follows
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * kc + 4 * qq + v;
+        const float sv = ((red[0][k][i] + red[1][k][i]) + red[2][k][i]) + red[3][k][i];
+        l[kc][v] = (tok_ok && k < K) ? round_to(sv, DT_BF16) : -INFINITY;
+      }
+  } else {
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * kc + 4 * qq + v;
+        l[kc][v] = (tok_ok && k < K) ? bf16_to_f32(static_cast<uint16_t>(lw[kc][v >> 1] >> (16 * (v & 1))))
+                                     : -INFINITY;
+      }
+  }
   float a[KC][4];
   if (routing == ROUTE_SOFTMAX) {
     float m = -INFINITY;
@@ -218,26 +285,42 @@ __global__ void __launch_bounds__(256) decode_kernel(
   }
 }
 
-template <int S, int KC, bool ACT>
+template <int S, int KC, bool ACT, bool FUSED>
 void launch_one(const void* x, const void* alpha, int routing, const void* basis, void* cache,
-                void* y, int64_t B, int64_t D, int64_t K, hipStream_t st) {
+                void* y, int64_t B, int64_t D, int64_t K, const void* z, const void* router,
+                int64_t Z, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>((D + 4 * 16 * kNC - 1) / (4 * 16 * kNC)),
                   static_cast<unsigned>((B + 15) / 16));
-  hipLaunchKernelGGL((decode_kernel<S, KC, ACT>), grid, dim3(256), 0, st,
+  hipLaunchKernelGGL((decode_kernel<S, KC, ACT, FUSED>), grid, dim3(256), 0, st,
                      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(alpha), routing,
                      static_cast<const uint16_t*>(basis), static_cast<uint16_t*>(cache),
-                     static_cast<uint16_t*>(y), B, D, static_cast<int>(K));
+                     static_cast<uint16_t*>(y), B, D, static_cast<int>(K),
+                     static_cast<const uint16_t*>(z), static_cast<const uint16_t*>(router),
+                     static_cast<int>(Z));
 }
 
-template <int S>
+template <int S, bool FUSED>
 void launch_s(const void* x, const void* alpha, int routing, const void* basis, void* cache,
-              void* y, int64_t B, int64_t D, int64_t K, int act, hipStream_t st) {
+              void* y, int64_t B, int64_t D, int64_t K, int act, const void* z, const void* router,
+              int64_t Z, hipStream_t st) {
   if (K <= 16) {
-    if (act) launch_one<S, 1, true>(x, alpha, routing, basis, cache, y, B, D, K, st);
-    else launch_one<S, 1, false>(x, alpha, routing, basis, cache, y, B, D, K, st);
+    if (act) launch_one<S, 1, true, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+    else launch_one<S, 1, false, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
   } else {
-    if (act) launch_one<S, 2, true>(x, alpha, routing, basis, cache, y, B, D, K, st);
-    else launch_one<S, 2, false>(x, alpha, routing, basis, cache, y, B, D, K, st);
+    if (act) launch_one<S, 2, true, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+    else launch_one<S, 2, false, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+  }
+}
+
+template <bool FUSED>
+void launch_any(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+                void* y, int64_t B, int64_t D, int64_t K, int64_t S, int act, const void* z,
+                const void* router, int64_t Z, hipStream_t st) {
+  switch (S) {
+    case 2: launch_s<2, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 3: launch_s<3, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 4: launch_s<4, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    default: launch_s<8, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
   }
 }
 
@@ -256,12 +339,21 @@ bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int 
 void launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
                    void* y, int64_t B, int64_t D, int64_t K, int64_t S, int activation,
                    hipStream_t st) {
-  switch (S) {
-    case 2: decode::launch_s<2>(x, alpha, routing, basis, cache, y, B, D, K, activation, st); break;
-    case 3: decode::launch_s<3>(x, alpha, routing, basis, cache, y, B, D, K, activation, st); break;
-    case 4: decode::launch_s<4>(x, alpha, routing, basis, cache, y, B, D, K, activation, st); break;
-    default: decode::launch_s<8>(x, alpha, routing, basis, cache, y, B, D, K, activation, st); break;
-  }
+  decode::launch_any<false>(x, alpha, routing, basis, cache, y, B, D, K, S, activation, nullptr,
+                            nullptr, 0, st);
+}
+
+bool decode_step_supported(int64_t B, int64_t D, int64_t Z, int64_t K, int64_t S) {
+  const int64_t lim = int64_t(1) << 31;
+  return decode_supported(B, D, K, S, DT_BF16, DT_BF16, DT_BF16, D * S, S, 1) && Z >= 64 &&
+         Z % 64 == 0 && 16 * Z * 2 < lim && K * Z * 2 < lim;
+}
+
+void launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
+                        void* cache, void* y, int64_t B, int64_t Z, int64_t D, int64_t K,
+                        int64_t S, int activation, int routing, hipStream_t st) {
+  decode::launch_any<true>(x, nullptr, routing, basis, cache, y, B, D, K, S, activation, z, router,
+                           Z, st);
 }
 
 }  // namespace moc

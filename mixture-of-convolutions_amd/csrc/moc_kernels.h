@@ -63,6 +63,12 @@ void launch_decode(const void* x, const void* alpha, int routing, const void* ba
                    void* y, int64_t B, int64_t D, int64_t K, int64_t S, int activation,
                    hipStream_t st);
 
+// decode step with the router GEMM in the same kernel (moc_decode.hip)
+bool decode_step_supported(int64_t B, int64_t D, int64_t Z, int64_t K, int64_t S);
+void launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
+                        void* cache, void* y, int64_t B, int64_t Z, int64_t D, int64_t K,
+                        int64_t S, int activation, int routing, hipStream_t st);
+
 // router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 32, Z % 64 == 0
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt);
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K);

@@ -5,6 +5,7 @@ fallback: if it is missing or fails to load, every MoC op raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -29,6 +30,8 @@ EXPORTED_SYMBOLS = (
     "moc_backward",
     "moc_update",
     "moc_profile_events",
+    "moc_decode_step_supported",
+    "moc_decode_step",
     "moc_router_supported",
     "moc_router_forward",
     "moc_router_backward_workspace_bytes",
@@ -85,6 +88,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_update.restype = _i
     lib.moc_profile_events.argtypes = [_p, _p]
     lib.moc_profile_events.restype = _i
+    lib.moc_decode_step_supported.argtypes = [_l, _l, _l, _l, _l]
+    lib.moc_decode_step_supported.restype = _i
+    lib.moc_decode_step.argtypes = [_p, _p, _p, _p, _p, _p, _l, _l, _l, _l, _l, _i, _i, _p]
+    lib.moc_decode_step.restype = _i
     lib.moc_router_supported.argtypes = [_l, _l, _l, _i]
     lib.moc_router_supported.restype = _i
     lib.moc_router_forward.argtypes = [_p, _p, _p, _l, _l, _l, _i, _p]
@@ -126,5 +133,20 @@ def dtype_code(dt: torch.dtype) -> int:
         raise TypeError(f"libmoc_hip has no kernel operand of dtype {dt}") from None
 
 
+# torch's direct bindings for the current device and stream (a few hundred ns
+# instead of several microseconds per launch); the public calls otherwise
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def device_guard(device: torch.device):
+    """``torch.cuda.device(device)``, or a no-op when it is already current."""
+    if _get_device is not None and (device.index is None or device.index == _get_device()):
+        return contextlib.nullcontext()
+    return torch.cuda.device(device)

@@ -243,7 +243,9 @@ def router_linear(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
     kernels of the HIP library where they apply (bf16, k % 4 == 0, k <= 32,
     z_dim % 64 == 0), torch's GEMM otherwise."""
     if ops.router_supported(z, router):
-        return _RouterLinear.apply(z, router)
+        if torch.is_grad_enabled() and (z.requires_grad or router.requires_grad):
+            return _RouterLinear.apply(z, router)
+        return ops.router_forward(z, router)
     return F.linear(z, router)
 
 
@@ -357,6 +359,17 @@ class MoC(nn.Module):
                 max_seqlen: Optional[int] = None, cu_seqlens_cpu: Optional[torch.Tensor] = None,
                 chunk_indices: Optional[torch.Tensor] = None
                 ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        if (cache is not None and cu_seqlens is None
+                and ops.decode_step_supported(x, z, self.router, self.conv_bases, cache)):
+            # single-token step: router GEMM, router activation and cache update
+            # in one launch (the step is not differentiable, as in the reference)
+            activation_flag(self.activation)
+            if cu_seqlens_cpu is not None or chunk_indices is not None:
+                raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+            y = ops.launch_decode_step(x[:, 0], z[:, 0], self.router, self.conv_bases, cache,
+                                       activation_flag=activation_flag(self.activation),
+                                       routing=_ROUTING_CODES[self.router_activation])
+            return y[:, None], (cache if output_final_state else None)
         logits = router_linear(z, self.router)
         return _dispatch(x, logits, self.conv_bases, cache, output_final_state,
                          self.activation, self.router_activation, cu_seqlens, max_seqlen,

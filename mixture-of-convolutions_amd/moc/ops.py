@@ -133,7 +133,7 @@ def launch_forward(
     x_dt = _lib.dtype_code(x.dtype)
     nbytes = L.moc_forward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
     ws = _workspace(nbytes, x.device)
-    with torch.cuda.device(x.device):
+    with _lib.device_guard(x.device):
         rc = L.moc_forward(
             x.data_ptr(), a.data_ptr(), b.data_ptr(), out.data_ptr(),
             cu_ptr, cu64, n_seqs, n_tokens, seq_len, D, K, S,
@@ -196,7 +196,7 @@ def launch_backward(
     x_dt = _lib.dtype_code(x.dtype)
     nbytes = L.moc_backward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
     ws = _workspace(nbytes, x.device)
-    with torch.cuda.device(x.device):
+    with _lib.device_guard(x.device):
         rc = L.moc_backward(
             x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(),
             None if dx is None else dx.data_ptr(), dalpha.data_ptr(), dbasis.data_ptr(),
@@ -231,7 +231,7 @@ def launch_update(
     B, D = x.shape
     K, S, _ = b.shape
     out = torch.empty_like(x)
-    with torch.cuda.device(x.device):
+    with _lib.device_guard(x.device):
         rc = L.moc_update(
             x.data_ptr(), a.data_ptr(), b.data_ptr(), cache.data_ptr(),
             *cache.stride(), out.data_ptr(), B, D, K, S,
@@ -242,6 +242,9 @@ def launch_update(
     return out
 
 
+_router_support_cache: dict[tuple, bool] = {}
+
+
 def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
     """Whether the router GEMM of ``MoC.forward`` runs on the library's kernels
     (bf16 z and router on a GPU, k % 4 == 0, k <= 32, z_dim % 64 == 0)."""
@@ -250,7 +253,14 @@ def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
     K, Z = router.shape
     if z.shape[-1] != Z or z.numel() == 0:
         return False
-    return bool(_lib.lib().moc_router_supported(z.numel() // Z, Z, K, _lib.DT_BF16))
+    N = z.numel() // Z
+    # the answer depends on N only through the 2^31-byte buffer bound
+    key = (Z, K, N * Z * 2 < (1 << 31))
+    hit = _router_support_cache.get(key)
+    if hit is None:
+        hit = bool(_lib.lib().moc_router_supported(N, Z, K, _lib.DT_BF16))
+        _router_support_cache[key] = hit
+    return hit
 
 
 def router_forward(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
@@ -261,7 +271,7 @@ def router_forward(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
     K, Z = r.shape
     N = z.numel() // Z
     out = torch.empty(*z.shape[:-1], K, dtype=z.dtype, device=z.device)
-    with torch.cuda.device(z.device):
+    with _lib.device_guard(z.device):
         rc = L.moc_router_forward(z.data_ptr(), r.data_ptr(), out.data_ptr(), N, Z, K,
                                   _lib.DT_BF16, _lib.stream_ptr(z.device))
     _lib.check(rc, "moc_router_forward")
@@ -284,7 +294,7 @@ def router_backward(z: torch.Tensor, router: torch.Tensor, dlogits: torch.Tensor
     dr = torch.empty_like(r) if need_router else None
     nbytes = L.moc_router_backward_workspace_bytes(N, Z, K, _lib.DT_BF16) if need_router else 0
     ws = _workspace(nbytes, z.device)
-    with torch.cuda.device(z.device):
+    with _lib.device_guard(z.device):
         rc = L.moc_router_backward(
             z.data_ptr(), r.data_ptr(), dl.data_ptr(),
             None if dz is None else dz.data_ptr(), None if dr is None else dr.data_ptr(),
@@ -292,3 +302,56 @@ def router_backward(z: torch.Tensor, router: torch.Tensor, dlogits: torch.Tensor
             _lib.stream_ptr(z.device))
     _lib.check(rc, "moc_router_backward")
     return dz, dr
+
+
+_step_support_cache: dict[tuple, bool] = {}
+
+
+def decode_step_supported(x: torch.Tensor, z: torch.Tensor, router: torch.Tensor,
+                          basis: torch.Tensor, cache: torch.Tensor) -> bool:
+    """Whether ``launch_decode_step`` applies: bf16 tensors on one GPU, x [B,1,D],
+    z [B,1,Z], contiguous cache [B,D,S], and a shape the kernel is built for."""
+    bf = torch.bfloat16
+    if not (x.is_cuda and x.dtype == bf and z.dtype == bf and router.dtype == bf
+            and basis.dtype == bf and cache.dtype == bf):
+        return False
+    if x.ndim != 3 or z.ndim != 3 or x.shape[1] != 1 or z.shape[:2] != x.shape[:2]:
+        return False
+    B, _, D = x.shape
+    K, S, Db = basis.shape
+    Z = z.shape[2]
+    if Db != D or tuple(router.shape) != (K, Z) or tuple(cache.shape) != (B, D, S):
+        return False
+    if not cache.is_contiguous():
+        return False
+    dev = x.device
+    if z.device != dev or router.device != dev or basis.device != dev or cache.device != dev:
+        return False
+    key = (B, Z, D, K, S)
+    hit = _step_support_cache.get(key)
+    if hit is None:
+        hit = bool(_lib.lib().moc_decode_step_supported(B, Z, D, K, S))
+        _step_support_cache[key] = hit
+    return hit
+
+
+def launch_decode_step(x: torch.Tensor, z: torch.Tensor, router: torch.Tensor,
+                       basis: torch.Tensor, cache: torch.Tensor, *, activation_flag: int,
+                       routing: int) -> torch.Tensor:
+    """One decode step of the MoC layer in one launch: router GEMM, softmax / exp
+    and the cache update (MoC.step, moc/api.py:403-425).  x [B,D], z [B,Z];
+    ``cache`` [B,D,S] contiguous, updated in place; returns y [B,D]."""
+    L = _lib.lib()
+    x = x.contiguous()
+    z = z.contiguous()
+    r = router.contiguous()
+    b = basis.contiguous()
+    B, D = x.shape
+    K, S, _ = b.shape
+    out = torch.empty_like(x)
+    with _lib.device_guard(x.device):
+        rc = L.moc_decode_step(z.data_ptr(), r.data_ptr(), x.data_ptr(), b.data_ptr(),
+                               cache.data_ptr(), out.data_ptr(), B, z.shape[1], D, K, S,
+                               int(activation_flag), int(routing), _lib.stream_ptr(x.device))
+    _lib.check(rc, "moc_decode_step")
+    return out

@@ -234,6 +234,34 @@ def test_decode_kernel_matches_oracle_and_generic(S, K, route):
     assert_close("decode y (mfma vs generic)", got_y, gen_y, torch.bfloat16)
 
 
+@pytest.mark.parametrize("S,K,route,act", [(4, 16, "softmax", "silu"), (2, 8, "exp", None),
+                                              (8, 32, "softmax", None), (3, 20, "exp", "silu")])
+def test_fused_decode_step_matches_router_then_update(S, K, route, act):
+    """MoC.step through the one-launch decode step (router GEMM + activation +
+    update) against the router kernel followed by the update kernel: identical
+    logits, so y and the cache agree bit for bit."""
+    g = gen(S * 31 + K)
+    Bt, D, Z = 45, 260, 192
+    m = MoC(D, Z, S, K, activation=act, init_std=0.1, router_activation=route)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.05))
+    m = m.to(DEV, torch.bfloat16)
+    x = randn(g, Bt, 1, D).to(DEV, torch.bfloat16)
+    z = randn(g, Bt, 1, Z).to(DEV, torch.bfloat16)
+    start = randn(g, Bt, D, S).to(DEV, torch.bfloat16)
+    c1, c2 = start.clone(), start.clone()
+    assert moc.ops.decode_step_supported(x, z, m.router, m.conv_bases, c1)
+    with torch.no_grad():
+        y1, st = m.step(x, z, cache=c1, output_final_state=True)
+        logits = moc.router_linear(z[:, 0], m.router)
+        y2 = moc.ops.launch_update(x[:, 0], logits, m.conv_bases, c2,
+                                   activation_flag=int(act is not None),
+                                   routing=moc.api._ROUTING_CODES[route])[:, None]
+    assert st is c1
+    assert torch.equal(c1, c2)
+    assert torch.equal(y1, y2)
+
+
 def alpha_pad(alpha, S):
     """Routing weights for the S history rows prepended to the steps (their
     outputs are dropped, so any weights do)."""
