@@ -10,7 +10,8 @@ inputs already resident in HBM.  Printed as one JSON line:
   value         tokens/s (millions) of the full layer step (router GEMMs + MoC)
   roofline      HBM roofline of the dominant entry (the fused backward)
   kernel_scope  forward / backward entry times alone (no router GEMMs)
-  decode        configs[3]: batch-256 single-token steps, us/step
+  decode        configs[3]: batch-256 single-token steps, us per MoC.step call and
+                per launch of the one-launch decode step (graph-replayed)
   cpu_baseline  the CPU oracle on a bounded slice of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
@@ -223,27 +224,31 @@ def bench_decode(dev):
             y, _ = m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache, output_final_state=True)
             torch.cuda.synchronize()
             per_step.append((time.perf_counter() - t0) * 1e6)
-        # kernel-only: 32 decode launches captured in one HIP graph, replayed
-        logits = torch.nn.functional.linear(zs[:, 0], m.router)
+        # kernel-only: 32 launches of the one-launch decode step that MoC.step
+        # runs (router GEMM + softmax + update), captured in one HIP graph
         xt = xs[:, 0].contiguous()
+        zt = zs[:, 0].contiguous()
         basis = m.conv_bases.detach()
+        router = m.router.detach()
         scratch = cache.clone()
+        step = lambda: ops.launch_decode_step(xt, zt, router, basis, scratch,  # noqa: E731
+                                              activation_flag=1, routing=ROUTE_SOFTMAX)
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             for _ in range(3):
-                ops.launch_update(xt, logits, basis, scratch, activation_flag=1,
-                                  routing=ROUTE_SOFTMAX)
+                step()
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         n_in_graph = 32
         with torch.cuda.graph(graph):
             for _ in range(n_in_graph):
-                ops.launch_update(xt, logits, basis, scratch, activation_flag=1,
-                                  routing=ROUTE_SOFTMAX)
+                step()
         ms = time_region(graph.replay, 20, 3)
-    kbytes = c["B"] * c["D"] * 2 * (1 + 1 + (c["S"] - 1) + c["S"]) + c["K"] * c["S"] * c["D"] * 2
+    # x, y, cache slots read (S-1) and written (S), z, router, basis
+    kbytes = (c["B"] * c["D"] * 2 * (1 + 1 + (c["S"] - 1) + c["S"]) + c["B"] * c["Z"] * 2
+              + c["K"] * c["Z"] * 2 + c["K"] * c["S"] * c["D"] * 2)
     kernel_us = ms * 1e3 / n_in_graph
     return dict(B=c["B"], D=c["D"], K=c["K"], S=c["S"], prompt=c["prompt"], steps=c["steps"],
                 step_us_median=round(statistics.median(per_step), 2),
