@@ -11,7 +11,10 @@ namespace mfma {
 
 // Tile shapes (see moc_mfma.h): forward NB x NC blocks per wave, 4 waves per
 // workgroup; backward NB x NC per wave, kBwdWPG waves per workgroup.
-constexpr int kFwdNB = 2, kFwdNC = 2;
+#ifndef MOC_FWD_NC
+#define MOC_FWD_NC 2
+#endif
+constexpr int kFwdNB = 2, kFwdNC = MOC_FWD_NC;
 constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
 // Resident workgroups the grids are sized for (256 CUs).
 constexpr int64_t kFwdTargetWG = 2048;
