@@ -97,7 +97,20 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
       a[kc] = 0.f;
     }
     if (live) {
-      for (int64_t p = 0; p < n_da; ++p) {
+      // eight partials' loads in flight at a time; sums in partial order
+      int64_t p = 0;
+      for (; p + 8 <= n_da; p += 8) {
+        float v[8][KC];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc) v[u][kc] = part_da[((p + u) * N + t) * KP + i + 16 * kc];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int kc = 0; kc < KC; ++kc) da[kc] += v[u][kc];
+      }
+      for (; p < n_da; ++p) {
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) da[kc] += part_da[(p * N + t) * KP + i + 16 * kc];
       }
@@ -130,8 +143,17 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
     const int64_t sd = static_cast<int64_t>(S) * D;
     if (idx >= static_cast<int64_t>(K) * sd) return;
     const int64_t k = idx / sd, rest = idx - k * sd;
+    // eight partials' loads in flight at a time; sums in partial order
     float acc = 0.f;
-    for (int64_t p = 0; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
+    int64_t p = 0;
+    for (; p + 8 <= n_db; p += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part_db[((p + u) * KP + k) * sd + rest];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc += v[u];
+    }
+    for (; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
     store_any(dbasis, b_dt, idx, acc);
   }
 }
