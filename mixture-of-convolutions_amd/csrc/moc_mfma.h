@@ -461,7 +461,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 #define MOC_BWD_MIN_WAVES 2
 #endif
 
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT>
 __global__ void __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(MOC_BWD_MIN_WAVES)))
 bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
            const typename CT<BF>::elem* __restrict__ a_c,
@@ -474,6 +474,11 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   using XV = Vec<E, NC>;
   using MS = MSplit<BF>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
+  // route chunks of dbasis / dalpha this workgroup accumulates: all KC, or with
+  // SPLIT the single chunk kc0 = blockIdx.z (W still uses every route)
+  constexpr int KX = SPLIT ? 1 : KC;
+  static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
+  const int kc0 = SPLIT ? static_cast<int>(blockIdx.z) : 0;
   constexpr int EOWN = TB - (S - 1);
   constexpr int NP = MS::kParts;
   constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
@@ -492,10 +497,10 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][NP][BF ? TT::kSlots : 1];
   // dalpha B operands of each wave's channels (bf16, one 16-route chunk): rows
   // (k, s), CW channels; with more routes they stay in registers
-  constexpr bool kBdaLds = BF && KC == 1;
+  constexpr bool kBdaLds = BF && KX == 1;
   constexpr int BROW = CW + 4;
-  __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? KP * S : 1][kBdaLds ? BROW : 1];
-  __shared__ float da_lds[2][WPG][NB][KC][16][17];
+  __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? 16 * KX * S : 1][kBdaLds ? BROW : 1];
+  __shared__ float da_lds[2][WPG][NB][KX][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
   const E* __restrict__ dy = static_cast<const E*>(dyv);
@@ -526,8 +531,6 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 
   // W operands: bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
   Op bop[NC][S][KC];
-  // dalpha B operands: bda[s][cg][kc] = basis[16kc + j, s, d0 + 16cg + 4q + v]
-  Op bda[S][NC][KC];
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -540,28 +543,36 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) bop[c][s][kc] = C::make(rows[0][c], rows[1][c], rows[2][c], rows[3][c]);
+    }
+  }
+  // dalpha B operands: bda[s][cg][kx] = basis[16 (kc0 + kx) + j, s, d0 + 16cg + 4q + v]
+  Op bda[S][NC][KX];
+#pragma unroll
+  for (int kx = 0; kx < KX; ++kx) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
 #pragma unroll
       for (int cg = 0; cg < NC; ++cg) {
         const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
-        bb.load<4 * ESZ>(row_off((16 * kc + j) * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ),
+        bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ),
                                  wave_on && ch < D),
                          e4);
         if constexpr (kBdaLds)  // read back per tap in the dalpha loop (wave-private rows)
-          Vec<E, 4>::store(&b_lds[wave][(16 * kc + j) * S + s][16 * cg + 4 * q], e4);
+          Vec<E, 4>::store(&b_lds[wave][(16 * kx + j) * S + s][16 * cg + 4 * q], e4);
         else
-          bda[s][cg][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+          bda[s][cg][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
       }
     }
   }
 
-  f32x4 dbacc[NC][S][KC];
+  f32x4 dbacc[NC][S][KX];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) dbacc[c][s][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kx = 0; kx < KX; ++kx) dbacc[c][s][kx] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // raw rows of one super-block for this lane: x window, dy rows; alpha rows
   // (AROWS x KP elements, spread over the workgroup's threads) for LDS
@@ -635,11 +646,11 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB + S - 2;
     const bool interior = !cursor.starts_in(seq, w_lo, w_hi);
 
-    f32x4 dacc[NB][KC];
+    f32x4 dacc[NB][KX];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) dacc[b][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kx = 0; kx < KX; ++kx) dacc[b][kx] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto body = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
@@ -699,8 +710,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
         for (int c = 0; c < NC; ++c) gf[e][c] = __shfl(g[e][c], src_lane, 64);
 
-      // dx: taps in ascending order
-      if (dx != nullptr) {
+      // dx: taps in ascending order (with SPLIT, by the kc0 = 0 workgroups only)
+      if (dx != nullptr && kc0 == 0) {
         float dxa[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -748,8 +759,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       }
 
       // alpha^T operands of the dbasis MFMA (zero for rows that are not this
-      // super-block's own): at[b][kc][v] = alpha[trun + 4b + v, 16kc + j]
-      Op at[NB][KC];
+      // super-block's own): at[b][kx][v] = alpha[trun + 4b + v, 16 (kc0 + kx) + j]
+      Op at[NB][KX];
       if constexpr (BF) {
         // transposed read: supplier lane 4e + a of each 16-lane group holds the
         // 4 routing weights 16kc + 4a.. of row R q + 4b + e (ds_read_b64_tr_b16)
@@ -759,23 +770,23 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
           const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
           const uint64_t keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc) {
-            const Op v = TT::read(&a_lds[buf][R * q + 4 * b + (j >> 2)][16 * kc + 4 * (j & 3)]);
-            at[b][kc] = __builtin_bit_cast(Op, __builtin_bit_cast(uint64_t, v) & keep);
+          for (int kx = 0; kx < KX; ++kx) {
+            const Op v = TT::read(&a_lds[buf][R * q + 4 * b + (j >> 2)][16 * (kc0 + kx) + 4 * (j & 3)]);
+            at[b][kx] = __builtin_bit_cast(Op, __builtin_bit_cast(uint64_t, v) & keep);
           }
         }
       } else {
 #pragma unroll
         for (int b = 0; b < NB; ++b)
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc) {
+          for (int kx = 0; kx < KX; ++kx) {
             E e4[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int row = R * q + 4 * b + v;
-              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * kc + j] : E(0);
+              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * (kc0 + kx) + j] : E(0);
             }
-            at[b][kc] = C::make(e4[0], e4[1], e4[2], e4[3]);
+            at[b][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
           }
       }
       // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
@@ -816,9 +827,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
                 m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
               }
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) {
-                dbacc[c][s][kc] = mma32(mh[0], mh[1], at[b2][kc], at[b2 + 1][kc], dbacc[c][s][kc]);
-                dbacc[c][s][kc] = mma32(ml[0], ml[1], at[b2][kc], at[b2 + 1][kc], dbacc[c][s][kc]);
+              for (int kx = 0; kx < KX; ++kx) {
+                dbacc[c][s][kx] = mma32(mh[0], mh[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
+                dbacc[c][s][kx] = mma32(ml[0], ml[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
               }
             }
           }
@@ -836,15 +847,15 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
               for (int cg = 0; cg < 2; ++cg)
                 ra[rb][h][cg] = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
           // dalpha B operands of tap s: basis[16 kc + j][s][16 cg + 4 q + {0..3}]
-          Op bs[KC][2];
+          Op bs[KX][2];
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc)
+          for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
             for (int cg = 0; cg < 2; ++cg) {
               if constexpr (kBdaLds)
-                bs[kc][cg] = *reinterpret_cast<const Op*>(&b_lds[wave][(16 * kc + j) * S + s][16 * cg + 4 * q]);
+                bs[kx][cg] = *reinterpret_cast<const Op*>(&b_lds[wave][(16 * kx + j) * S + s][16 * cg + 4 * q]);
               else
-                bs[kc][cg] = bda[s][cg][kc];
+                bs[kx][cg] = bda[s][cg][kx];
             }
           // keep the reads ahead of the next tap's VALU work
           __builtin_amdgcn_sched_barrier(0);
@@ -855,8 +866,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
             for (int h = 0; h < NP; ++h)
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc)
-                dacc[rb][kc] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kc][0], bs[kc][1], dacc[rb][kc]);
+              for (int kx = 0; kx < KX; ++kx)
+                dacc[rb][kx] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kx][0], bs[kx][1], dacc[rb][kx]);
         }
         wave_lds_sync();
       } else {
@@ -885,7 +896,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int c = 0; c < NC; ++c) {
               const Op am = C::make(mv[h][0][c], mv[h][1][c], mv[h][2][c], mv[h][3][c]);
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) dbacc[c][s][kc] = C::mma(am, at[b][kc], dbacc[c][s][kc]);
+              for (int kx = 0; kx < KX; ++kx) dbacc[c][s][kx] = C::mma(am, at[b][kx], dbacc[c][s][kx]);
             }
         }
         wave_lds_sync();
@@ -898,7 +909,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             for (int cg = 0; cg < NC; ++cg) {
               const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][h][16 * rb + j][16 * cg + 4 * q]);
 #pragma unroll
-              for (int kc = 0; kc < KC; ++kc) dacc[rb][kc] = C::mma(am, bda[s][cg][kc], dacc[rb][kc]);
+              for (int kx = 0; kx < KX; ++kx) dacc[rb][kx] = C::mma(am, bda[s][cg][kx], dacc[rb][kx]);
             }
         wave_lds_sync();
       }
@@ -915,30 +926,31 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
     for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc)
+      for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kc][4 * q + v][j] = dacc[rb][kc][v];
+        for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
     if (more) stage_alpha(buf ^ 1);
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
-    for (int idx = tid; idx < NB * KC * 256; idx += 64 * WPG) {
-      const int rb = idx / (KC * 256);
-      const int kc = (idx / 256) % KC;
+    for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
+      const int rb = idx / (KX * 256);
+      const int kx = (idx / 256) % KX;
       const int row = (idx >> 4) & 15, col = idx & 15;
       float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kc][row][col];
+      for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kx][row][col];
       const int64_t t = t0 + 16 * rb + row;
-      if (t < own_end) part_da[(static_cast<int64_t>(blockIdx.x) * N + t) * KP + 16 * kc + col] = sum;
+      if (t < own_end)
+        part_da[(static_cast<int64_t>(blockIdx.x) * N + t) * KP + 16 * (kc0 + kx) + col] = sum;
     }
   }
 
-  // this workgroup's dbasis partial: dbacc[c][s][kc][v] is
-  // (k = 16kc + j, s, channel d0 + NC (4q + v) + c)
+  // this workgroup's dbasis partial: dbacc[c][s][kx][v] is
+  // (k = 16 (kc0 + kx) + j, s, channel d0 + NC (4q + v) + c)
   if (wave_on) {
     const int64_t base = static_cast<int64_t>(blockIdx.y) * KP;
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
+    for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
       for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -947,7 +959,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
           for (int c = 0; c < NC; ++c) {
             const int64_t ch = d0 + NC * (4 * q + v) + c;
             if (ch < D)
-              part_db[((base + 16 * kc + j) * S + s) * D + ch] = dbacc[c][s][kc][v];
+              part_db[((base + 16 * (kc0 + kx) + j) * S + s) * D + ch] = dbacc[c][s][kx][v];
           }
   }
 }

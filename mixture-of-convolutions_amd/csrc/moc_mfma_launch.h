@@ -61,14 +61,19 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
                      g.n_sb);
 }
 
+// With 32 routes (bf16) each workgroup accumulates dbasis / dalpha for one of
+// the two 16-route chunks (grid.z): the accumulators and dalpha operands of
+// both would not fit in registers beside the W operands.
 template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
              void* dx, float* part_da, float* part_db, hipStream_t st) {
   using E = typename CT<BF>::elem;
+  constexpr bool kSplit = BF && KC == 2;
   const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
-  hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF>), dim3(g.gx, g.gy),
-                     dim3(64 * kBwdWPG), 0, st, x, dy, static_cast<const E*>(a_c),
-                     static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D, g.n_sb);
+  hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit>),
+                     dim3(g.gx, g.gy, kSplit ? KC : 1), dim3(64 * kBwdWPG), 0, st, x, dy,
+                     static_cast<const E*>(a_c), static_cast<const E*>(b_c), dx, part_da, part_db,
+                     p.seq, p.D, g.n_sb);
 }
 
 // Dispatch over (KC, activation, dtype) for one S.
