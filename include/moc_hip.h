@@ -17,7 +17,7 @@
  *     moc_last_error() then returns a message (thread-local).
  *
  * Math (tap s = S-1 multiplies the current token, moc/reference.py:29-32):
- *   alpha[n,k] = alpha_in[n,k]            (MOC_ROUTE_ALPHA)
+ *   alpha[n,k] = alpha_in[n,k]            (MOC_ROUTE_ALPHA, *_WEIGHTS)
  *              = softmax_k(logits[n,:])    (MOC_ROUTE_SOFTMAX)
  *              = exp(logits[n,k])          (MOC_ROUTE_EXP)
  *   P[n,d] = sum_s x[n-(S-1-s), d] * sum_k alpha[n,k] * basis[k,s,d]
@@ -39,11 +39,17 @@ extern "C" {
 #define MOC_DT_BF16 1
 #define MOC_DT_F16  2
 
-/* what the `alpha` argument holds: routing weights, or router logits whose
- * activation (softmax / exp, moc/api.py:383-388) is fused into the kernels */
-#define MOC_ROUTE_ALPHA   0
-#define MOC_ROUTE_SOFTMAX 1
-#define MOC_ROUTE_EXP     2
+/* what the `alpha` argument holds: routing weights (ALPHA); router logits whose
+ * activation (softmax / exp, moc/api.py:383-388) is fused into the kernels
+ * (SOFTMAX, EXP); or weights that already are that activation of the logits,
+ * e.g. from moc_router_forward_routed (SOFTMAX_WEIGHTS, EXP_WEIGHTS): the
+ * forward uses them as given and the backward's dalpha is d/dlogits, the
+ * activation gradient formed from the given weights */
+#define MOC_ROUTE_ALPHA           0
+#define MOC_ROUTE_SOFTMAX         1
+#define MOC_ROUTE_EXP             2
+#define MOC_ROUTE_SOFTMAX_WEIGHTS 3
+#define MOC_ROUTE_EXP_WEIGHTS     4
 
 /* status codes */
 #define MOC_OK             0
@@ -101,7 +107,8 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
  * _moc_bwd_dalpha_dbasis_dot_kernel (moc/kernels.py:282-439).
  *   dx     : [n_tokens, dim] in x_dtype, or NULL to skip it (need_x = False)
  *   dalpha : [n_tokens, k] in alpha_dtype; d/dalpha for MOC_ROUTE_ALPHA, or
- *            d/dlogits with the softmax / exp gradient fused in
+ *            d/dlogits with the softmax / exp gradient fused in (routing 1-4;
+ *            with *_WEIGHTS: softmax a (g - <a, g>), exp a g, a = alpha)
  *   dbasis : [k, kernel_size, dim] in basis_dtype
  * dbasis and dalpha are reduced in a fixed order: results are bitwise
  * reproducible run to run (the reference used relaxed fp32 atomics).
@@ -162,6 +169,19 @@ int moc_decode_step(const void* z, const void* router, const void* x, const void
 int moc_router_supported(int64_t n_tokens, int64_t z_dim, int64_t k, int dtype);
 int moc_router_forward(const void* z, const void* router, void* logits, int64_t n_tokens,
                        int64_t z_dim, int64_t k, int dtype, void* stream);
+
+/*
+ * The router forward with the router activation of MoC.forward
+ * (moc/api.py:383-388: torch.softmax / torch.exp of the logits) fused in:
+ * weights = softmax_k(logits) (routing 1) or exp(logits) (routing 2), formed
+ * from the bf16 logits and rounded to bf16, as torch forms them.  The weights
+ * feed moc_forward / moc_backward with routing MOC_ROUTE_SOFTMAX_WEIGHTS /
+ * MOC_ROUTE_EXP_WEIGHTS, whose dalpha is then the logits gradient for
+ * moc_router_backward.
+ *   weights : [n_tokens, k] bf16
+ */
+int moc_router_forward_routed(const void* z, const void* router, void* weights, int64_t n_tokens,
+                              int64_t z_dim, int64_t k, int dtype, int routing, void* stream);
 
 /* Workspace bytes moc_router_backward needs when drouter is requested. */
 size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,

@@ -54,8 +54,8 @@ int check_common(int x_dt, int a_dt, int b_dt, int activation, int routing) {
   if (!dt_ok(b_dt)) return fail(MOC_ERR_DTYPE, "unsupported basis dtype code %d", b_dt);
   if (activation != 0 && activation != 1)
     return fail(MOC_ERR_ARG, "activation must be 0 or 1, got %d", activation);
-  if (routing < MOC_ROUTE_ALPHA || routing > MOC_ROUTE_EXP)
-    return fail(MOC_ERR_ARG, "routing must be 0, 1 or 2, got %d", routing);
+  if (routing < MOC_ROUTE_ALPHA || routing > MOC_ROUTE_EXP_WEIGHTS)
+    return fail(MOC_ERR_ARG, "routing must be 0, 1, 2, 3 or 4, got %d", routing);
   return MOC_OK;
 }
 
@@ -249,7 +249,7 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   if (!force_generic && moc::decode_supported(batch, dim, k, kernel_size, x_dtype, alpha_dtype,
                                               basis_dtype, cache_stride_b, cache_stride_d,
                                               cache_stride_s)) {
-    moc::launch_decode(x, alpha, routing, basis, cache, y, batch, dim, k, kernel_size, activation,
+    moc::launch_decode(x, alpha, moc::route_form(routing), basis, cache, y, batch, dim, k, kernel_size, activation,
                        static_cast<hipStream_t>(stream));
     return hip_status("moc_update launch");
   }
@@ -299,8 +299,25 @@ int moc_router_forward(const void* z, const void* router, void* logits, int64_t 
                 (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
   if (!z || !router || !logits) return fail(MOC_ERR_ARG, "null tensor pointer");
   if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
-  moc::router_forward(z, router, logits, n_tokens, z_dim, k, static_cast<hipStream_t>(stream));
+  moc::router_forward(z, router, logits, n_tokens, z_dim, k, moc::ROUTE_ALPHA,
+                      static_cast<hipStream_t>(stream));
   return hip_status("moc_router_forward launch");
+}
+
+int moc_router_forward_routed(const void* z, const void* router, void* weights, int64_t n_tokens,
+                              int64_t z_dim, int64_t k, int dtype, int routing, void* stream) {
+  g_err[0] = '\0';
+  if (!moc::router_supported(n_tokens, z_dim, k, dtype))
+    return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
+                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
+  if (routing != MOC_ROUTE_SOFTMAX && routing != MOC_ROUTE_EXP)
+    return fail(MOC_ERR_ARG, "routing must be softmax (1) or exp (2), got %d", routing);
+  if (!z || !router || !weights) return fail(MOC_ERR_ARG, "null tensor pointer");
+  if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
+  moc::router_forward(z, router, weights, n_tokens, z_dim, k, routing,
+                      static_cast<hipStream_t>(stream));
+  return hip_status("moc_router_forward_routed launch");
 }
 
 size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,

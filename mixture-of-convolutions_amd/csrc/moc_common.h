@@ -7,7 +7,21 @@
 namespace moc {
 
 enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
-enum Route : int { ROUTE_ALPHA = 0, ROUTE_SOFTMAX = 1, ROUTE_EXP = 2 };
+// What `alpha` holds: weights (ROUTE_ALPHA); logits whose softmax / exp the
+// kernels form (ROUTE_SOFTMAX / ROUTE_EXP); or weights that already are the
+// softmax / exp of the logits (ROUTE_SOFTMAX_W / ROUTE_EXP_W), used as they are
+// in the forward, with the backward's dalpha the logits gradient.
+enum Route : int {
+  ROUTE_ALPHA = 0,
+  ROUTE_SOFTMAX = 1,
+  ROUTE_EXP = 2,
+  ROUTE_SOFTMAX_W = 3,
+  ROUTE_EXP_W = 4
+};
+// activation the kernels apply to alpha before the mixture
+__host__ __device__ inline int route_form(int r) { return r >= ROUTE_SOFTMAX_W ? ROUTE_ALPHA : r; }
+// activation whose gradient the backward applies to dalpha
+__host__ __device__ inline int route_grad(int r) { return r >= ROUTE_SOFTMAX_W ? r - 2 : r; }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);

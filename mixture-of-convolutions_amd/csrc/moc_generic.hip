@@ -311,7 +311,7 @@ static inline unsigned grid_for(int64_t total, int threads, int64_t cap = 65536)
 void launch_prep(const Problem& p, const void* alpha, const void* basis, float* a_r,
                  float* basis_c, hipStream_t st) {
   hipLaunchKernelGGL(prep_alpha_kernel, dim3(grid_for(p.n_tokens, 256, 1LL << 30)), dim3(256),
-                     0, st, alpha, p.a_dt, p.routing, p.n_tokens, p.K, a_r);
+                     0, st, alpha, p.a_dt, route_form(p.routing), p.n_tokens, p.K, a_r);
   const int64_t nb = p.K * p.S * p.D;
   hipLaunchKernelGGL(prep_basis_kernel, dim3(grid_for(nb, 256, 1LL << 30)), dim3(256), 0, st,
                      basis, p.b_dt, nb, p.x_dt, basis_c);
@@ -343,7 +343,8 @@ void launch_backward_generic(const Problem& p, const void* x, const void* dy, vo
   }
   hipLaunchKernelGGL(bwd_dalpha_kernel, dim3(static_cast<unsigned>(p.n_tokens)),
                      dim3(kRedThreads), static_cast<size_t>(p.K) * sizeof(float), st, x, p.x_dt,
-                     g, a_r, basis_c, dalpha, p.a_dt, p.routing, p.seq, p.D, p.K, p.S);
+                     g, a_r, basis_c, dalpha, p.a_dt, route_grad(p.routing), p.seq, p.D, p.K,
+                     p.S);
   hipLaunchKernelGGL(bwd_dbasis_partial_kernel,
                      dim3(static_cast<unsigned>((p.D + 255) / 256), static_cast<unsigned>(n_chunks)),
                      dim3(256), 0, st, x, p.x_dt, g, a_r, part, p.seq, p.D, p.K, p.S);
@@ -358,7 +359,7 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int activation, int routing, hipStream_t st) {
   dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(B));
   hipLaunchKernelGGL(update_kernel, grid, dim3(256), static_cast<size_t>(K) * sizeof(float), st,
-                     x, alpha, a_dt, routing, basis, b_dt, cache, cs_b, cs_d, cs_s, y, x_dt, D, K,
+                     x, alpha, a_dt, route_form(routing), basis, b_dt, cache, cs_b, cs_d, cs_s, y, x_dt, D, K,
                      S, activation);
 }
 

@@ -72,8 +72,10 @@ void launch_decode_step(const void* z, const void* router, const void* x, const 
 // router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 32, Z % 64 == 0
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt);
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K);
-void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
-                    hipStream_t st);
+// routing ROUTE_ALPHA: out = the bf16 logits; ROUTE_SOFTMAX / ROUTE_EXP: out =
+// that activation of the bf16 logits, rounded to bf16
+void router_forward(const void* z, const void* r, void* out, int64_t N, int64_t Z, int64_t K,
+                    int routing, hipStream_t st);
 void router_backward(const void* z, const void* r, const void* dl, void* dz, void* dr,
                      int64_t N, int64_t Z, int64_t K, void* workspace, hipStream_t st);
 

@@ -1,4 +1,6 @@
 // MFMA path: operand preparation, backward stage 2, workspace plans, dispatch.
+#include <cstdlib>
+
 #include "moc_mfma_launch.h"
 
 namespace moc {
@@ -17,6 +19,7 @@ __global__ void __launch_bounds__(256)
 prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* __restrict__ basis,
             int b_dt, int64_t N, int K, int S, int64_t D, typename CT<BF>::elem* __restrict__ a_c,
             float* __restrict__ a_r, typename CT<BF>::elem* __restrict__ b_c, int64_t a_blocks) {
+  // routing is route_form of the caller's code; a_r (if not null) receives the weights
   using C = CT<BF>;
   using E = typename C::elem;
   constexpr int KP = 16 * KC;
@@ -60,7 +63,7 @@ prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* _
     for (int kc = 0; kc < KC; ++kc) {
       const int k = i + 16 * kc;
       a_c[t * KP + k] = C::from_f(v[kc]);
-      if (routing != ROUTE_ALPHA && k < K) a_r[t * K + k] = v[kc];
+      if (a_r != nullptr && k < K) a_r[t * K + k] = v[kc];
     }
   } else {
     const int64_t idx = (static_cast<int64_t>(blockIdx.x) - a_blocks) * 256 + threadIdx.x;
@@ -69,6 +72,28 @@ prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* _
     const int64_t k = idx / sd;
     b_c[idx] = (k < K) ? C::from_f(load_any(basis, b_dt, idx)) : E(0);
   }
+}
+
+// dbasis element idx (of K S D) = sum of the n_db token partials in order.
+template <int KP>
+__device__ __forceinline__ void stage2_db(const float* __restrict__ part_db, int64_t n_db,
+                                          void* __restrict__ dbasis, int b_dt, int K, int S,
+                                          int64_t D, int64_t idx) {
+  const int64_t sd = static_cast<int64_t>(S) * D;
+  if (idx >= static_cast<int64_t>(K) * sd) return;
+  const int64_t k = idx / sd, rest = idx - k * sd;
+  // eight partials' loads in flight at a time; sums in partial order
+  float acc = 0.f;
+  int64_t p = 0;
+  for (; p + 8 <= n_db; p += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part_db[((p + u) * KP + k) * sd + rest];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc += v[u];
+  }
+  for (; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
+  store_any(dbasis, b_dt, idx, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -82,9 +107,11 @@ prep_kernel(const void* __restrict__ alpha, int a_dt, int routing, const void* _
 template <int KC>
 __global__ void __launch_bounds__(256)
 stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __restrict__ part_db,
-              int64_t n_db, const float* __restrict__ a_r, void* __restrict__ dalpha, int a_dt,
-              int routing, void* __restrict__ dbasis, int b_dt, int64_t N, int K, int S,
-              int64_t D, int64_t da_blocks) {
+              int64_t n_db, const float* __restrict__ a_r, const uint16_t* __restrict__ a_w,
+              void* __restrict__ dalpha, int a_dt, int routing, void* __restrict__ dbasis,
+              int b_dt, int64_t N, int K, int S, int64_t D, int64_t da_blocks) {
+  // the weights of the activation gradient: a_r (fp32) or, if a_r is null,
+  // a_w (the caller's bf16 weights)
   constexpr int KP = 16 * KC;
   if (static_cast<int64_t>(blockIdx.x) < da_blocks) {
     const int64_t t = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
@@ -116,8 +143,10 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
       }
       if (routing != ROUTE_ALPHA) {
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc)
-          if (i + 16 * kc < K) a[kc] = a_r[t * K + i + 16 * kc];
+        for (int kc = 0; kc < KC; ++kc) {
+          const int64_t at = t * K + i + 16 * kc;
+          if (i + 16 * kc < K) a[kc] = (a_r != nullptr) ? a_r[at] : bf16_to_f32(a_w[at]);
+        }
       }
     }
     float dot = 0.f;
@@ -139,22 +168,8 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
       }
     }
   } else {
-    const int64_t idx = (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x;
-    const int64_t sd = static_cast<int64_t>(S) * D;
-    if (idx >= static_cast<int64_t>(K) * sd) return;
-    const int64_t k = idx / sd, rest = idx - k * sd;
-    // eight partials' loads in flight at a time; sums in partial order
-    float acc = 0.f;
-    int64_t p = 0;
-    for (; p + 8 <= n_db; p += 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = part_db[((p + u) * KP + k) * sd + rest];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc += v[u];
-    }
-    for (; p < n_db; ++p) acc += part_db[(p * KP + k) * sd + rest];
-    store_any(dbasis, b_dt, idx, acc);
+    stage2_db<KP>(part_db, n_db, dbasis, b_dt, K, S, D,
+                  (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x);
   }
 }
 
@@ -173,6 +188,20 @@ struct Plan {
   Grid2 bg;
 };
 
+// The kernels read the caller's weights and basis in place when both already
+// have the operand layout: weights given (no activation to form), bf16
+// everywhere, K = 16 (no padded routes) and 16-byte aligned rows; then no prep
+// launch runs.  The workspace is sized for the prep path either way, since its
+// size is asked for without the pointers.
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+bool direct(const Problem& p, const void* alpha, const void* basis, const void* dalpha) {
+  static const bool prep_forced = std::getenv("MOC_MFMA_PREP") != nullptr;
+  return !prep_forced && route_form(p.routing) == ROUTE_ALPHA && p.x_dt == DT_BF16 &&
+         p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && p.K == 16 && aligned16(alpha) &&
+         aligned16(basis) && aligned16(dalpha);
+}
+
 Plan plan(const Problem& p, bool backward) {
   Plan pl{};
   pl.KP = static_cast<int>(16 * ((p.K + 15) / 16));
@@ -183,7 +212,7 @@ Plan plan(const Problem& p, bool backward) {
   pl.off_bc = off;
   off += al(static_cast<size_t>(pl.KP) * p.S * p.D * pl.esz);
   pl.off_ar = off;
-  if (p.routing != ROUTE_ALPHA) off += al(static_cast<size_t>(p.n_tokens) * p.K * 4);
+  if (route_grad(p.routing) != ROUTE_ALPHA) off += al(static_cast<size_t>(p.n_tokens) * p.K * 4);
   if (backward) {
     pl.bg = bwd_grid(p.n_tokens, p.D, p.S);
     pl.off_pda = off;
@@ -197,27 +226,29 @@ Plan plan(const Problem& p, bool backward) {
 
 template <bool BF, int KC>
 void prep_one(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
-              hipStream_t st) {
+              bool keep_ar, hipStream_t st) {
   using E = typename CT<BF>::elem;
   const int64_t a_blocks = cdiv(p.n_tokens * 16, 256);
   const int64_t b_blocks = cdiv(static_cast<int64_t>(pl.KP) * p.S * p.D, 256);
-  float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<float*>(ws + pl.off_ar) : nullptr;
+  float* a_r = (keep_ar && route_grad(p.routing) != ROUTE_ALPHA)
+                  ? reinterpret_cast<float*>(ws + pl.off_ar) : nullptr;
   hipLaunchKernelGGL((prep_kernel<BF, KC>), dim3(static_cast<unsigned>(a_blocks + b_blocks)),
-                     dim3(256), 0, st, alpha, p.a_dt, p.routing, basis, p.b_dt, p.n_tokens,
+                     dim3(256), 0, st, alpha, p.a_dt, route_form(p.routing), basis, p.b_dt, p.n_tokens,
                      static_cast<int>(p.K), static_cast<int>(p.S), p.D,
                      reinterpret_cast<E*>(ws + pl.off_ac), a_r, reinterpret_cast<E*>(ws + pl.off_bc),
                      a_blocks);
 }
 
+// keep_ar: also store the weights in fp32 for stage 2's activation gradient
 void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void* basis, char* ws,
-                 hipStream_t st) {
+                 bool keep_ar, hipStream_t st) {
   const bool bf = p.x_dt == DT_BF16;
   if (pl.KP == 16) {
-    if (bf) prep_one<true, 1>(p, pl, alpha, basis, ws, st);
-    else prep_one<false, 1>(p, pl, alpha, basis, ws, st);
+    if (bf) prep_one<true, 1>(p, pl, alpha, basis, ws, keep_ar, st);
+    else prep_one<false, 1>(p, pl, alpha, basis, ws, keep_ar, st);
   } else {
-    if (bf) prep_one<true, 2>(p, pl, alpha, basis, ws, st);
-    else prep_one<false, 2>(p, pl, alpha, basis, ws, st);
+    if (bf) prep_one<true, 2>(p, pl, alpha, basis, ws, keep_ar, st);
+    else prep_one<false, 2>(p, pl, alpha, basis, ws, keep_ar, st);
   }
 }
 
@@ -236,9 +267,14 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
              void* workspace, hipStream_t st) {
   const Plan pl = plan(p, false);
   char* ws = static_cast<char*>(workspace);
-  launch_prep(p, pl, alpha, basis, ws, st);
-  const void* a_c = ws + pl.off_ac;
-  const void* b_c = ws + pl.off_bc;
+  const bool dir = direct(p, alpha, basis, nullptr);
+  const void* a_c = alpha;
+  const void* b_c = basis;
+  if (!dir) {
+    launch_prep(p, pl, alpha, basis, ws, false, st);
+    a_c = ws + pl.off_ac;
+    b_c = ws + pl.off_bc;
+  }
   prof_begin(p, st);
   switch (p.S) {
     case 2: launch_fwd<2>(p, x, a_c, b_c, y, st); break;
@@ -255,9 +291,14 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
               hipStream_t st) {
   const Plan pl = plan(p, true);
   char* ws = static_cast<char*>(workspace);
-  launch_prep(p, pl, alpha, basis, ws, st);
-  const void* a_c = ws + pl.off_ac;
-  const void* b_c = ws + pl.off_bc;
+  const bool dir = direct(p, alpha, basis, dalpha);
+  const void* a_c = alpha;
+  const void* b_c = basis;
+  if (!dir) {
+    launch_prep(p, pl, alpha, basis, ws, true, st);
+    a_c = ws + pl.off_ac;
+    b_c = ws + pl.off_bc;
+  }
   float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
   float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
   prof_begin(p, st);
@@ -269,20 +310,24 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     default: break;
   }
   prof_end(p, st);
-  const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
   const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
-  const float* a_r = (p.routing != ROUTE_ALPHA) ? reinterpret_cast<const float*>(ws + pl.off_ar)
-                                                : nullptr;
+  const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
+  const int grad = route_grad(p.routing);
+  // weights for the activation gradient: prep's fp32 copy, or the caller's
+  // bf16 weights read in place
+  const float* a_r = (grad != ROUTE_ALPHA && !dir)
+                         ? reinterpret_cast<const float*>(ws + pl.off_ar) : nullptr;
+  const auto* a_w = static_cast<const uint16_t*>(alpha);
   const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
   if (pl.KP == 16) {
     hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda,
                        static_cast<int64_t>(pl.bg.gx), pdb, static_cast<int64_t>(pl.bg.gy), a_r,
-                       dalpha, p.a_dt, p.routing, dbasis, p.b_dt, p.n_tokens,
+                       a_w, dalpha, p.a_dt, grad, dbasis, p.b_dt, p.n_tokens,
                        static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
   } else {
     hipLaunchKernelGGL(stage2_kernel<2>, grid, dim3(256), 0, st, pda,
                        static_cast<int64_t>(pl.bg.gx), pdb, static_cast<int64_t>(pl.bg.gy), a_r,
-                       dalpha, p.a_dt, p.routing, dbasis, p.b_dt, p.n_tokens,
+                       a_w, dalpha, p.a_dt, grad, dbasis, p.b_dt, p.n_tokens,
                        static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
   }
 }

@@ -17,7 +17,10 @@ namespace mfma {
 constexpr int kFwdNB = 2, kFwdNC = MOC_FWD_NC;
 constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
 // Resident workgroups the grids are sized for (256 CUs).
-constexpr int64_t kFwdTargetWG = 2048;
+#ifndef MOC_FWD_TARGET_WG
+#define MOC_FWD_TARGET_WG 2048
+#endif
+constexpr int64_t kFwdTargetWG = MOC_FWD_TARGET_WG;
 #ifndef MOC_BWD_TARGET_WG
 #define MOC_BWD_TARGET_WG 512
 #endif

@@ -56,7 +56,7 @@ template <int KC>
 __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restrict__ z,
                                                          const uint16_t* __restrict__ r,
                                                          uint16_t* __restrict__ logits,
-                                                         int64_t N, int Z, int K) {
+                                                         int64_t N, int Z, int K, int routing) {
   constexpr int KP = 16 * KC;
   __shared__ float red[4][2][KP][17];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -112,10 +112,30 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[w][h][16 * kc + i][4 * qq + v] = acc[h][kc][v];
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * KP; idx += 256) {
+  // KP consecutive lanes hold one token's routes; every lane runs every pass
+  // (the shuffles of the routing need all of them)
+#pragma unroll
+  for (int pass = 0; pass < 32 * KP / 256; ++pass) {
+    const int idx = threadIdx.x + 256 * pass;
     const int tok = idx / KP, k = idx % KP, h = tok >> 4, tr = tok & 15;
     const float s = ((red[0][h][k][tr] + red[1][h][k][tr]) + red[2][h][k][tr]) + red[3][h][k][tr];
-    if (k < K && tok < rows) logits[(t0 + tok) * K + k] = f32_to_bf16(s);
+    float v = round_to(s, DT_BF16);
+    if (routing == ROUTE_SOFTMAX) {
+      // softmax of the bf16 logits over the token's KP lanes (routes >= K
+      // excluded), rounded to bf16
+      const float l = (k < K) ? v : -INFINITY;
+      float m = l;
+#pragma unroll
+      for (int o = KP / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const float e = (k < K) ? __expf(l - m) : 0.f;
+      float sum = e;
+#pragma unroll
+      for (int o = KP / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      v = round_to(e * (1.0f / sum), DT_BF16);
+    } else if (routing == ROUTE_EXP) {
+      v = round_to(__expf(v), DT_BF16);
+    }
+    if (k < K && tok < rows) logits[(t0 + tok) * K + k] = f32_to_bf16(v);
   }
 }
 
@@ -362,17 +382,17 @@ size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
 }
 
 void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
-                    hipStream_t st) {
+                    int routing, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(router::cdiv(N, 32)));
   const auto* zp = static_cast<const uint16_t*>(z);
   const auto* rp = static_cast<const uint16_t*>(r);
   auto* lp = static_cast<uint16_t*>(logits);
   if (K <= 16)
     hipLaunchKernelGGL(router::router_fwd_kernel<1>, grid, dim3(256), 0, st, zp, rp, lp, N,
-                       static_cast<int>(Z), static_cast<int>(K));
+                       static_cast<int>(Z), static_cast<int>(K), routing);
   else
     hipLaunchKernelGGL(router::router_fwd_kernel<2>, grid, dim3(256), 0, st, zp, rp, lp, N,
-                       static_cast<int>(Z), static_cast<int>(K));
+                       static_cast<int>(Z), static_cast<int>(K), routing);
 }
 
 void router_backward(const void* z, const void* r, const void* dl, void* dz, void* dr,

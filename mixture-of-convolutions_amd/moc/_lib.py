@@ -18,6 +18,8 @@ LIB_PATH = Path(os.environ.get("MOC_HIP_LIB") or Path(__file__).resolve().parent
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
+# alpha holds softmax / exp weights already; the backward returns d/dlogits
+ROUTE_SOFTMAX_WEIGHTS, ROUTE_EXP_WEIGHTS = 3, 4
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float16: DT_F16}
 
@@ -34,6 +36,7 @@ EXPORTED_SYMBOLS = (
     "moc_decode_step",
     "moc_router_supported",
     "moc_router_forward",
+    "moc_router_forward_routed",
     "moc_router_backward_workspace_bytes",
     "moc_router_backward",
 )
@@ -96,6 +99,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_router_supported.restype = _i
     lib.moc_router_forward.argtypes = [_p, _p, _p, _l, _l, _l, _i, _p]
     lib.moc_router_forward.restype = _i
+    lib.moc_router_forward_routed.argtypes = [_p, _p, _p, _l, _l, _l, _i, _i, _p]
+    lib.moc_router_forward_routed.restype = _i
     lib.moc_router_backward_workspace_bytes.argtypes = [_l, _l, _l, _i]
     lib.moc_router_backward_workspace_bytes.restype = _z
     lib.moc_router_backward.argtypes = [_p, _p, _p, _p, _p, _l, _l, _l, _i, _p, _z, _p]

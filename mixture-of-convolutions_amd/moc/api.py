@@ -7,9 +7,12 @@ the gfx950 HIP kernels of libmoc_hip.so through ``ops`` and
 
 * the backward recomputes the pre-activation inside the kernel instead of
   re-running the forward (moc/api.py:176-183);
-* ``MoC.forward`` / ``MoC.step`` hand the router *logits* to the kernels, which
-  apply softmax / exp themselves and return d(logits) directly, so the router
-  activation and its gradient cost no separate kernels (moc/api.py:383-388);
+* the router activation and its gradient cost no kernels of their own
+  (moc/api.py:383-388): for bf16 layers ``MoC.forward`` is one autograd node
+  whose router kernel forms softmax / exp(z . router^T) and whose MoC backward
+  returns d(logits) for the router backward; otherwise (and in ``MoC.step``)
+  the kernels take the router *logits*, form the weights themselves and
+  return d(logits);
 * the router GEMM logits = z . router^T and its backward run on the library's
   skinny-GEMM kernels for bf16 layers (``router_linear``), torch's F.linear
   otherwise.
@@ -25,12 +28,14 @@ import torch.nn.functional as F
 from torch.autograd.function import once_differentiable
 
 from . import ops
-from ._lib import ROUTE_ALPHA, ROUTE_EXP, ROUTE_SOFTMAX
+from ._lib import (ROUTE_ALPHA, ROUTE_EXP, ROUTE_EXP_WEIGHTS, ROUTE_SOFTMAX,
+                   ROUTE_SOFTMAX_WEIGHTS)
 from .optim import moc_fan_in_std
 
 SUPPORTED_DTYPES = (torch.bfloat16, torch.float32)
 
 _ROUTING_CODES = {"softmax": ROUTE_SOFTMAX, "exp": ROUTE_EXP}
+_WEIGHTS_CODES = {"softmax": ROUTE_SOFTMAX_WEIGHTS, "exp": ROUTE_EXP_WEIGHTS}
 
 
 # ---------------------------------------------------------------------------
@@ -162,16 +167,17 @@ def _prepare(ctx_like, x, alpha, basis, cu_seqlens, max_seqlen, cu_seqlens_cpu, 
 
 
 def _moc_forward(ctx, x, alpha, basis, activation, routing, cu_seqlens, max_seqlen,
-                 cu_seqlens_cpu, chunk_indices):
+                 cu_seqlens_cpu, chunk_indices, extra=()):
+    """Forward of the autograd functions; saves x, alpha, basis, then the
+    tensors of ``extra``, then cu_seqlens (varlen)."""
     x, alpha, basis, cu_seqlens = _prepare(ctx, x, alpha, basis, cu_seqlens, max_seqlen,
                                            cu_seqlens_cpu, chunk_indices)
     act = activation_flag(activation)
     y = ops.launch_forward(x, alpha, basis, activation_flag=act, cu_seqlens=cu_seqlens,
                            routing=routing)
-    if cu_seqlens is None:
-        ctx.save_for_backward(x, alpha, basis)
-    else:
-        ctx.save_for_backward(x, alpha, basis, cu_seqlens)
+    tail = () if cu_seqlens is None else (cu_seqlens,)
+    ctx.save_for_backward(x, alpha, basis, *extra, *tail)
+    ctx.n_extra = len(extra)
     ctx.act = act
     ctx.routing = routing
     ctx.varlen = cu_seqlens is not None
@@ -181,7 +187,7 @@ def _moc_forward(ctx, x, alpha, basis, activation, routing, cu_seqlens, max_seql
 def _moc_backward(ctx, dy):
     saved = ctx.saved_tensors
     x, alpha, basis = saved[:3]
-    cu_seqlens = saved[3] if ctx.varlen else None
+    cu_seqlens = saved[3 + ctx.n_extra] if ctx.varlen else None
     return ops.launch_backward(x, alpha, basis, dy, activation_flag=ctx.act,
                                need_x=ctx.needs_input_grad[0], cu_seqlens=cu_seqlens,
                                routing=ctx.routing)
@@ -236,6 +242,33 @@ class _RouterLinear(torch.autograd.Function):
         dz, dr = ops.router_backward(z, router, dlogits, ctx.needs_input_grad[0],
                                      ctx.needs_input_grad[1])
         return dz, dr
+
+
+class _MoCLayerFunction(torch.autograd.Function):
+    """The MoC layer (moc/api.py:372-400) on the library's kernels end to end:
+    the router kernel forms the routing weights softmax / exp(z . router^T)
+    (bf16, once per token), the MoC forward uses them as given, the MoC
+    backward (routing *_WEIGHTS) returns the logits gradient, which the router
+    backward turns into dz and drouter."""
+
+    @staticmethod
+    def forward(ctx, x, z, router, basis, activation, router_activation, cu_seqlens, max_seqlen,
+                cu_seqlens_cpu, chunk_indices):
+        weights = ops.router_forward(z, router, routing=_ROUTING_CODES[router_activation])
+        return _moc_forward(ctx, x, weights, basis, activation,
+                            _WEIGHTS_CODES[router_activation], cu_seqlens, max_seqlen,
+                            cu_seqlens_cpu, chunk_indices, extra=(z, router))
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy):
+        dx, dlogits, dbasis = _moc_backward(ctx, dy)
+        z, router = ctx.saved_tensors[3:5]
+        dz = dr = None
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            dz, dr = ops.router_backward(z, router, dlogits, ctx.needs_input_grad[1],
+                                         ctx.needs_input_grad[2])
+        return dx, dz, dr, dbasis, None, None, None, None, None, None
 
 
 def router_linear(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
@@ -370,10 +403,34 @@ class MoC(nn.Module):
                                        activation_flag=activation_flag(self.activation),
                                        routing=_ROUTING_CODES[self.router_activation])
             return y[:, None], (cache if output_final_state else None)
+        if cache is None and ops.router_supported(z, self.router):
+            return self._forward_kernels(x, z, output_final_state, cu_seqlens, max_seqlen,
+                                         cu_seqlens_cpu, chunk_indices)
         logits = router_linear(z, self.router)
         return _dispatch(x, logits, self.conv_bases, cache, output_final_state,
                          self.activation, self.router_activation, cu_seqlens, max_seqlen,
                          cu_seqlens_cpu, chunk_indices)
+
+    def _forward_kernels(self, x, z, output_final_state, cu_seqlens, max_seqlen, cu_seqlens_cpu,
+                         chunk_indices):
+        """forward without a cache, router included, as one autograd node
+        (_MoCLayerFunction); same checks and returns as _dispatch."""
+        activation_flag(self.activation)
+        args = (self.router, self.conv_bases, self.activation, self.router_activation)
+        if cu_seqlens is None:
+            if cu_seqlens_cpu is not None or chunk_indices is not None:
+                raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+            y = _MoCLayerFunction.apply(x, z, *args, None, None, None, None)
+            state = _final_state(x, None, self.kernel_size) if output_final_state else None
+            return y, state
+        if output_final_state:
+            raise ValueError("cache and output_final_state are only supported for fixed-length inputs")
+        if max_seqlen is None:
+            raise ValueError("max_seqlen is required for varlen inputs")
+        xp, zp, restore = _canonicalize_packed_input(x, z)
+        y = _MoCLayerFunction.apply(xp, zp, *args, cu_seqlens, max_seqlen, cu_seqlens_cpu,
+                                    chunk_indices)
+        return (y[None] if restore else y), None
 
     def step(self, x: torch.Tensor, z: torch.Tensor, cache: torch.Tensor | None = None,
              output_final_state: bool = False) -> tuple[torch.Tensor, torch.Tensor | None]:

@@ -121,7 +121,8 @@ def launch_forward(
     routing: int = ROUTE_ALPHA,
 ) -> torch.Tensor:
     """y = MoC(x, alpha, basis) (moc/ops.py:129-194).  ``alpha`` holds routing
-    weights (routing=0) or router logits whose softmax (1) / exp (2) is fused."""
+    weights (routing 0, 3, 4) or router logits whose softmax (1) / exp (2) is
+    fused."""
     del cu_seqlens_cpu, chunk_indices  # boundaries come from cu_seqlens on device
     L = _lib.lib()
     x = x.contiguous()
@@ -179,7 +180,8 @@ def launch_backward(
     """(dx or None, dalpha, dbasis) (moc/ops.py:216-338).  ``preact`` is
     accepted for signature compatibility and ignored: the kernel recomputes the
     pre-activation in registers.  With routing != 0, ``dalpha`` is the
-    gradient with respect to the logits."""
+    gradient with respect to the logits (routing 3 / 4: the softmax / exp
+    gradient formed from the weights ``alpha``)."""
     del preact, cu_seqlens_cpu, chunk_indices
     L = _lib.lib()
     x = x.contiguous()
@@ -263,8 +265,11 @@ def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
     return hit
 
 
-def router_forward(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
-    """logits = z . router^T (the F.linear(z, router) of moc/api.py:383-388)."""
+def router_forward(z: torch.Tensor, router: torch.Tensor, routing: int = ROUTE_ALPHA
+                   ) -> torch.Tensor:
+    """logits = z . router^T (the F.linear(z, router) of moc/api.py:383-388);
+    with routing 1 / 2 the router activation of moc/api.py:385-388 too:
+    softmax / exp of the bf16 logits, rounded to bf16 (the routing weights)."""
     L = _lib.lib()
     z = z.contiguous()
     r = router.contiguous()
@@ -272,8 +277,13 @@ def router_forward(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
     N = z.numel() // Z
     out = torch.empty(*z.shape[:-1], K, dtype=z.dtype, device=z.device)
     with _lib.device_guard(z.device):
-        rc = L.moc_router_forward(z.data_ptr(), r.data_ptr(), out.data_ptr(), N, Z, K,
-                                  _lib.DT_BF16, _lib.stream_ptr(z.device))
+        if routing == ROUTE_ALPHA:
+            rc = L.moc_router_forward(z.data_ptr(), r.data_ptr(), out.data_ptr(), N, Z, K,
+                                      _lib.DT_BF16, _lib.stream_ptr(z.device))
+        else:
+            rc = L.moc_router_forward_routed(z.data_ptr(), r.data_ptr(), out.data_ptr(), N, Z,
+                                             K, _lib.DT_BF16, int(routing),
+                                             _lib.stream_ptr(z.device))
     _lib.check(rc, "moc_router_forward")
     return out
 

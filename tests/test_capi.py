@@ -67,7 +67,8 @@ def _fwd(**kw):
     (dict(dim=0), -1),
     (dict(k=-3), -1),
     (dict(act=2), -1),
-    (dict(route=3), -1),
+    (dict(route=5), -1),
+    (dict(route=-1), -1),
     (dict(x=None), -1),
     (dict(seq_len=0), -1),
     (dict(cu=FAKE, n_seqs=0), -1),

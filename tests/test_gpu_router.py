@@ -109,3 +109,69 @@ def test_module_router_kernels_match_torch_gemm(route):
     got, ref = run(True), run(False)
     for name, a, b in zip(("y", "dx", "dz", "drouter", "dbasis"), got, ref):
         assert_close(name, a, b.float(), BF)
+
+
+@pytest.mark.parametrize("K,S,route,act,varlen", [
+    (16, 4, "softmax", "silu", False), (16, 4, "exp", None, False),
+    (16, 3, "softmax", "silu", True), (12, 4, "softmax", "silu", False),
+    (32, 8, "exp", "silu", False), (20, 2, "softmax", None, True),
+])
+def test_layer_function_matches_logits_path(K, S, route, act, varlen):
+    """MoC.forward as one autograd node (the router kernel forms the weights,
+    the MoC kernels take them as given and return d(logits)) against the
+    two-node path (router logits, the MoC kernels form the weights): both run
+    the same arithmetic in the same order, so y and every gradient agree bit
+    for bit.  K = 16 takes the kernels' in-place operand path, other K the
+    prepared-operand path."""
+    D, Z, B, T = 192, 128, 2, 77
+    torch.manual_seed(K + S)
+    m = MoC(D, Z, S, K, activation=act, init_std=0.1, router_activation=route)
+    g = gen(K * 10 + S)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.1))
+    m = m.to(DEV, BF)
+    if varlen:
+        lengths = [1, 30, 2, 77, 44]
+        cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32,
+                          device=DEV)
+        shape, kw = (sum(lengths),), dict(cu_seqlens=cu, max_seqlen=max(lengths))
+    else:
+        shape, kw = (B, T), {}
+    x = randn(g, *shape, D).to(DEV, BF)
+    z = randn(g, *shape, Z).to(DEV, BF)
+    dy = randn(g, *shape, D, scale=0.1).to(DEV, BF)
+
+    def run(one_node):
+        m.zero_grad(set_to_none=True)
+        xi = x.clone().requires_grad_()
+        zi = z.clone().requires_grad_()
+        if one_node:
+            y, _ = m(xi, zi, **kw)
+            assert type(y.grad_fn).__name__.startswith("_MoCLayerFunction")
+        else:
+            logits = moc.router_linear(zi, m.router)
+            y, _ = moc.api._dispatch(xi, logits, m.conv_bases, None, False, m.activation,
+                                     m.router_activation, kw.get("cu_seqlens"),
+                                     kw.get("max_seqlen"), None, None)
+        y.backward(dy)
+        return y.detach(), xi.grad, zi.grad, m.router.grad.clone(), m.conv_bases.grad.clone()
+
+    got, ref = run(True), run(False)
+    for name, a, b in zip(("y", "dx", "dz", "drouter", "dbasis"), got, ref):
+        assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("K", [4, 16, 20, 32])
+@pytest.mark.parametrize("route", ["softmax", "exp"])
+def test_router_forward_routed_weights(K, route):
+    """The router kernel's fused activation against torch's softmax / exp of
+    the kernel's own bf16 logits (torch rounds the activation to bf16 once)."""
+    N, Z = 333, 192
+    z, r, _ = _inputs(N, Z, K, K + 3)
+    code = moc.api._ROUTING_CODES[route]
+    w = ops.router_forward(z, r, routing=code)
+    logits = ops.router_forward(z, r)
+    ref = torch.softmax(logits.float(), -1) if route == "softmax" else torch.exp(logits.float())
+    assert w.dtype == BF and w.shape == (N, K)
+    # one bf16 ulp: torch's exp / division may round differently in fp32
+    assert_close("weights", w, ref, BF)
