@@ -9,6 +9,8 @@
 // dz with K = 16); accumulation is fp32, results are rounded to bf16 once.
 // drouter is reduced in a fixed order (per-range partials, then one sum), so it
 // is bitwise reproducible.  bf16 data only; K % 4 == 0, K <= 32, Z % 64 == 0.
+#include <cstdlib>
+
 #include "moc_kernels.h"
 #include "moc_mfma.h"
 
@@ -29,6 +31,12 @@ __device__ __forceinline__ u32x4 load16(const Buf& b, uint32_t off) {
 }
 __device__ __forceinline__ u32x2 load8(const Buf& b, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(b.r, static_cast<int>(off), 0, 0);
+}
+
+// Wave index, known to the compiler as uniform over the wave (so that loops
+// and branches on it compile as scalar control flow, not exec-masked).
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
 }
 
 // 16 x 16 x 32 product of 8-element bf16 operands held as 16 bytes.
@@ -59,7 +67,7 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
                                                          int64_t N, int Z, int K, int routing) {
   constexpr int KP = 16 * KC;
   __shared__ float red[4][2][KP][17];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int i = lane & 15, qq = lane >> 4;
   const int64_t t0 = static_cast<int64_t>(blockIdx.x) * 32;
   const int64_t rows = (N - t0 < 32) ? N - t0 : 32;
@@ -159,7 +167,7 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
                                                         const uint16_t* __restrict__ r,
                                                         uint16_t* __restrict__ dz, int64_t N,
                                                         int Z, int K) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int i = lane & 15, qq = lane >> 4;
   const int zs = (blockIdx.x * 4 + w) * 64;
   if (zs >= Z) return;  // whole wave; the kernel has no barrier
@@ -239,7 +247,7 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
   __shared__ __align__(16) uint16_t zt[4][32][kZRow];
   __shared__ __align__(16) uint16_t dt[4][32][KROW];
   __shared__ float red[4][KP][65];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, w = wave_id();
   const int i = lane & 15, qq = lane >> 4;
   const int zs = blockIdx.x * 64;
   const Buf zb(z, N * Z * 2);
@@ -303,16 +311,22 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
         acc[tl][kc] = mfma::mma32(ad[kc][0], ad[kc][1], bz[tl][0], bz[tl][1], acc[tl][kc]);
     mfma::wave_lds_sync();
   };
+  // the wave's blocks are w, w + 4, ...: nb of them; straight-line loop body
+  // (single exit, so both sets stay in flight across the back edge), one
+  // block left over runs after it
+  const int nb = (blocks_per_range - w + 3) / 4;
   Regs ra, rb2;
   load_block(ra, w);
   load_block(rb2, w + 4);
-  for (int b = w; b < blocks_per_range; b += 8) {  // per wave; no barrier inside
+  int it = 0;
+  for (; it + 2 <= nb; it += 2) {  // per wave; no barrier inside
+    const int b = w + 4 * it;
     mult_block(ra);
     load_block(ra, b + 8);
-    if (b + 4 >= blocks_per_range) break;
     mult_block(rb2);
     load_block(rb2, b + 12);
   }
+  if (it < nb) mult_block(ra);
   // D lane (j, q): column 16 tl + j, routes 16 kc + 4 q + v
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl)
@@ -325,6 +339,168 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
     const int k = idx / 64, col = idx % 64;
     const float s = ((red[0][k][col] + red[1][k][col]) + red[2][k][col]) + red[3][k][col];
     part[(static_cast<int64_t>(blockIdx.y) * K + k) * Z + zs + col] = s;
+  }
+}
+
+// dz and the partial drouter in one pass (both requested): the workgroup of
+// router_dr_kernel (64 columns, one token range, 4 waves taking 32-token blocks
+// in turn, the same block order, so the partials are the same bit for bit)
+// also writes dz for its columns and tokens, D[zc][t] = router^T . dl^T as in
+// router_dz_kernel, with the dl B operands read from the block's LDS tile.
+// Three blocks' loads are in flight per wave.
+template <int KC>
+__global__ void __launch_bounds__(256) router_bwd_kernel(const uint16_t* __restrict__ dl,
+                                                         const uint16_t* __restrict__ z,
+                                                         const uint16_t* __restrict__ r,
+                                                         uint16_t* __restrict__ dz,
+                                                         float* __restrict__ part, int64_t N,
+                                                         int Z, int K, int blocks_per_range) {
+  constexpr int KP = 16 * KC;
+  constexpr int KROW = KP + 4;  // padded LDS row of a dl tile (bf16)
+  __shared__ __align__(16) uint16_t zt[4][32][kZRow];
+  __shared__ __align__(16) uint16_t dt[4][32][KROW];
+  __shared__ float red[4][KP][65];
+  const int lane = threadIdx.x & 63, w = wave_id();
+  const int i = lane & 15, qq = lane >> 4;
+  const int zs = blockIdx.x * 64;
+  const Buf zb(z, N * Z * 2);
+  const Buf db(dl, N * K * 2);
+  const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
+  const Buf ob(dz, N * Z * 2);
+  f32x4 acc[4][KC];
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) acc[tl][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // dz A operands: router[16 kc + 4 qq + v][zs + dz_col(tl, i)] (routes >= K load 0)
+  s16x4 aop[4][KC];
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      uint16_t e[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int k = 16 * kc + 4 * qq + v;
+        const uint32_t off = static_cast<uint32_t>((k * Z + zs + dz_col(tl, i)) * 2);
+        e[v] = __builtin_amdgcn_raw_buffer_load_b16(rb.r, static_cast<int>(off), 0, 0);
+      }
+      aop[tl][kc] = s16x4{static_cast<short>(e[0]), static_cast<short>(e[1]),
+                          static_cast<short>(e[2]), static_cast<short>(e[3])};
+    }
+
+  const int64_t blk0 = static_cast<int64_t>(blockIdx.y) * blocks_per_range;
+  struct Regs {
+    u32x4 z[4];
+    u32x2 d[KP / 8];
+  };
+  // as router_dr_kernel: blocks past the range or past N load zeros
+  auto load_block = [&](Regs& rg, int bb) {
+    const int64_t t0 = (blk0 + bb) * 32;
+    const bool on = bb < blocks_per_range && t0 < N;
+#pragma unroll
+    for (int ld = 0; ld < 4; ++ld) {
+      const int row = lane / 8 + 8 * ld;
+      rg.z[ld] = load16(zb, on ? static_cast<uint32_t>(((t0 + row) * Z + zs + 8 * (lane % 8)) * 2)
+                               : kOffNone);
+    }
+#pragma unroll
+    for (int ld = 0; ld < KP / 8; ++ld) {
+      const int chunk = lane + 64 * ld;
+      const int row = chunk / (KP / 4), k = 4 * (chunk % (KP / 4));
+      rg.d[ld] = load8(db, (on && k < K) ? static_cast<uint32_t>(((t0 + row) * K + k) * 2) : kOffNone);
+    }
+  };
+  // block bb is in the range; rows past N are dropped by the dz buffer's bound
+  auto mult_block = [&](const Regs& rg, int bb) {
+#pragma unroll
+    for (int ld = 0; ld < 4; ++ld)
+      *reinterpret_cast<u32x4*>(&zt[w][lane / 8 + 8 * ld][8 * (lane % 8)]) = rg.z[ld];
+#pragma unroll
+    for (int ld = 0; ld < KP / 8; ++ld) {
+      const int chunk = lane + 64 * ld;
+      *reinterpret_cast<u32x2*>(&dt[w][chunk / (KP / 4)][4 * (chunk % (KP / 4))]) = rg.d[ld];
+    }
+    mfma::wave_lds_sync();
+    const int e = i >> 2, a = i & 3;
+    s16x4 bz[4][2], ad[KC][2], bd[2][KC];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 8 * qq + 4 * h + e;
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) bz[tl][h] = tr_read(&zt[w][row][16 * tl + 4 * a]);
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) ad[kc][h] = tr_read(&dt[w][row][16 * kc + 4 * a]);
+    }
+    // dz B operands: dl[t0 + 16 hb + i][16 kc + 4 qq + {0..3}]
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        bd[hb][kc] = *reinterpret_cast<const s16x4*>(&dt[w][16 * hb + i][16 * kc + 4 * qq]);
+#pragma unroll
+    for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc)
+        acc[tl][kc] = mfma::mma32(ad[kc][0], ad[kc][1], bz[tl][0], bz[tl][1], acc[tl][kc]);
+    const int64_t t0 = (blk0 + bb) * 32;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb) {
+      f32x4 o[4];
+#pragma unroll
+      for (int tl = 0; tl < 4; ++tl) {
+        if constexpr (KC == 1) {
+          o[tl] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bd[hb][0],
+                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        } else {
+          o[tl] = mfma::mma32(aop[tl][0], aop[tl][1], bd[hb][0], bd[hb][1],
+                              f32x4{0.f, 0.f, 0.f, 0.f});
+        }
+      }
+      const int64_t t = t0 + 16 * hb + i;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const f32x4 a0 = o[2 * half], a1 = o[2 * half + 1];
+        const u32x4 pk = {mfma::pack2_bf16(a0[0], a0[1]), mfma::pack2_bf16(a0[2], a0[3]),
+                          mfma::pack2_bf16(a1[0], a1[1]), mfma::pack2_bf16(a1[2], a1[3])};
+        const uint32_t off = static_cast<uint32_t>((t * Z + zs + 32 * half + 8 * qq) * 2);
+        __builtin_amdgcn_raw_buffer_store_b128(pk, ob.r, static_cast<int>(off), 0, 0);
+      }
+    }
+    mfma::wave_lds_sync();
+  };
+  // the wave's blocks are w, w + 4, ...: nb of them.  The loop body is
+  // straight-line (three blocks, each set reloaded right after use) and the
+  // zero to two blocks left run after it, so the loop has a single exit and
+  // the three sets stay in flight across its back edge.
+  const int nb = (blocks_per_range - w + 3) / 4;
+  Regs r0, r1, r2;
+  load_block(r0, w);
+  load_block(r1, w + 4);
+  load_block(r2, w + 8);
+  int it = 0;
+  for (; it + 3 <= nb; it += 3) {  // per wave; no barrier inside
+    const int b = w + 4 * it;
+    mult_block(r0, b);
+    load_block(r0, b + 12);
+    mult_block(r1, b + 4);
+    load_block(r1, b + 16);
+    mult_block(r2, b + 8);
+    load_block(r2, b + 20);
+  }
+  if (it < nb) mult_block(r0, w + 4 * it);
+  if (it + 1 < nb) mult_block(r1, w + 4 * it + 4);
+#pragma unroll
+  for (int tl = 0; tl < 4; ++tl)
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[w][16 * kc + 4 * qq + v][16 * tl + i] = acc[tl][kc][v];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < K * 64; idx += 256) {
+    const int k = idx / 64, col = idx % 64;
+    const float sm = ((red[0][k][col] + red[1][k][col]) + red[2][k][col]) + red[3][k][col];
+    part[(static_cast<int64_t>(blockIdx.y) * K + k) * Z + zs + col] = sm;
   }
 }
 
@@ -358,10 +534,14 @@ struct BwdPlan {
   int64_t ranges, blocks_per_range;
 };
 
+#ifndef MOC_RB_TARGET_WG
+#define MOC_RB_TARGET_WG 512
+#endif
+
 BwdPlan bwd_plan(int64_t N, int64_t Z) {
   const int64_t nblk = cdiv(N, 32);
   const int64_t slices = Z / 64;
-  int64_t ranges = cdiv(512, slices);  // about 512 workgroups
+  int64_t ranges = cdiv(MOC_RB_TARGET_WG, slices);  // about MOC_RB_TARGET_WG workgroups
   if (ranges > cdiv(nblk, 4)) ranges = cdiv(nblk, 4);
   if (ranges < 1) ranges = 1;
   const int64_t bpr = cdiv(nblk, ranges);
@@ -401,6 +581,23 @@ void router_backward(const void* z, const void* r, const void* dl, void* dz, voi
   const auto* rp = static_cast<const uint16_t*>(r);
   const auto* dp = static_cast<const uint16_t*>(dl);
   const int Zi = static_cast<int>(Z), Ki = static_cast<int>(K);
+  if (dz != nullptr && dr != nullptr && std::getenv("MOC_ROUTER_SPLIT") == nullptr) {
+    const router::BwdPlan pl = router::bwd_plan(N, Z);
+    float* part = static_cast<float*>(workspace);
+    const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
+    auto* op = static_cast<uint16_t*>(dz);
+    if (K <= 16)
+      hipLaunchKernelGGL(router::router_bwd_kernel<1>, grid, dim3(256), 0, st, dp, zp, rp, op,
+                         part, N, Zi, Ki, static_cast<int>(pl.blocks_per_range));
+    else
+      hipLaunchKernelGGL(router::router_bwd_kernel<2>, grid, dim3(256), 0, st, dp, zp, rp, op,
+                         part, N, Zi, Ki, static_cast<int>(pl.blocks_per_range));
+    const int64_t KZ = K * Z;
+    hipLaunchKernelGGL(router::router_dr_reduce_kernel, dim3(static_cast<unsigned>(router::cdiv(KZ, 256))),
+                       dim3(256), 0, st, part, static_cast<uint16_t*>(dr), KZ,
+                       static_cast<int>(pl.ranges));
+    return;
+  }
   if (dz != nullptr) {
     const int64_t waves_x = Z / 64;
     const dim3 grid(static_cast<unsigned>(router::cdiv(waves_x, 4)),
