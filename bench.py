@@ -10,8 +10,10 @@ inputs already resident in HBM.  Printed as one JSON line:
   value         tokens/s (millions) of the full layer step (router GEMMs + MoC)
   roofline      HBM roofline of the dominant entry (the fused backward)
   kernel_scope  forward / backward entry times alone (no router GEMMs)
-  decode        configs[3]: batch-256 single-token steps, us per MoC.step call and
-                per launch of the one-launch decode step (graph-replayed)
+  decode        configs[3]: batch-256 single-token steps: us per MoC.step call
+                (host-synchronised each step, and back to back), per MoC.step
+                replayed from a HIP graph, and per launch of the one-launch
+                decode step alone (graph-replayed)
   cpu_baseline  the CPU oracle on a bounded slice of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
@@ -224,6 +226,30 @@ def bench_decode(dev):
             y, _ = m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache, output_final_state=True)
             torch.cuda.synchronize()
             per_step.append((time.perf_counter() - t0) * 1e6)
+        # back to back, one synchronisation at the end: what a decode loop sees
+        # when it does not wait for each token on the host
+        t0 = time.perf_counter()
+        for t in range(c["steps"]):
+            m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache)
+        torch.cuda.synchronize()
+        async_us = (time.perf_counter() - t0) * 1e6 / c["steps"]
+        # MoC.step itself captured in a HIP graph (static x / z buffers, cache
+        # updated in place): 32 module steps per graph launch
+        xin = xs[:, :1].clone()
+        zin = zs[:, :1].clone()
+        gcache = cache.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                m.step(xin, zin, cache=gcache)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        mgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(mgraph):
+            for _ in range(32):
+                m.step(xin, zin, cache=gcache)
+        module_graph_us = time_region(mgraph.replay, 20, 3) * 1e3 / 32
         # kernel-only: 32 launches of the one-launch decode step that MoC.step
         # runs (router GEMM + softmax + update), captured in one HIP graph
         xt = xs[:, 0].contiguous()
@@ -253,6 +279,8 @@ def bench_decode(dev):
     return dict(B=c["B"], D=c["D"], K=c["K"], S=c["S"], prompt=c["prompt"], steps=c["steps"],
                 step_us_median=round(statistics.median(per_step), 2),
                 step_us_p10=round(sorted(per_step)[len(per_step) // 10], 2),
+                step_us_async=round(async_us, 2),
+                step_us_graph=round(module_graph_us, 2),
                 kernel_us=round(kernel_us, 3),
                 kernel_GBps=round(kbytes / (kernel_us * 1e-6) / 1e9, 1),
                 kernel_roofline_us=round(kbytes / HBM_PEAK * 1e6, 3))

@@ -289,3 +289,48 @@ def test_config4_decode():
         alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
         full = O.moc_ref(x[rows].float(), alpha, m.conv_bases.float(), "silu")
     assert_close("decode y", y_steps[rows], full[:, P:], torch.bfloat16)
+
+
+def test_module_step_graph_capture():
+    """MoC.step captured in a HIP graph (static x / z buffers, the cache updated
+    in place by the captured launch) and replayed once per token: each replay
+    matches the eager step bit for bit (y and cache), with eager work and a
+    synchronisation between replays."""
+    B, D, Z, K, S, steps = 64, 512, 256, 16, 4, 6
+    g = gen(77)
+    m = MoC(D, Z, S, K, activation="silu", init_std=0.1)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.05))
+    m = m.to(DEV, torch.bfloat16)
+    xs = randn(g, B, steps, D).to(DEV, torch.bfloat16)
+    zs = randn(g, B, steps, Z).to(DEV, torch.bfloat16)
+    cache0 = randn(g, B, D, S).to(DEV, torch.bfloat16)
+    assert moc.ops.decode_step_supported(xs[:, :1], zs[:, :1], m.router, m.conv_bases, cache0)
+    ce, ye = cache0.clone(), []
+    with torch.no_grad():
+        for t in range(steps):
+            y, _ = m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=ce)
+            ye.append(y.clone())
+    xin = torch.empty(B, 1, D, device=DEV, dtype=torch.bfloat16)
+    zin = torch.empty(B, 1, Z, device=DEV, dtype=torch.bfloat16)
+    cg = cache0.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.no_grad():
+        scratch = cache0.clone()
+        for _ in range(2):
+            m.step(xin.zero_(), zin.zero_(), cache=scratch)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        yg, _ = m.step(xin, zin, cache=cg)
+    assert torch.equal(cg, cache0)  # capture records, it does not run
+    for t in range(steps):
+        xin.copy_(xs[:, t:t + 1])
+        zin.copy_(zs[:, t:t + 1])
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, ye[t]), t
+        (xs.float() * 2).sum().item()  # eager work between replays
+    assert torch.equal(cg, ce)
