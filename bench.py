@@ -37,6 +37,7 @@ import torch  # noqa: E402
 
 METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/step"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
+VALU_PEAK = 157.3e12       # flop/s, MI355X fp32 vector (packed)
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
 # FETCH_SIZE (68780 KiB) and WRITE_SIZE (98367 KiB) per dispatch of
@@ -154,25 +155,27 @@ def time_kernel(fn, steps, warmup):
 
 
 def entry_calls(dev):
-    """The forward and backward C-ABI entries on the layer's logits, as two
-    zero-argument callables (fwd, bwd)."""
+    """The forward and backward C-ABI entries as the layer calls them, as two
+    zero-argument callables (fwd, bwd): on the routing weights the router
+    kernel forms (softmax of the bf16 logits), routing "softmax weights given",
+    so the backward returns the logits gradient."""
     from moc import ops
-    from moc._lib import ROUTE_SOFTMAX
+    from moc._lib import ROUTE_SOFTMAX, ROUTE_SOFTMAX_WEIGHTS
     m, x, z = build_layer(dev)
     with torch.no_grad():
-        logits = torch.nn.functional.linear(z, m.router)
+        weights = ops.router_forward(z, m.router, routing=ROUTE_SOFTMAX)
         basis = m.conv_bases.detach()
         xd = x.detach()
         dy = torch.ones_like(xd)
-    fwd = lambda: ops.launch_forward(xd, logits, basis, activation_flag=1,  # noqa: E731
-                                     routing=ROUTE_SOFTMAX)
-    bwd = lambda: ops.launch_backward(xd, logits, basis, dy, activation_flag=1,  # noqa: E731
-                                      need_x=True, routing=ROUTE_SOFTMAX)
+    fwd = lambda: ops.launch_forward(xd, weights, basis, activation_flag=1,  # noqa: E731
+                                     routing=ROUTE_SOFTMAX_WEIGHTS)
+    bwd = lambda: ops.launch_backward(xd, weights, basis, dy, activation_flag=1,  # noqa: E731
+                                      need_x=True, routing=ROUTE_SOFTMAX_WEIGHTS)
     return fwd, bwd
 
 
 def bench_entries(dev, steps, warmup):
-    """Forward and backward C-ABI entries alone, on the layer's logits:
+    """Forward and backward C-ABI entries alone, as the layer calls them:
     (entry ms fwd, entry ms bwd, main-kernel ms fwd, main-kernel ms bwd)."""
     fwd, bwd = entry_calls(dev)
     return (time_region(fwd, steps, warmup), time_region(bwd, steps, warmup),
@@ -352,6 +355,11 @@ def main():
     fb, bb = bytes_fwd(N, D, K, S), bytes_bwd(N, D, K, S)
     roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / 2.5e15)
                + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / 2.5e15)) * 1e6
+    # the same bytes with the algorithm's flops on the fp32 VALU (157.3 TF/s):
+    # the bound of an implementation that runs the K-contractions on VALU,
+    # which binds at this config (about 54 flop/B)
+    valu_roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / VALU_PEAK)
+                    + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / VALU_PEAK)) * 1e6
     # dominant kernel: the fused backward stage 1; its algorithmic bytes are x, dy
     # and dx, the routing weights and the basis (dalpha / dbasis leave it as
     # partial sums that the stage-2 reduction turns into the outputs)
@@ -385,7 +393,9 @@ def main():
                          "fwd_GBps": round(fb / (t_fwd * 1e-3) / 1e9, 1),
                          "bwd_GBps": round(bb / (t_bwd * 1e-3) / 1e9, 1),
                          "hbm_roofline_us": round(roof_us, 2),
-                         "roofline_frac": round(roof_us / ((t_fwd + t_bwd) * 1e3), 4)},
+                         "roofline_frac": round(roof_us / ((t_fwd + t_bwd) * 1e3), 4),
+                         "valu_roofline_us": round(valu_roof_us, 2),
+                         "valu_roofline_frac": round(valu_roof_us / ((t_fwd + t_bwd) * 1e3), 4)},
     }
     if not args.no_decode:
         out["decode"] = bench_decode(dev)

@@ -159,7 +159,7 @@ int moc_decode_step(const void* z, const void* router, const void* x, const void
 /*
  * Router of the MoC layer: logits = z . router^T, the F.linear(z, router) of
  * MoC.forward (moc/api.py:383-388) that the reference runs as a library GEMM,
- * and its backward.  bf16 only; k % 4 == 0, k <= 32, z_dim % 64 == 0 and
+ * and its backward.  bf16 only; k % 4 == 0, k <= 96, z_dim % 64 == 0 and
  * n_tokens * z_dim * 2 < 2^31 (moc_router_supported returns 1 for such shapes).
  *   z      : [n_tokens, z_dim] contiguous
  *   router : [k, z_dim] contiguous
@@ -177,11 +177,29 @@ int moc_router_forward(const void* z, const void* router, void* logits, int64_t 
  * from the bf16 logits and rounded to bf16, as torch forms them.  The weights
  * feed moc_forward / moc_backward with routing MOC_ROUTE_SOFTMAX_WEIGHTS /
  * MOC_ROUTE_EXP_WEIGHTS, whose dalpha is then the logits gradient for
- * moc_router_backward.
+ * moc_router_backward.  k <= 32.
  *   weights : [n_tokens, k] bf16
  */
 int moc_router_forward_routed(const void* z, const void* router, void* weights, int64_t n_tokens,
                               int64_t z_dim, int64_t k, int dtype, int routing, void* stream);
+
+/*
+ * Several MoC layers that share their routing input z (the QKV pattern of the
+ * reference README, README.md:80-129, where three MoC.forward calls each run
+ * F.linear(z, router) and their own activation, moc/api.py:383-388): one pass
+ * over z against the concatenated routers [sum k, z_dim] (group g owns rows
+ * k[0] + .. + k[g-1] onward), and group g's weights, routing[g] (0 logits,
+ * 1 softmax, 2 exp) of its bf16 logits rounded to bf16, written to
+ * weights[g] ([n_tokens, k[g]] bf16, 8-byte aligned).  Each group's weights
+ * equal moc_router_forward_routed's for that group's router bit for bit.
+ * 1 <= n_groups <= 4, k[g] % 4 == 0, k[g] <= 32, sum k <= 96.  The backward
+ * is moc_router_backward with the concatenated router and the groups' logits
+ * gradients side by side ([n_tokens, sum k]): dz is then their sum.
+ * weights, k and routing are host arrays of n_groups entries.
+ */
+int moc_router_forward_grouped(const void* z, const void* router, void* const* weights,
+                               const int64_t* k, const int* routing, int n_groups,
+                               int64_t n_tokens, int64_t z_dim, int dtype, void* stream);
 
 /* Workspace bytes moc_router_backward needs when drouter is requested. */
 size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,

@@ -295,7 +295,7 @@ int moc_router_forward(const void* z, const void* router, void* logits, int64_t 
   g_err[0] = '\0';
   if (!moc::router_supported(n_tokens, z_dim, k, dtype))
     return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
-                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                             "dtype %d): bf16, k %% 4 == 0, k <= 96, z_dim %% 64 == 0",
                 (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
   if (!z || !router || !logits) return fail(MOC_ERR_ARG, "null tensor pointer");
   if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
@@ -309,15 +309,52 @@ int moc_router_forward_routed(const void* z, const void* router, void* weights, 
   g_err[0] = '\0';
   if (!moc::router_supported(n_tokens, z_dim, k, dtype))
     return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
-                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                             "dtype %d): bf16, k %% 4 == 0, k <= 96, z_dim %% 64 == 0",
                 (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
   if (routing != MOC_ROUTE_SOFTMAX && routing != MOC_ROUTE_EXP)
     return fail(MOC_ERR_ARG, "routing must be softmax (1) or exp (2), got %d", routing);
+  if (k > moc::kRouterMaxRoutedK)
+    return fail(MOC_ERR_ARG, "the fused router activation needs k <= %d, got %lld",
+                moc::kRouterMaxRoutedK, (long long)k);
   if (!z || !router || !weights) return fail(MOC_ERR_ARG, "null tensor pointer");
   if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
   moc::router_forward(z, router, weights, n_tokens, z_dim, k, routing,
                       static_cast<hipStream_t>(stream));
   return hip_status("moc_router_forward_routed launch");
+}
+
+int moc_router_forward_grouped(const void* z, const void* router, void* const* weights,
+                               const int64_t* k, const int* routing, int n_groups,
+                               int64_t n_tokens, int64_t z_dim, int dtype, void* stream) {
+  g_err[0] = '\0';
+  if (n_groups < 1 || n_groups > moc::kMaxRouteGroups)
+    return fail(MOC_ERR_ARG, "n_groups must be in [1, %d], got %d", moc::kMaxRouteGroups, n_groups);
+  if (!k || !routing || !weights) return fail(MOC_ERR_ARG, "null group array");
+  moc::RouteGroups grp{};
+  grp.n = n_groups;
+  int64_t total = 0;
+  for (int g = 0; g < n_groups; ++g) {
+    if (k[g] <= 0 || k[g] > moc::kRouterMaxRoutedK || k[g] % 4 != 0)
+      return fail(MOC_ERR_ARG, "group %d: k must be a multiple of 4 in [4, %d], got %lld", g,
+                  moc::kRouterMaxRoutedK, (long long)k[g]);
+    if (routing[g] < MOC_ROUTE_ALPHA || routing[g] > MOC_ROUTE_EXP)
+      return fail(MOC_ERR_ARG, "group %d: routing must be 0, 1 or 2, got %d", g, routing[g]);
+    if (!weights[g] || (reinterpret_cast<uintptr_t>(weights[g]) & 7) != 0)
+      return fail(MOC_ERR_ARG, "group %d: output pointer null or not 8-byte aligned", g);
+    grp.k0[g] = static_cast<int>(total);
+    grp.kn[g] = static_cast<int>(k[g]);
+    grp.routing[g] = routing[g];
+    grp.out[g] = static_cast<uint16_t*>(weights[g]);
+    total += k[g];
+  }
+  if (!moc::router_supported(n_tokens, z_dim, total, dtype))
+    return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, total k %lld, "
+                             "dtype %d): bf16, total k <= %d, z_dim %% 64 == 0",
+                (long long)n_tokens, (long long)z_dim, (long long)total, dtype, moc::kRouterMaxK);
+  if (!z || !router) return fail(MOC_ERR_ARG, "null tensor pointer");
+  if ((n_tokens + 15) / 16 > 0x7fffffff) return fail(MOC_ERR_ARG, "n_tokens too large");
+  moc::router_forward_grouped(z, router, grp, n_tokens, z_dim, static_cast<hipStream_t>(stream));
+  return hip_status("moc_router_forward_grouped launch");
 }
 
 size_t moc_router_backward_workspace_bytes(int64_t n_tokens, int64_t z_dim, int64_t k,
@@ -332,7 +369,7 @@ int moc_router_backward(const void* z, const void* router, const void* dlogits, 
   g_err[0] = '\0';
   if (!moc::router_supported(n_tokens, z_dim, k, dtype))
     return fail(MOC_ERR_ARG, "router shape not supported (n_tokens %lld, z_dim %lld, k %lld, "
-                             "dtype %d): bf16, k %% 4 == 0, k <= 32, z_dim %% 64 == 0",
+                             "dtype %d): bf16, k %% 4 == 0, k <= 96, z_dim %% 64 == 0",
                 (long long)n_tokens, (long long)z_dim, (long long)k, dtype);
   if (!router || !dlogits || (drouter && !z)) return fail(MOC_ERR_ARG, "null tensor pointer");
   if (drouter) {

@@ -69,8 +69,24 @@ void launch_decode_step(const void* z, const void* router, const void* x, const 
                         void* cache, void* y, int64_t B, int64_t Z, int64_t D, int64_t K,
                         int64_t S, int activation, int routing, hipStream_t st);
 
-// router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 32, Z % 64 == 0
+// router GEMMs (moc_router.hip): bf16, K % 4 == 0, K <= 96, Z % 64 == 0; the
+// fused router activation needs K <= 32
+constexpr int kRouterMaxK = 96;
+constexpr int kRouterMaxRoutedK = 32;
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt);
+
+// Routes [k0, k0 + kn) of a concatenated router form group g: its weights are
+// routing[g] (softmax / exp) of those logits, written to out[g] as [N, kn].
+constexpr int kMaxRouteGroups = 4;
+struct RouteGroups {
+  int n;
+  int k0[kMaxRouteGroups];
+  int kn[kMaxRouteGroups];
+  int routing[kMaxRouteGroups];
+  uint16_t* out[kMaxRouteGroups];
+};
+void router_forward_grouped(const void* z, const void* r, const RouteGroups& groups, int64_t N,
+                            int64_t Z, hipStream_t st);
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K);
 // routing ROUTE_ALPHA: out = the bf16 logits; ROUTE_SOFTMAX / ROUTE_EXP: out =
 // that activation of the bf16 logits, rounded to bf16

@@ -60,12 +60,52 @@ __device__ __forceinline__ s16x4 tr_read(const void* p) {
 // so that each load instruction reads 64 contiguous bytes per row and the
 // router operands serve both token blocks.  The 4 partial tiles are summed in
 // LDS in wave order.
+// Chunks whose loads are issued together: four up to 32 routes, fewer above
+// (the router operands of a chunk take 8 KC registers per lane).
 template <int KC>
+constexpr int kFwdBatch = KC <= 2 ? 4 : (KC <= 4 ? 2 : 1);
+
+// Weights of one token of a route group from its bf16 logits l[0, kn): the
+// softmax sum in the order of router_fwd_kernel's lane tree over KPg = 16 or
+// 32 lanes (pairs k ^ 16, then k ^ 8, k ^ 4, k ^ 2, k ^ 1), so that a group
+// gets the weights a single router of kn routes gets, bit for bit.
+__device__ __forceinline__ void route_group(float (&l)[32], int kn, int routing) {
+  if (routing == ROUTE_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      if (k < kn) m = fmaxf(m, l[k]);
+    float e[32], sm[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) {
+      e[k] = (k < kn) ? __expf(l[k] - m) : 0.f;
+      sm[k] = e[k];
+    }
+    if (kn > 16) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sm[k] = sm[k] + sm[k + 16];
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1)
+#pragma unroll
+      for (int k = 0; k < o; ++k) sm[k] = sm[k] + sm[k + o];
+    const float inv = 1.0f / sm[0];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) l[k] = round_to(e[k] * inv, DT_BF16);
+  } else if (routing == ROUTE_EXP) {
+#pragma unroll
+    for (int k = 0; k < 32; ++k) l[k] = round_to(__expf(l[k]), DT_BF16);
+  }
+}
+
+template <int KC, bool GROUPED>
 __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restrict__ z,
                                                          const uint16_t* __restrict__ r,
                                                          uint16_t* __restrict__ logits,
-                                                         int64_t N, int Z, int K, int routing) {
+                                                         int64_t N, int Z, int K, int routing,
+                                                         RouteGroups grp) {
   constexpr int KP = 16 * KC;
+  constexpr int UB = kFwdBatch<KC>;
   __shared__ float red[4][2][KP][17];
   const int lane = threadIdx.x & 63, w = wave_id();
   const int i = lane & 15, qq = lane >> 4;
@@ -80,12 +120,12 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) acc[h][kc] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int nchunk = Z / 64;
-  // four chunks per step with all their loads issued first (16 + 8 KC per lane);
-  // chunks past the row end load zeros instead of branching
-  for (int c0 = w; c0 < nchunk; c0 += 16) {
-    u32x4 za[4][2][2], ra[4][KC][2];
+  // UB chunks per step with all their loads issued first (4 + 2 KC per chunk
+  // and lane); chunks past the row end load zeros instead of branching
+  for (int c0 = w; c0 < nchunk; c0 += 4 * UB) {
+    u32x4 za[UB][2][2], ra[UB][KC][2];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < UB; ++u) {
       const int c = c0 + 4 * u;
       const bool on = c < nchunk;
       const uint32_t col0 = static_cast<uint32_t>((64 * c + 8 * qq) * 2), col1 = col0 + 64;
@@ -103,7 +143,7 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < UB; ++u)
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
@@ -120,15 +160,42 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[w][h][16 * kc + i][4 * qq + v] = acc[h][kc][v];
   __syncthreads();
+  if constexpr (GROUPED) {
+    // route groups: one thread per (group, token) forms the group's weights
+    for (int idx = threadIdx.x; idx < 32 * grp.n; idx += 256) {
+      const int tok = idx & 31, gi = idx >> 5, h = tok >> 4, tr = tok & 15;
+      if (tok >= rows) continue;
+      const int k0 = grp.k0[gi], kn = grp.kn[gi];
+      float l[32];
+#pragma unroll
+      for (int k = 0; k < 32; ++k) {
+        const int kk = k0 + ((k < kn) ? k : 0);
+        const float sm =
+            ((red[0][h][kk][tr] + red[1][h][kk][tr]) + red[2][h][kk][tr]) + red[3][h][kk][tr];
+        l[k] = round_to(sm, DT_BF16);
+      }
+      route_group(l, kn, grp.routing[gi]);
+      // kn % 4 == 0: 8-byte stores
+      uint2* o = reinterpret_cast<uint2*>(grp.out[gi] + (t0 + tok) * kn);
+#pragma unroll
+      for (int k = 0; k < 32; k += 4)
+        if (k < kn)
+          o[k / 4] = make_uint2(static_cast<uint32_t>(f32_to_bf16(l[k])) |
+                                    (static_cast<uint32_t>(f32_to_bf16(l[k + 1])) << 16),
+                                static_cast<uint32_t>(f32_to_bf16(l[k + 2])) |
+                                    (static_cast<uint32_t>(f32_to_bf16(l[k + 3])) << 16));
+    }
+    return;
+  }
   // KP consecutive lanes hold one token's routes; every lane runs every pass
-  // (the shuffles of the routing need all of them)
+  // (the shuffles of the routing need all of them; routing needs KC <= 2)
 #pragma unroll
   for (int pass = 0; pass < 32 * KP / 256; ++pass) {
     const int idx = threadIdx.x + 256 * pass;
     const int tok = idx / KP, k = idx % KP, h = tok >> 4, tr = tok & 15;
     const float s = ((red[0][h][k][tr] + red[1][h][k][tr]) + red[2][h][k][tr]) + red[3][h][k][tr];
     float v = round_to(s, DT_BF16);
-    if (routing == ROUTE_SOFTMAX) {
+    if (KC <= 2 && routing == ROUTE_SOFTMAX) {
       // softmax of the bf16 logits over the token's KP lanes (routes >= K
       // excluded), rounded to bf16
       const float l = (k < K) ? v : -INFINITY;
@@ -140,7 +207,7 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 #pragma unroll
       for (int o = KP / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
       v = round_to(e * (1.0f / sum), DT_BF16);
-    } else if (routing == ROUTE_EXP) {
+    } else if (KC <= 2 && routing == ROUTE_EXP) {
       v = round_to(__expf(v), DT_BF16);
     }
     if (k < K && tok < rows) logits[(t0 + tok) * K + k] = f32_to_bf16(v);
@@ -156,10 +223,33 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 // the result lane (j, q) holds columns 8 q + {0..7} (tiles 0, 1) and
 // 32 + 8 q + {0..7} (tiles 2, 3) of token t_j: two 16-byte stores, and each
 // store instruction writes 64 contiguous bytes of every token row.
-constexpr int kDzBlocks = 8;
+// token blocks per wave: 8 up to 32 routes, 4 above (registers)
+template <int KC>
+constexpr int kDzBlocks = KC <= 2 ? 8 : 4;
 
 __device__ __forceinline__ int dz_col(int tl, int r) {
   return 32 * (tl >> 1) + 8 * (r >> 2) + 4 * (tl & 1) + (r & 3);
+}
+
+// One 16 x 16 tile of router^T . dl^T over KC route chunks.  One route chunk:
+// a 16x16x16 MFMA.  More: chunk pairs in 16x16x32 MFMAs, an odd last chunk
+// paired with zeros, so that the accumulator chain never mixes MFMA shapes (a
+// 16x16x16 accumulating onto a 16x16x32 result gave wrong rows here).
+template <int KC>
+__device__ __forceinline__ f32x4 dz_tile(const s16x4 (&a)[KC], const s16x4 (&b)[KC]) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (KC == 1) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a[0], b[0], acc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int kc = 0; kc + 1 < KC; kc += 2)
+      acc = mfma::mma32(a[kc], a[kc + 1], b[kc], b[kc + 1], acc);
+    if constexpr (KC % 2 == 1) {
+      const s16x4 zero = {0, 0, 0, 0};
+      acc = mfma::mma32(a[KC - 1], zero, b[KC - 1], zero, acc);
+    }
+  }
+  return acc;
 }
 
 template <int KC>
@@ -174,11 +264,12 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
   const Buf rb(r, static_cast<int64_t>(K) * Z * 2);
   const Buf db(dl, N * K * 2);
   const Buf ob(dz, N * Z * 2);
-  const int64_t tb = static_cast<int64_t>(blockIdx.y) * kDzBlocks * 16;
+  constexpr int NBLK = kDzBlocks<KC>;
+  const int64_t tb = static_cast<int64_t>(blockIdx.y) * NBLK * 16;
   // B operands of all blocks first: rows past N load zeros
-  s16x4 bop[kDzBlocks][KC];
+  s16x4 bop[NBLK][KC];
 #pragma unroll
-  for (int b = 0; b < kDzBlocks; ++b)
+  for (int b = 0; b < NBLK; ++b)
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       const int k = 16 * kc + 4 * qq;
@@ -202,19 +293,11 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
                           static_cast<short>(e[2]), static_cast<short>(e[3])};
     }
 #pragma unroll
-  for (int b = 0; b < kDzBlocks; ++b) {
+  for (int b = 0; b < NBLK; ++b) {
     const int64_t t = tb + 16 * b + i;
     f32x4 acc[4];
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl) {
-      if constexpr (KC == 1) {
-        acc[tl] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bop[b][0],
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-      } else {
-        acc[tl] = mfma::mma32(aop[tl][0], aop[tl][1], bop[b][0], bop[b][1],
-                              f32x4{0.f, 0.f, 0.f, 0.f});
-      }
-    }
+    for (int tl = 0; tl < 4; ++tl) acc[tl] = dz_tile<KC>(aop[tl], bop[b]);
     // rows past N lie outside the buffer: their stores are dropped
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -246,7 +329,7 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
   constexpr int KROW = KP + 4;  // padded LDS row of a dl tile (bf16)
   __shared__ __align__(16) uint16_t zt[4][32][kZRow];
   __shared__ __align__(16) uint16_t dt[4][32][KROW];
-  __shared__ float red[4][KP][65];
+  __shared__ float red[KP][65];
   const int lane = threadIdx.x & 63, w = wave_id();
   const int i = lane & 15, qq = lane >> 4;
   const int zs = blockIdx.x * 64;
@@ -327,18 +410,26 @@ __global__ void __launch_bounds__(256) router_dr_kernel(const uint16_t* __restri
     load_block(rb2, b + 12);
   }
   if (it < nb) mult_block(ra);
-  // D lane (j, q): column 16 tl + j, routes 16 kc + 4 q + v
+  // D lane (j, q): column 16 tl + j, routes 16 kc + 4 q + v.  The waves' tiles
+  // are summed in wave order, ((w0 + w1) + w2) + w3, one wave at a time.
 #pragma unroll
-  for (int tl = 0; tl < 4; ++tl)
+  for (int ww = 0; ww < 4; ++ww) {
+    if (w == ww) {
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
+      for (int tl = 0; tl < 4; ++tl)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) red[w][16 * kc + 4 * qq + v][16 * tl + i] = acc[tl][kc][v];
-  __syncthreads();
+        for (int kc = 0; kc < KC; ++kc)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            float& cell = red[16 * kc + 4 * qq + v][16 * tl + i];
+            cell = (ww == 0) ? acc[tl][kc][v] : cell + acc[tl][kc][v];
+          }
+    }
+    __syncthreads();
+  }
   for (int idx = threadIdx.x; idx < K * 64; idx += 256) {
     const int k = idx / 64, col = idx % 64;
-    const float s = ((red[0][k][col] + red[1][k][col]) + red[2][k][col]) + red[3][k][col];
-    part[(static_cast<int64_t>(blockIdx.y) * K + k) * Z + zs + col] = s;
+    part[(static_cast<int64_t>(blockIdx.y) * K + k) * Z + zs + col] = red[k][col];
   }
 }
 
@@ -448,15 +539,7 @@ __global__ void __launch_bounds__(256) router_bwd_kernel(const uint16_t* __restr
     for (int hb = 0; hb < 2; ++hb) {
       f32x4 o[4];
 #pragma unroll
-      for (int tl = 0; tl < 4; ++tl) {
-        if constexpr (KC == 1) {
-          o[tl] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(aop[tl][0], bd[hb][0],
-                                                            f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        } else {
-          o[tl] = mfma::mma32(aop[tl][0], aop[tl][1], bd[hb][0], bd[hb][1],
-                              f32x4{0.f, 0.f, 0.f, 0.f});
-        }
-      }
+      for (int tl = 0; tl < 4; ++tl) o[tl] = dz_tile<KC>(aop[tl], bd[hb]);
       const int64_t t = t0 + 16 * hb + i;
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
@@ -552,8 +635,8 @@ BwdPlan bwd_plan(int64_t N, int64_t Z) {
 
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt) {
   // buffer resources address [N, Z] bf16 with 32-bit byte offsets
-  return dt == DT_BF16 && K > 0 && K <= 32 && K % 4 == 0 && Z >= 64 && Z % 64 == 0 && N > 0 &&
-         N * Z * 2 < (int64_t(1) << 31);
+  return dt == DT_BF16 && K > 0 && K <= kRouterMaxK && K % 4 == 0 && Z >= 64 && Z % 64 == 0 &&
+         N > 0 && N * Z * 2 < (int64_t(1) << 31);
 }
 
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
@@ -561,18 +644,83 @@ size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
   return static_cast<size_t>(pl.ranges * K * Z) * 4;
 }
 
+namespace router {
+
+// Launch F<KC> with KC = ceil(K / 16) (1..6).
+template <template <int> class F, typename... A>
+void with_kc(int64_t K, A&&... a) {
+  switch ((K + 15) / 16) {
+    case 1: F<1>::run(a...); break;
+    case 2: F<2>::run(a...); break;
+    case 3: F<3>::run(a...); break;
+    case 4: F<4>::run(a...); break;
+    case 5: F<5>::run(a...); break;
+    default: F<6>::run(a...); break;
+  }
+}
+
+template <int KC>
+struct FwdLaunch {
+  static void run(const uint16_t* z, const uint16_t* r, uint16_t* out, int64_t N, int Z, int K,
+                  int routing, const RouteGroups& grp, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(cdiv(N, 32)));
+    if (grp.n > 0)
+      hipLaunchKernelGGL((router_fwd_kernel<KC, true>), grid, dim3(256), 0, st, z, r, out, N, Z, K,
+                         routing, grp);
+    else
+      hipLaunchKernelGGL((router_fwd_kernel<KC, false>), grid, dim3(256), 0, st, z, r, out, N, Z,
+                         K, routing, grp);
+  }
+};
+
+template <int KC>
+struct DzLaunch {
+  static void run(const uint16_t* dl, const uint16_t* r, uint16_t* dz, int64_t N, int Z, int K,
+                  hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(cdiv(Z / 64, 4)),
+                    static_cast<unsigned>(cdiv(N, 16 * kDzBlocks<KC>)));
+    hipLaunchKernelGGL(router_dz_kernel<KC>, grid, dim3(256), 0, st, dl, r, dz, N, Z, K);
+  }
+};
+
+template <int KC>
+struct DrLaunch {
+  static void run(const uint16_t* dl, const uint16_t* z, float* part, int64_t N, int Z, int K,
+                  const BwdPlan& pl, hipStream_t st) {
+    const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
+    hipLaunchKernelGGL(router_dr_kernel<KC>, grid, dim3(256), 0, st, dl, z, part, N, Z, K,
+                       static_cast<int>(pl.blocks_per_range));
+  }
+};
+
+void dr_reduce(const float* part, void* dr, int64_t K, int64_t Z, const BwdPlan& pl,
+               hipStream_t st) {
+  const int64_t KZ = K * Z;
+  hipLaunchKernelGGL(router_dr_reduce_kernel, dim3(static_cast<unsigned>(cdiv(KZ, 256))),
+                     dim3(256), 0, st, part, static_cast<uint16_t*>(dr), KZ,
+                     static_cast<int>(pl.ranges));
+}
+
+}  // namespace router
+
 void router_forward(const void* z, const void* r, void* logits, int64_t N, int64_t Z, int64_t K,
                     int routing, hipStream_t st) {
-  const dim3 grid(static_cast<unsigned>(router::cdiv(N, 32)));
-  const auto* zp = static_cast<const uint16_t*>(z);
-  const auto* rp = static_cast<const uint16_t*>(r);
-  auto* lp = static_cast<uint16_t*>(logits);
-  if (K <= 16)
-    hipLaunchKernelGGL(router::router_fwd_kernel<1>, grid, dim3(256), 0, st, zp, rp, lp, N,
-                       static_cast<int>(Z), static_cast<int>(K), routing);
-  else
-    hipLaunchKernelGGL(router::router_fwd_kernel<2>, grid, dim3(256), 0, st, zp, rp, lp, N,
-                       static_cast<int>(Z), static_cast<int>(K), routing);
+  // the fused activation (routing 1 / 2) is built for K <= 32 only
+  const RouteGroups none{};
+  router::with_kc<router::FwdLaunch>(K, static_cast<const uint16_t*>(z),
+                                     static_cast<const uint16_t*>(r),
+                                     static_cast<uint16_t*>(logits), N, static_cast<int>(Z),
+                                     static_cast<int>(K), K <= 32 ? routing : ROUTE_ALPHA, none,
+                                     st);
+}
+
+void router_forward_grouped(const void* z, const void* r, const RouteGroups& groups, int64_t N,
+                            int64_t Z, hipStream_t st) {
+  int K = 0;
+  for (int g = 0; g < groups.n; ++g) K += groups.kn[g];
+  router::with_kc<router::FwdLaunch>(K, static_cast<const uint16_t*>(z),
+                                     static_cast<const uint16_t*>(r), static_cast<uint16_t*>(nullptr),
+                                     N, static_cast<int>(Z), K, ROUTE_ALPHA, groups, st);
 }
 
 void router_backward(const void* z, const void* r, const void* dl, void* dz, void* dr,
@@ -581,9 +729,10 @@ void router_backward(const void* z, const void* r, const void* dl, void* dz, voi
   const auto* rp = static_cast<const uint16_t*>(r);
   const auto* dp = static_cast<const uint16_t*>(dl);
   const int Zi = static_cast<int>(Z), Ki = static_cast<int>(K);
-  if (dz != nullptr && dr != nullptr && std::getenv("MOC_ROUTER_SPLIT") == nullptr) {
-    const router::BwdPlan pl = router::bwd_plan(N, Z);
-    float* part = static_cast<float*>(workspace);
+  const router::BwdPlan pl = router::bwd_plan(N, Z);
+  float* part = static_cast<float*>(workspace);
+  // both outputs, K <= 32: one pass over z and dz
+  if (dz != nullptr && dr != nullptr && K <= 32 && std::getenv("MOC_ROUTER_SPLIT") == nullptr) {
     const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
     auto* op = static_cast<uint16_t*>(dz);
     if (K <= 16)
@@ -592,36 +741,14 @@ void router_backward(const void* z, const void* r, const void* dl, void* dz, voi
     else
       hipLaunchKernelGGL(router::router_bwd_kernel<2>, grid, dim3(256), 0, st, dp, zp, rp, op,
                          part, N, Zi, Ki, static_cast<int>(pl.blocks_per_range));
-    const int64_t KZ = K * Z;
-    hipLaunchKernelGGL(router::router_dr_reduce_kernel, dim3(static_cast<unsigned>(router::cdiv(KZ, 256))),
-                       dim3(256), 0, st, part, static_cast<uint16_t*>(dr), KZ,
-                       static_cast<int>(pl.ranges));
+    router::dr_reduce(part, dr, K, Z, pl, st);
     return;
   }
-  if (dz != nullptr) {
-    const int64_t waves_x = Z / 64;
-    const dim3 grid(static_cast<unsigned>(router::cdiv(waves_x, 4)),
-                    static_cast<unsigned>(router::cdiv(N, 16 * router::kDzBlocks)));
-    auto* op = static_cast<uint16_t*>(dz);
-    if (K <= 16)
-      hipLaunchKernelGGL(router::router_dz_kernel<1>, grid, dim3(256), 0, st, dp, rp, op, N, Zi, Ki);
-    else
-      hipLaunchKernelGGL(router::router_dz_kernel<2>, grid, dim3(256), 0, st, dp, rp, op, N, Zi, Ki);
-  }
+  if (dz != nullptr)
+    router::with_kc<router::DzLaunch>(K, dp, rp, static_cast<uint16_t*>(dz), N, Zi, Ki, st);
   if (dr != nullptr) {
-    const router::BwdPlan pl = router::bwd_plan(N, Z);
-    float* part = static_cast<float*>(workspace);
-    const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
-    if (K <= 16)
-      hipLaunchKernelGGL(router::router_dr_kernel<1>, grid, dim3(256), 0, st, dp, zp, part, N, Zi,
-                         Ki, static_cast<int>(pl.blocks_per_range));
-    else
-      hipLaunchKernelGGL(router::router_dr_kernel<2>, grid, dim3(256), 0, st, dp, zp, part, N, Zi,
-                         Ki, static_cast<int>(pl.blocks_per_range));
-    const int64_t KZ = K * Z;
-    hipLaunchKernelGGL(router::router_dr_reduce_kernel, dim3(static_cast<unsigned>(router::cdiv(KZ, 256))),
-                       dim3(256), 0, st, part, static_cast<uint16_t*>(dr), KZ,
-                       static_cast<int>(pl.ranges));
+    router::with_kc<router::DrLaunch>(K, dp, zp, part, N, Zi, Ki, pl, st);
+    router::dr_reduce(part, dr, K, Z, pl, st);
   }
 }
 

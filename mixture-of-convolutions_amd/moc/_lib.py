@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "moc_router_supported",
     "moc_router_forward",
     "moc_router_forward_routed",
+    "moc_router_forward_grouped",
     "moc_router_backward_workspace_bytes",
     "moc_router_backward",
 )
@@ -101,6 +102,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_router_forward.restype = _i
     lib.moc_router_forward_routed.argtypes = [_p, _p, _p, _l, _l, _l, _i, _i, _p]
     lib.moc_router_forward_routed.restype = _i
+    lib.moc_router_forward_grouped.argtypes = [_p, _p, _p, _p, _p, _i, _l, _l, _i, _p]
+    lib.moc_router_forward_grouped.restype = _i
     lib.moc_router_backward_workspace_bytes.argtypes = [_l, _l, _l, _i]
     lib.moc_router_backward_workspace_bytes.restype = _z
     lib.moc_router_backward.argtypes = [_p, _p, _p, _p, _p, _l, _l, _l, _i, _p, _z, _p]

@@ -271,6 +271,65 @@ class _MoCLayerFunction(torch.autograd.Function):
         return dx, dz, dr, dbasis, None, None, None, None, None, None
 
 
+class _MoCGroupFunction(torch.autograd.Function):
+    """Several MoC layers on one routing input z as one autograd node: one
+    router pass over the concatenated routers forms every layer's weights, each
+    layer's MoC forward / backward runs on its weights (routing *_WEIGHTS), and
+    one router backward over the layers' logits gradients side by side gives
+    dz (their sum) and every drouter."""
+
+    @staticmethod
+    def forward(ctx, z, spec, *tensors):
+        # spec: (n, activations, router_activations, cu_seqlens, max_seqlen,
+        #        cu_seqlens_cpu, chunk_indices); tensors: routers, xs, bases
+        n, acts, routes, cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices = spec
+        routers, xs, bases = tensors[:n], tensors[n:2 * n], tensors[2 * n:]
+        ks = [r.shape[0] for r in routers]
+        router_cat = torch.cat([r.contiguous() for r in routers], 0)
+        weights = ops.router_forward_grouped(z, router_cat, ks,
+                                             [_ROUTING_CODES[r] for r in routes])
+        ys, saved_x, saved_b = [], [], []
+        cu = None
+        for g in range(n):
+            x, w, b, cu = _prepare(None, xs[g], weights[g], bases[g], cu_seqlens, max_seqlen,
+                                   cu_seqlens_cpu, chunk_indices)
+            ys.append(ops.launch_forward(x, w, b, activation_flag=activation_flag(acts[g]),
+                                         cu_seqlens=cu, routing=_WEIGHTS_CODES[routes[g]]))
+            saved_x.append(x)
+            saved_b.append(b)
+        tail = () if cu is None else (cu,)
+        ctx.save_for_backward(z, router_cat, *saved_x, *weights, *saved_b, *tail)
+        ctx.spec = (n, [activation_flag(a) for a in acts], [_WEIGHTS_CODES[r] for r in routes],
+                    ks, cu is not None)
+        return tuple(ys)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, *dys):
+        n, acts, codes, ks, varlen = ctx.spec
+        saved = ctx.saved_tensors
+        z, router_cat = saved[0], saved[1]
+        xs, weights, bases = saved[2:2 + n], saved[2 + n:2 + 2 * n], saved[2 + 2 * n:2 + 3 * n]
+        cu = saved[2 + 3 * n] if varlen else None
+        dxs, dls, dbs = [], [], []
+        for g in range(n):
+            dy = dys[g] if dys[g] is not None else torch.zeros_like(xs[g])
+            dx, dl, db = ops.launch_backward(xs[g], weights[g], bases[g], dy,
+                                             activation_flag=acts[g],
+                                             need_x=ctx.needs_input_grad[2 + n + g],
+                                             cu_seqlens=cu, routing=codes[g])
+            dxs.append(dx)
+            dls.append(dl)
+            dbs.append(db)
+        need_z = ctx.needs_input_grad[0]
+        need_r = any(ctx.needs_input_grad[2:2 + n])
+        dz, dr = None, None
+        if need_z or need_r:
+            dz, dr = ops.router_backward(z, router_cat, torch.cat(dls, -1), need_z, need_r)
+        drs = list(dr.split(ks, 0)) if dr is not None else [None] * n
+        return (dz, None, *drs, *dxs, *dbs)
+
+
 def router_linear(z: torch.Tensor, router: torch.Tensor) -> torch.Tensor:
     """``F.linear(z, router)`` of ``MoC.forward`` (moc/api.py:383): the router
     kernels of the HIP library where they apply (bf16, k % 4 == 0, k <= 32,
@@ -403,7 +462,8 @@ class MoC(nn.Module):
                                        activation_flag=activation_flag(self.activation),
                                        routing=_ROUTING_CODES[self.router_activation])
             return y[:, None], (cache if output_final_state else None)
-        if cache is None and ops.router_supported(z, self.router):
+        if (cache is None and self.router.shape[0] <= ops.ROUTER_MAX_ROUTED_K
+                and ops.router_supported(z, self.router)):
             return self._forward_kernels(x, z, output_final_state, cu_seqlens, max_seqlen,
                                          cu_seqlens_cpu, chunk_indices)
         logits = router_linear(z, self.router)
@@ -447,4 +507,74 @@ class MoC(nn.Module):
         return self.dim * self.kernel_size
 
 
-__all__ = ["MoC", "moc_triton", "moc_hip", "router_linear"]
+class MoCGroup(nn.Module):
+    """MoC layers that share their routing input ``z``, run together: the QKV
+    pattern of the reference README (README.md:80-129), where each of
+    ``q_conv(q, x_norm)``, ``k_conv(k, x_norm)``, ``v_conv(v, x_norm)`` runs its
+    own router GEMM over ``x_norm`` (moc/api.py:383-388).
+
+    ``MoCGroup(q_conv, k_conv, v_conv)(xs=[q, k, v], z=x_norm)`` returns the
+    same ``[(y, state), ...]`` as calling the layers one by one.  For bf16
+    layers on the library's router kernels (at most 4 layers, k % 4 == 0,
+    k <= 32 each) the routers run as one: z is read once in the forward, and
+    once in the backward, which writes dz once instead of once per layer plus
+    autograd's sum.  Otherwise, or with a cache, the layers run one by one.
+    The layers keep their parameters (held here as submodules).
+    """
+
+    def __init__(self, *layers: MoC) -> None:
+        super().__init__()
+        if not layers:
+            raise ValueError("MoCGroup needs at least one MoC layer")
+        if any(not isinstance(m, MoC) for m in layers):
+            raise TypeError("MoCGroup takes MoC layers")
+        if len({m.z_dim for m in layers}) != 1:
+            raise ValueError("the layers of a MoCGroup must share z_dim")
+        self.layers = nn.ModuleList(layers)
+
+    def _grouped(self, xs, z, cache) -> bool:
+        return (cache is None and ops.router_grouped_supported(z, [m.router for m in self.layers])
+                and all(isinstance(x, torch.Tensor) and x.device == z.device for x in xs))
+
+    def forward(self, xs, z: torch.Tensor, cache=None, output_final_state: bool = False,
+                cu_seqlens: Optional[torch.Tensor] = None, max_seqlen: Optional[int] = None,
+                cu_seqlens_cpu: Optional[torch.Tensor] = None,
+                chunk_indices: Optional[torch.Tensor] = None
+                ) -> list[tuple[torch.Tensor, torch.Tensor | None]]:
+        xs = list(xs)
+        if len(xs) != len(self.layers):
+            raise ValueError(f"MoCGroup of {len(self.layers)} layers got {len(xs)} inputs")
+        caches = list(cache) if cache is not None else [None] * len(xs)
+        if len(caches) != len(xs):
+            raise ValueError(f"MoCGroup of {len(self.layers)} layers got {len(caches)} caches")
+        if not self._grouped(xs, z, cache):
+            return [m(x, z, cache=c, output_final_state=output_final_state, cu_seqlens=cu_seqlens,
+                      max_seqlen=max_seqlen, cu_seqlens_cpu=cu_seqlens_cpu,
+                      chunk_indices=chunk_indices)
+                    for m, x, c in zip(self.layers, xs, caches)]
+        for m in self.layers:
+            activation_flag(m.activation)
+        n = len(xs)
+        routers = [m.router for m in self.layers]
+        bases = [m.conv_bases for m in self.layers]
+        acts = [m.activation for m in self.layers]
+        routes = [m.router_activation for m in self.layers]
+        if cu_seqlens is None:
+            if cu_seqlens_cpu is not None or chunk_indices is not None:
+                raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+            spec = (n, acts, routes, None, None, None, None)
+            ys = _MoCGroupFunction.apply(z, spec, *routers, *xs, *bases)
+            return [(y, _final_state(x, None, m.kernel_size) if output_final_state else None)
+                    for y, x, m in zip(ys, xs, self.layers)]
+        if output_final_state:
+            raise ValueError("cache and output_final_state are only supported for fixed-length inputs")
+        if max_seqlen is None:
+            raise ValueError("max_seqlen is required for varlen inputs")
+        packed = [_canonicalize_packed_input(x, z) for x in xs]
+        restore = packed[0][2]
+        spec = (n, acts, routes, cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices)
+        ys = _MoCGroupFunction.apply(packed[0][1], spec, *routers, *[p[0] for p in packed], *bases)
+        return [((y[None] if restore else y), None) for y in ys]
+
+
+__all__ = ["MoC", "MoCGroup", "moc_triton", "moc_hip", "router_linear"]

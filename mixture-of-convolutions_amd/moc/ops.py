@@ -249,10 +249,15 @@ _router_support_cache: dict[tuple, bool] = {}
 
 def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
     """Whether the router GEMM of ``MoC.forward`` runs on the library's kernels
-    (bf16 z and router on a GPU, k % 4 == 0, k <= 32, z_dim % 64 == 0)."""
+    (bf16 z and router on a GPU, k % 4 == 0, k <= 96, z_dim % 64 == 0; the
+    fused router activation further needs k <= 32)."""
     if not (z.is_cuda and router.is_cuda) or z.dtype != torch.bfloat16 or router.dtype != z.dtype:
         return False
     K, Z = router.shape
+    return _router_shape_supported(z, K, Z)
+
+
+def _router_shape_supported(z: torch.Tensor, K: int, Z: int) -> bool:
     if z.shape[-1] != Z or z.numel() == 0:
         return False
     N = z.numel() // Z
@@ -286,6 +291,53 @@ def router_forward(z: torch.Tensor, router: torch.Tensor, routing: int = ROUTE_A
                                              _lib.stream_ptr(z.device))
     _lib.check(rc, "moc_router_forward")
     return out
+
+
+ROUTER_MAX_ROUTED_K = 32   # the fused router activation
+ROUTER_MAX_GROUPS = 4
+
+
+def router_grouped_supported(z: torch.Tensor, routers: list[torch.Tensor]) -> bool:
+    """Whether ``router_forward_grouped`` applies: bf16 z and routers on one
+    GPU, at most 4 groups of k % 4 == 0, k <= 32 routes, 96 in all."""
+    if not routers or len(routers) > ROUTER_MAX_GROUPS:
+        return False
+    if not z.is_cuda or z.dtype != torch.bfloat16:
+        return False
+    if any(r.dtype != torch.bfloat16 or r.device != z.device or r.ndim != 2 for r in routers):
+        return False
+    ks = [r.shape[0] for r in routers]
+    if any(k % 4 or k > ROUTER_MAX_ROUTED_K for k in ks):
+        return False
+    Z = routers[0].shape[1]
+    if any(r.shape[1] != Z for r in routers):
+        return False
+    return _router_shape_supported(z, sum(ks), Z)
+
+
+def router_forward_grouped(z: torch.Tensor, router_cat: torch.Tensor, ks: list[int],
+                           routings: list[int]) -> list[torch.Tensor]:
+    """One pass over z against the concatenated routers [sum(ks), Z]: group g's
+    weights routings[g] (softmax / exp, or 0 for the logits) of its logits,
+    each [..., ks[g]] bf16 (the F.linear + activation of several MoC.forward
+    calls on one z, moc/api.py:383-388)."""
+    import ctypes
+    L = _lib.lib()
+    z = z.contiguous()
+    r = router_cat.contiguous()
+    Z = r.shape[1]
+    N = z.numel() // Z
+    outs = [torch.empty(*z.shape[:-1], k, dtype=z.dtype, device=z.device) for k in ks]
+    n = len(ks)
+    ptrs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    karr = (ctypes.c_int64 * n)(*ks)
+    rarr = (ctypes.c_int * n)(*routings)
+    with _lib.device_guard(z.device):
+        rc = L.moc_router_forward_grouped(z.data_ptr(), r.data_ptr(), ctypes.addressof(ptrs),
+                                          ctypes.addressof(karr), ctypes.addressof(rarr), n, N,
+                                          Z, _lib.DT_BF16, _lib.stream_ptr(z.device))
+    _lib.check(rc, "moc_router_forward_grouped")
+    return outs
 
 
 def router_backward(z: torch.Tensor, router: torch.Tensor, dlogits: torch.Tensor,

@@ -105,3 +105,28 @@ def test_dtype_codes():
     with pytest.raises(TypeError):
         _lib.dtype_code(torch.int8)
     assert isinstance(_lib.lib(), ctypes.CDLL)
+
+
+def test_router_grouped_rejects_bad_groups():
+    """moc_router_forward_grouped validates its group arrays before any launch."""
+    L = _lib.lib()
+
+    def call(ks, routes, outs=None, n=None, Z=64):
+        n = len(ks) if n is None else n
+        m = max(n, 1)
+        karr = (ctypes.c_int64 * m)(*ks)
+        rarr = (ctypes.c_int * m)(*routes)
+        ptrs = (ctypes.c_void_p * m)(*(outs if outs is not None else [FAKE] * m))
+        return L.moc_router_forward_grouped(FAKE, FAKE, ctypes.addressof(ptrs),
+                                            ctypes.addressof(karr), ctypes.addressof(rarr), n,
+                                            100, Z, 1, None)
+
+    assert call([16], [1], n=0) == -1
+    assert call([16] * 5, [1] * 5) == -1            # more than 4 groups
+    assert call([18], [1]) == -1                    # k % 4 != 0
+    assert call([36], [1]) == -1                    # k > 32
+    assert call([32, 32, 32, 4], [1, 1, 1, 1]) == -1  # 100 routes in all
+    assert call([16], [3]) == -1                    # routing code
+    assert call([16], [1], outs=[FAKE + 2]) == -1   # misaligned output
+    assert call([16], [1], Z=48) == -1              # z_dim % 64 != 0
+    assert b"group" in L.moc_last_error() or b"z_dim" in L.moc_last_error()

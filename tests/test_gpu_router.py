@@ -5,7 +5,7 @@ backward), which replace the F.linear(z, router) of MoC.forward
 References are plain fp32 products of the same bf16 inputs; the bf16 outputs
 are held to the bf16 rule of tests/_parity.py.  Shapes cover single tokens,
 token counts that are not multiples of the 16-token tiles, every supported k
-class (k % 4 == 0 up to 32, with and without a second 16-route half) and the
+class (k % 4 == 0 up to 96, one to six 16-route chunks) and the
 BASELINE sizes.
 """
 from __future__ import annotations
@@ -24,6 +24,8 @@ BF = torch.bfloat16
 SHAPES = [
     (1, 64, 16), (15, 64, 4), (16, 128, 16), (17, 192, 12), (50, 64, 20), (77, 320, 28),
     (333, 256, 32), (1000, 2048, 16), (4096, 4096, 32), (16384, 2048, 16),
+    (70, 128, 36), (129, 192, 48), (33, 64, 64), (300, 256, 80), (1000, 512, 96),
+    (16384, 4096, 96),
 ]
 
 
@@ -68,7 +70,7 @@ def test_router_batched_input_and_autograd():
     assert_close("drouter", r.grad, dl.float().reshape(-1, K).T @ zf.reshape(-1, Z), BF)
 
 
-@pytest.mark.parametrize("Z,K,dtype", [(48, 16, BF), (64, 6, BF), (64, 36, BF), (64, 16, torch.float32)])
+@pytest.mark.parametrize("Z,K,dtype", [(48, 16, BF), (64, 6, BF), (64, 100, BF), (64, 16, torch.float32)])
 def test_router_unsupported_shapes_use_torch(Z, K, dtype):
     g = gen(Z + K)
     z = randn(g, 5, Z).to(DEV, dtype)
@@ -175,3 +177,98 @@ def test_router_forward_routed_weights(K, route):
     assert w.dtype == BF and w.shape == (N, K)
     # one bf16 ulp: torch's exp / division may round differently in fp32
     assert_close("weights", w, ref, BF)
+
+
+def _qkv_layers(specs, Z, seed):
+    """MoC layers (dim, k, S, activation, router_activation) on one z_dim, bf16."""
+    g = gen(seed)
+    layers = []
+    for D, K, S, act, route in specs:
+        m = MoC(D, Z, S, K, activation=act, init_std=0.1, router_activation=route)
+        with torch.no_grad():
+            m.router.copy_(randn(g, K, Z, scale=0.05))
+        layers.append(m.to(DEV, BF))
+    return layers, g
+
+
+def _run_layers(layers, xs, z, dys, grouped, **kw):
+    for m in layers:
+        m.zero_grad(set_to_none=True)
+    xi = [x.clone().requires_grad_() for x in xs]
+    zi = z.clone().requires_grad_()
+    if grouped:
+        outs = moc.MoCGroup(*layers)(xi, zi, **kw)
+    else:
+        outs = [m(x, zi, **kw) for m, x in zip(layers, xi)]
+    torch.autograd.backward([y for y, _ in outs], dys)
+    return ([y.detach() for y, _ in outs], [x.grad for x in xi], zi.grad,
+            [m.router.grad.clone() for m in layers], [m.conv_bases.grad.clone() for m in layers])
+
+
+QKV_SPECS = [
+    [(256, 32, 8, None, "exp"), (64, 32, 8, None, "exp"), (64, 32, 8, None, "softmax")],
+    [(192, 16, 4, "silu", "softmax"), (128, 20, 3, None, "exp")],
+    [(128, 8, 2, "silu", "softmax"), (64, 4, 4, None, "exp"), (64, 12, 4, None, "softmax"),
+     (32, 32, 8, "silu", "exp")],
+]
+
+
+@pytest.mark.parametrize("specs", QKV_SPECS)
+@pytest.mark.parametrize("varlen", [False, True])
+def test_group_matches_separate_layers(specs, varlen):
+    """MoCGroup (one router pass over the concatenated routers, one router
+    backward) against the same layers called one by one: y, dx, drouter and
+    dbasis bit for bit (same kernels, same reduction order); dz, which the
+    group sums over all routes in fp32 while autograd adds the layers' bf16
+    dz, within the bf16 rule."""
+    Z, B, T = 128, 2, 61
+    layers, g = _qkv_layers(specs, Z, len(specs) * 10 + varlen)
+    if varlen:
+        lengths = [5, 40, 1, 70, 7]
+        cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32,
+                          device=DEV)
+        lead, kw = (sum(lengths),), dict(cu_seqlens=cu, max_seqlen=max(lengths))
+    else:
+        lead, kw = (B, T), {}
+    xs = [randn(g, *lead, D).to(DEV, BF) for D, *_ in specs]
+    z = randn(g, *lead, Z).to(DEV, BF)
+    dys = [randn(g, *lead, D, scale=0.1).to(DEV, BF) for D, *_ in specs]
+    assert moc.ops.router_grouped_supported(z, [m.router for m in layers])
+    got = _run_layers(layers, xs, z, dys, True, **kw)
+    ref = _run_layers(layers, xs, z, dys, False, **kw)
+    for name, a, b in (("y", got[0], ref[0]), ("dx", got[1], ref[1]), ("drouter", got[3], ref[3]),
+                       ("dbasis", got[4], ref[4])):
+        for i, (u, v) in enumerate(zip(a, b)):
+            assert torch.equal(u, v), f"{name}[{i}]"
+    assert_close("dz", got[2], ref[2].float(), BF)
+
+
+def test_group_falls_back_to_layers():
+    """fp32 layers (no router kernels): the group runs the layers one by one."""
+    Z = 64
+    g = gen(3)
+    layers = [MoC(64, Z, 4, 8, init_std=0.1).to(DEV), MoC(32, Z, 4, 8, init_std=0.1).to(DEV)]
+    for m in layers:
+        with torch.no_grad():
+            m.router.copy_(randn(g, 8, Z, scale=0.1))
+    xs = [randn(g, 2, 9, 64).to(DEV), randn(g, 2, 9, 32).to(DEV)]
+    z = randn(g, 2, 9, Z).to(DEV)
+    assert not moc.ops.router_grouped_supported(z, [m.router for m in layers])
+    outs = moc.MoCGroup(*layers)(xs, z, output_final_state=True)
+    for (y, st), m, x in zip(outs, layers, xs):
+        y2, st2 = m(x, z, output_final_state=True)
+        assert torch.equal(y, y2) and torch.equal(st, st2)
+
+
+@pytest.mark.parametrize("ks,routes", [([32, 32, 32], [2, 2, 1]), ([16, 20], [1, 0]),
+                                       ([4, 8, 12, 28], [1, 2, 1, 2])])
+def test_router_forward_grouped_matches_per_router(ks, routes):
+    """The grouped router pass against one router launch per group: bit for bit
+    (routing 0 gives the group's logits)."""
+    N, Z = 301, 192
+    g = gen(sum(ks))
+    z = randn(g, N, Z).to(DEV, BF)
+    rs = [randn(g, k, Z, scale=0.05).to(DEV, BF) for k in ks]
+    outs = ops.router_forward_grouped(z, torch.cat(rs, 0), ks, routes)
+    for o, r, code in zip(outs, rs, routes):
+        assert torch.equal(o, ops.router_forward(z, r, routing=code))
