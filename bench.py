@@ -40,11 +40,11 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 VALU_PEAK = 157.3e12       # flop/s, MI355X fp32 vector (packed)
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
-# FETCH_SIZE (68780 KiB) and WRITE_SIZE (98367 KiB) per dispatch of
+# FETCH_SIZE (68654 KiB) and WRITE_SIZE (98373 KiB) per dispatch of
 # `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
 # 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
 # 131072 KiB -> factor 1.0)
-TRAFFIC_BWD = 241_563_114
+TRAFFIC_BWD = 241_337_344
 DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
 
 
