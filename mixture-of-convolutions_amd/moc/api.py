@@ -362,6 +362,29 @@ def _step(x, a, basis, cache, activation, router_activation):
     return y[:, None]
 
 
+def _prefill(x, a, basis, cache, activation, router_activation):
+    """Prefill continuing from a cache (moc/api.py:299-307).  The reference
+    prepends the whole cache to x (and zero routing to a) and drops the first
+    S outputs.  Only the first S-1 tokens of each sequence have taps that reach
+    into the cache, so here the op runs on x as it is, and those tokens are
+    recomputed from a short window (the S-1 newest cached tokens, then the
+    tokens themselves) and written over the first result.  No copy of x; y is
+    the reference's bit for bit (each token's output depends only on its own
+    window), and gradients flow to x, a, basis and the cache as there."""
+    B, T, _ = x.shape
+    KS = basis.shape[1]
+    y = _apply(x, a, basis, activation, router_activation)
+    h = min(KS - 1, T)
+    if h == 0:
+        return y
+    hist = cache.transpose(1, 2)[:, 1:]
+    xh = torch.cat((hist, x[:, :h]), 1)
+    ah = torch.cat((a.new_zeros(B, KS - 1, a.shape[-1]), a[:, :h]), 1)
+    yh = _apply(xh, ah, basis, activation, router_activation)[:, KS - 1:]
+    y[:, :h] = yh
+    return y
+
+
 def _dispatch(x, a, basis, cache, output_final_state, activation, router_activation,
               cu_seqlens, max_seqlen, cu_seqlens_cpu, chunk_indices):
     """Routing of moc/api.py:262-335 for weights (router_activation None) or
@@ -376,12 +399,7 @@ def _dispatch(x, a, basis, cache, output_final_state, activation, router_activat
             if T == 1:
                 y = _step(x, a, basis, cache, activation, router_activation)
                 return y, (cache if output_final_state else None)
-            # Prefill continuing from a cache: the cached tokens are prepended as
-            # history; their own outputs are computed and dropped.
-            hist = cache.transpose(1, 2)
-            a_hist = a.new_zeros(B, KS, K)
-            y = _apply(torch.cat((hist, x), 1), torch.cat((a_hist, a), 1), basis, activation,
-                       router_activation)[:, KS:]
+            y = _prefill(x, a, basis, cache, activation, router_activation)
         else:
             y = _apply(x, a, basis, activation, router_activation)
         return y, (_final_state(x, cache, KS) if output_final_state else None)

@@ -373,3 +373,60 @@ def test_routed_function_dlogits(route, dtype):
     assert_close("dx", xx.grad, rx.grad, dtype)
     assert_close("dlogits", ll.grad, rl.grad, dtype)
     assert_close("dbasis", bb.grad, rb.grad, dtype)
+
+
+@pytest.mark.parametrize("T2,S", [(10, 4), (2, 4), (3, 4), (7, 2), (5, 8), (40, 3), (4, 8)])
+def test_prefill_matches_concatenated_history(T2, S):
+    """Prefill from a cache against the reference's formulation of it
+    (moc/api.py:299-307: the cache prepended to x, zero weights prepended to
+    alpha, the first S outputs dropped) on the same kernels: y bit for bit
+    (each token's output depends only on its own window); dx, dalpha, dbasis
+    and dcache within the bf16 rule (partial sums are rounded separately)."""
+    Bn, Dn, Kn, dtype = 3, 192, 16, torch.bfloat16
+    g = gen(T2 * 10 + S)
+    x = randn(g, Bn, T2, Dn).to(DEV, dtype)
+    a = torch.softmax(randn(g, Bn, T2, Kn), -1).to(DEV, dtype)
+    b = randn(g, Kn, S, Dn, scale=0.1).to(DEV, dtype)
+    c = randn(g, Bn, Dn, S).to(DEV, dtype)
+    dy = randn(g, Bn, T2, Dn, scale=0.1).to(DEV, dtype)
+
+    def run(native):
+        xi, ai, bi, ci = (t.clone().requires_grad_() for t in (x, a, b, c))
+        if native:
+            y, st = moc_triton(xi, ai, bi, cache=ci, output_final_state=True, activation="silu")
+        else:
+            hist = ci.transpose(1, 2)
+            y, _ = moc_triton(torch.cat((hist, xi), 1),
+                              torch.cat((ai.new_zeros(Bn, S, Kn), ai), 1), bi, activation="silu")
+            y = y[:, S:]
+            st = None
+        y.backward(dy)
+        return y.detach(), xi.grad, ai.grad, bi.grad, ci.grad, st
+
+    got, ref = run(True), run(False)
+    assert torch.equal(got[0], ref[0])
+    for name, u, v in zip(("dx", "dalpha", "dbasis", "dcache"), got[1:5], ref[1:5]):
+        assert_close(name, u, v.float(), dtype)
+    full = torch.cat((c.transpose(1, 2), x), 1)
+    assert torch.equal(got[5], O.final_state(full, None, S))
+
+
+def test_module_prefill_from_cache_matches_full_forward():
+    """MoC.forward continuing from a cache (router logits path): the second
+    chunk's y within tolerance of the full-sequence forward, final cache bit-exact."""
+    torch.manual_seed(0)
+    Z = 64
+    m = MoC(D, Z, 4, K, activation="silu", init_std=0.1)
+    g = gen(13)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.1))
+    m = m.to(DEV, torch.bfloat16)
+    x = randn(g, B, T, D).to(DEV, torch.bfloat16)
+    z = randn(g, B, T, Z).to(DEV, torch.bfloat16)
+    t1 = T // 3
+    with torch.no_grad():
+        y_full, st_full = m(x, z, output_final_state=True)
+        _, cache = m(x[:, :t1], z[:, :t1], output_final_state=True)
+        y2, st2 = m(x[:, t1:], z[:, t1:], cache=cache, output_final_state=True)
+    assert_close("prefill y", y2, y_full[:, t1:].float(), torch.bfloat16)
+    assert torch.equal(st2, st_full)
