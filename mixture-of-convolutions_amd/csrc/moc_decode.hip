@@ -250,8 +250,12 @@ __global__ void __launch_bounds__(256) decode_kernel(
 #pragma unroll
     for (int c = 0; c < kNC; ++c) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KC == 2) {
+        acc = C::mma2(aop[0], aop[1], bop[s][c][0], bop[s][c][1], acc);
+      } else {
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) acc = C::mma(aop[kc], bop[s][c][kc], acc);
+        for (int kc = 0; kc < KC; ++kc) acc = C::mma(aop[kc], bop[s][c][kc], acc);
+      }
       w[s][c] = acc;
     }
 #pragma unroll

@@ -46,6 +46,16 @@ struct CT<true> {
   static __device__ __forceinline__ f32x4 mma(opnd a, opnd b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
+  // two route chunks in one v_mfma_f32_16x16x32_bf16: lane entries a0 ++ a1
+  // against b0 ++ b1 (A and B list their entries in the same order)
+  static __device__ __forceinline__ f32x4 mma2(opnd a0, opnd a1, opnd b0, opnd b1, f32x4 c) {
+    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
+    const s16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
   static __device__ __forceinline__ float to_f(elem e) { return bf16_to_f32(e); }
   static __device__ __forceinline__ elem from_f(float v) { return f32_to_bf16(v); }
   static __device__ __forceinline__ opnd make(elem a, elem b, elem c, elem d) {
@@ -314,8 +324,12 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
             f32x4 w = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (BF && KC == 2) {
+              w = C::mma2(aop[b][0], aop[b][1], bop[c][s][0], bop[c][s][1], w);
+            } else {
 #pragma unroll
-            for (int kc = 0; kc < KC; ++kc) w = C::mma(aop[b][kc], bop[c][s][kc], w);
+              for (int kc = 0; kc < KC; ++kc) w = C::mma(aop[b][kc], bop[c][s][kc], w);
+            }
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int r = 4 * b + v;
@@ -676,8 +690,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         auto issue = [&](int jb) {
           const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (BF && KC == 2) {
+            w4 = C::mma2(aop(0, b, 0), aop(0, b, 1), bop[c][s][0], bop[c][s][1], w4);
+          } else {
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
+            for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
+          }
           wq[jb] = w4;
         };
 #pragma unroll
@@ -722,8 +740,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         auto issue = [&](int jb) {
           const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (BF && KC == 2) {
+            w4 = C::mma2(aop(S - 1 - s, b, 0), aop(S - 1 - s, b, 1), bop[c][s][0], bop[c][s][1], w4);
+          } else {
 #pragma unroll
-          for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(S - 1 - s, b, kc), bop[c][s][kc], w4);
+            for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(S - 1 - s, b, kc), bop[c][s][kc], w4);
+          }
           wq[jb] = w4;
         };
 #pragma unroll
