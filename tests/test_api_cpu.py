@@ -183,3 +183,28 @@ def test_prepare_chunk_indices_closed_form_and_lru():
     for i in range(6):
         ops.prepare_chunk_indices(torch.tensor([0, i + 1]), 16)
     assert len(ops._chunk_index_cache) == ops._CHUNK_CACHE_SIZE
+
+
+def test_group_construction_and_arguments():
+    """MoCGroup: layer checks, input counts, and the layers' own validation on
+    the fallback path (CPU tensors never take the router kernels)."""
+    assert "MoCGroup" in moc.__all__
+    q = moc.MoC(16, 8, 4, 4)
+    k = moc.MoC(8, 8, 4, 4)
+    with pytest.raises(ValueError, match="at least one"):
+        moc.MoCGroup()
+    with pytest.raises(TypeError, match="takes MoC layers"):
+        moc.MoCGroup(q, torch.nn.Linear(2, 2))
+    with pytest.raises(ValueError, match="share z_dim"):
+        moc.MoCGroup(q, moc.MoC(8, 4, 4, 4))
+    grp = moc.MoCGroup(q, k)
+    assert list(grp.parameters()) == list(q.parameters()) + list(k.parameters())
+    z = torch.zeros(1, 3, 8)
+    xs = [torch.zeros(1, 3, 16), torch.zeros(1, 3, 8)]
+    with pytest.raises(ValueError, match="got 1 inputs"):
+        grp(xs[:1], z)
+    with pytest.raises(ValueError, match="got 3 caches"):
+        grp(xs, z, cache=[None] * 3)
+    assert not ops.router_grouped_supported(z, [q.router, k.router])
+    with pytest.raises(ValueError, match="must all be CUDA tensors"):
+        grp(xs, z)
