@@ -17,6 +17,7 @@ inputs already resident in HBM.  Printed as one JSON line:
   cpu_baseline  the CPU oracle on a bounded slice of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
+       python bench.py --config 3|5     (BASELINE configs[2] / configs[4] instead)
 """
 from __future__ import annotations
 
@@ -324,6 +325,81 @@ def cpu_baseline(seconds):
                       f"K={CFG['K']} S={CFG['S']} fp32, {reps} reps in {el:.1f}s"}
 
 
+def bench_config3(dev, steps, warmup):
+    """packed varlen layer fwd+bwd, 32768 tokens in sequences of
+    lengths uniform in [16, 4096] (seeded, cu_seqlens int32), D=4096,
+    z_dim=2048, K=16, S=4, bf16, exp routing, no SiLU, dy ~ N(0, 1)."""
+    import moc
+    g = torch.Generator().manual_seed(0)
+    total, lengths = 32768, []
+    while sum(lengths) < total:
+        lengths.append(int(torch.randint(16, 4097, (1,), generator=g)))
+    lengths[-1] -= sum(lengths) - total
+    cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32).to(dev)
+    D, Z, K, S = 4096, 2048, 16, 4
+    m = moc.MoC(D, Z, S, K, init_std=0.002, router_activation="exp")
+    with torch.no_grad():
+        m.router.copy_(torch.randn(K, Z, generator=g) * 0.02)
+    m = m.to(dev, torch.bfloat16)
+    x = torch.randn(total, D, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    z = torch.randn(total, Z, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    dy = torch.randn(total, D, generator=g).to(dev, torch.bfloat16)
+
+    def step():
+        m.zero_grad(set_to_none=True)
+        x.grad = None
+        z.grad = None
+        y, _ = m(x, z, cu_seqlens=cu, max_seqlen=max(lengths))
+        y.backward(dy)
+
+    ms = time_region(step, steps, warmup)
+    return {"metric": "configs[2] varlen layer fwd+bwd Mtok/s", "value": round(total / (ms * 1e-3) / 1e6, 3),
+            "unit": "Mtok/s", "ms_per_step": round(ms, 4), "n_seqs": len(lengths),
+            "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[2]", "tokens": total, "D": D,
+                       "z_dim": Z, "K": K, "S": S, "routing": "exp", "activation": None}}
+
+
+def bench_config5(dev, steps, warmup):
+    """the QKV triple, three MoC layers (q 4096, k 1024, v 1024
+    channels) on one routing input x_norm [2, 8192, 4096], K=32, S=8, bf16, exp
+    routing for q and k, softmax for v, no SiLU, fan-in init, loss = sum of the
+    three y.sum(); the layers called one by one and as one MoCGroup."""
+    import moc
+    g = torch.Generator().manual_seed(0)
+    torch.manual_seed(0)
+    B, T, Dm = 2, 8192, 4096
+    layers = []
+    for dim, route in ((4096, "exp"), (1024, "exp"), (1024, "softmax")):
+        m = moc.MoC(dim, Dm, 8, 32, router_activation=route)
+        with torch.no_grad():
+            m.router.copy_(torch.randn(32, Dm, generator=g) * 0.02)
+        layers.append(m.to(dev, torch.bfloat16))
+    xn = torch.randn(B, T, Dm, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    vs = [torch.randn(B, T, m.dim, generator=g).to(dev, torch.bfloat16).requires_grad_()
+          for m in layers]
+    grp = moc.MoCGroup(*layers)
+
+    def step(grouped):
+        def run():
+            for m in layers:
+                m.zero_grad(set_to_none=True)
+            for v in vs:
+                v.grad = None
+            xn.grad = None
+            outs = grp(vs, xn) if grouped else [m(v, xn) for m, v in zip(layers, vs)]
+            sum(y.sum() for y, _ in outs).backward()
+        return run
+
+    ms_sep = time_region(step(False), steps, warmup)
+    ms_grp = time_region(step(True), steps, warmup)
+    return {"metric": "configs[4] QKV triple fwd+bwd Mtok/s (MoCGroup)",
+            "value": round(B * T / (ms_grp * 1e-3) / 1e6, 3), "unit": "Mtok/s",
+            "ms_per_step": round(ms_grp, 4), "ms_per_step_separate_layers": round(ms_sep, 4),
+            "config": {"workload": "QKV triple, BASELINE configs[4]", "B": B, "T": T, "d_model": Dm,
+                       "dims": [4096, 1024, 1024], "K": 32, "S": 8,
+                       "routing": ["exp", "exp", "softmax"], "activation": None}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -332,6 +408,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
+                    help="2: the headline line (default); 3 / 5: one JSON line for BASELINE "
+                         "configs[2] (varlen) / configs[4] (QKV triple) instead")
     ap.add_argument("--counters", choices=("fwd", "bwd", "copy"), default=None,
                     help="only run 3 calls of one entry (or the calibration copy) "
                          "for a rocprofv3 --pmc pass; prints no JSON")
@@ -346,6 +425,12 @@ def main():
     dev = torch.device("cuda:0")
     if args.counters:
         counter_run(dev, args.counters)
+        return
+    if args.config != 2:
+        fn = bench_config3 if args.config == 3 else bench_config5
+        out = fn(dev, min(args.steps, 20), min(args.warmup, 5))
+        out.update({"n_gpus": 1, "dtype": "bf16", "data": "synthetic (seeded)"})
+        print(json.dumps(out), flush=True)
         return
     N = CFG["B"] * CFG["T"]
     D, K, S = CFG["D"], CFG["K"], CFG["S"]
