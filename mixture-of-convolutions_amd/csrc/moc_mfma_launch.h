@@ -33,12 +33,18 @@ struct Grid2 {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Forward: about kFwdTargetWG workgroups, each wave walking at most
+// kFwdMaxSb super-blocks; larger problems get more workgroups rather than
+// longer ones (measured: D 4096, 32768 tokens, 161 -> 141 us).
+constexpr int64_t kFwdMaxSb = 4;
+
 inline Grid2 fwd_grid(int64_t N, int64_t D) {
   const int64_t gx = cdiv(D, 4 * 16 * kFwdNC);
   const int64_t n_super = cdiv(N, 16 * kFwdNB);
   int64_t gy_target = kFwdTargetWG / gx;
   if (gy_target < 1) gy_target = 1;
-  const int64_t n_sb = cdiv(n_super, gy_target);
+  int64_t n_sb = cdiv(n_super, gy_target);
+  if (n_sb > kFwdMaxSb) n_sb = kFwdMaxSb;
   return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
                static_cast<int>(n_sb)};
 }
