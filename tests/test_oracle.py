@@ -4,14 +4,17 @@ Each oracle function is checked against something it does not share code or
 formula with: explicit fp64 loops, torch's conv1d (one-hot routing reduces MoC
 to a depthwise causal convolution), closed forms (S=1, impulse inputs),
 linearity, finite differences (gradcheck), the adjoint identity, a fixed-length
-batch packed as varlen, and decode / prefill round trips.  The last test plants
+batch packed as varlen, and decode / prefill round trips.  One test plants
 plausible mistakes in copies of the oracle and checks that these pins catch
-every one of them.
+every one of them; the last one checks the oracle against the committed golden
+vectors (tests/golden/), which the GPU parity tests also use.
 """
 from __future__ import annotations
 
 import itertools
+from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -301,3 +304,40 @@ def test_grid_of_shapes_matches_loops():
         a = _rand(1, T, K, seed=S * 11 + K)
         b = _rand(K, S, 3, seed=S * 13 + K)
         torch.testing.assert_close(O.moc_ref(x, a, b), _loops(x, a, b), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures (tests/golden/make_golden.py)
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "moc_golden.npz"
+
+
+def golden_cases():
+    """(name, S, activation, arrays) of every case in the golden file."""
+    data = np.load(GOLDEN)  # allow_pickle is False by default
+    out = []
+    for name in sorted({k.split("/")[0] for k in data.files}):
+        S = int(name.split("_S")[1].split("_")[0])
+        act = None if name.endswith("_none") else "silu"
+        arrays = {k.split("/")[1]: data[k] for k in data.files if k.startswith(name + "/")}
+        out.append((name, S, act, arrays))
+    return out
+
+
+def test_oracle_reproduces_golden():
+    """The oracle, run again in fp64 on the stored inputs, reproduces the stored
+    outputs (fp32 rounding of the fp64 values)."""
+    cases = golden_cases()
+    assert len(cases) == 8
+    for name, S, act, a in cases:
+        t = {k: torch.from_numpy(v).double() for k, v in a.items() if k != "cu_seqlens"}
+        assert t["basis"].shape[1] == S
+        if "cu_seqlens" in a:
+            cu = torch.from_numpy(a["cu_seqlens"]).long()
+            got = O.moc_varlen_grads_ref(t["x"], t["alpha"], t["basis"], cu, t["dy"], act)
+        else:
+            got = O.moc_grads_ref(t["x"], t["alpha"], t["basis"], t["dy"], act)
+        for key, g in zip(("y", "dx", "dalpha", "dbasis"), got):
+            ref = t[key]
+            tol = 1e-6 * ref.abs().max().item() + 1e-12
+            assert (g - ref).abs().max().item() <= tol, (name, key)
