@@ -45,6 +45,8 @@ inline Grid2 fwd_grid(int64_t N, int64_t D) {
   if (gy_target < 1) gy_target = 1;
   int64_t n_sb = cdiv(n_super, gy_target);
   if (n_sb > kFwdMaxSb) n_sb = kFwdMaxSb;
+  // grid.y stays within the 65535 launch limit: longer ranges instead
+  if (cdiv(n_super, n_sb) > 65535) n_sb = cdiv(n_super, 65535);
   return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
                static_cast<int>(n_sb)};
 }

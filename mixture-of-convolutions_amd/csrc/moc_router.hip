@@ -634,9 +634,10 @@ BwdPlan bwd_plan(int64_t N, int64_t Z) {
 }  // namespace router
 
 bool router_supported(int64_t N, int64_t Z, int64_t K, int dt) {
-  // buffer resources address [N, Z] bf16 with 32-bit byte offsets
+  // buffer resources address [N, Z] bf16 with 32-bit byte offsets; the dz grid
+  // (N / 64 token blocks at most) stays within the 65535 limit of grid.y
   return dt == DT_BF16 && K > 0 && K <= kRouterMaxK && K % 4 == 0 && Z >= 64 && Z % 64 == 0 &&
-         N > 0 && N * Z * 2 < (int64_t(1) << 31);
+         N > 0 && N * Z * 2 < (int64_t(1) << 31) && N <= int64_t(65535) * 64;
 }
 
 size_t router_backward_workspace(int64_t N, int64_t Z, int64_t K) {
