@@ -159,8 +159,9 @@ int moc_decode_step(const void* z, const void* router, const void* x, const void
 /*
  * Router of the MoC layer: logits = z . router^T, the F.linear(z, router) of
  * MoC.forward (moc/api.py:383-388) that the reference runs as a library GEMM,
- * and its backward.  bf16 only; k % 4 == 0, k <= 96, z_dim % 64 == 0 and
- * n_tokens * z_dim * 2 < 2^31 (moc_router_supported returns 1 for such shapes).
+ * and its backward.  bf16 only; k % 4 == 0, k <= 96, z_dim % 64 == 0,
+ * n_tokens * z_dim * 2 < 2^31 and n_tokens <= 65535 * 64 (moc_router_supported
+ * returns 1 for such shapes).
  *   z      : [n_tokens, z_dim] contiguous
  *   router : [k, z_dim] contiguous
  *   logits : [n_tokens, k] (output of the forward)
