@@ -256,8 +256,11 @@ void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void
 
 bool supported(const Problem& p) {
   const bool s_ok = p.S == 2 || p.S == 3 || p.S == 4 || p.S == 8;
-  return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 &&
-         (p.x_dt == DT_BF16 || p.x_dt == DT_F32);
+  // the grids' y dimensions stay within the 65535 launch limit and one
+  // super-block's rows within a buffer's 32-bit range
+  return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
+         (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
+         bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D).gy <= 65535;
 }
 
 size_t forward_workspace(const Problem& p) { return plan(p, false).total; }

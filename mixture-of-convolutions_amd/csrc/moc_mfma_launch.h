@@ -57,7 +57,11 @@ inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S) {
   const int64_t n_super = cdiv(N, eown);
   int64_t gy_target = kBwdTargetWG / gx;
   if (gy_target < 1) gy_target = 1;
-  const int64_t n_sb = cdiv(n_super, gy_target);
+  int64_t n_sb = cdiv(n_super, gy_target);
+  // a workgroup's x / dy buffers span its token range: keep them under 2^30
+  // bytes (4-byte elements assumed), i.e. more, shorter ranges for long inputs
+  const int64_t max_sb = ((int64_t(1) << 30) / (D * 4) - 16 * kBwdNB) / eown;
+  if (n_sb > max_sb) n_sb = max_sb > 1 ? max_sb : 1;
   return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
                static_cast<int>(n_sb)};
 }
