@@ -470,18 +470,27 @@ __device__ __forceinline__ void wave_lds_sync() {
 // double buffered; x / dy rows of the next super-block are loaded before the
 // current one is computed.
 // Outputs: dx (own rows), part_da[blockIdx.x][t][KP], part_db[blockIdx.y][KP][S][D].
+//
+// MODE selects the work: kBwdFused does all of the above; kBwdDx only dx;
+// kBwdTaps only the m products (dalpha / dbasis) of the taps
+// [blockIdx.z * S/2, (blockIdx.z + 1) * S/2), writing dalpha partial
+// 2 blockIdx.x + blockIdx.z.  The two partial modes (no activation) keep the
+// working set of 8 taps x 32 routes within two waves per SIMD: the fused pass
+// needs the W operands of every tap beside the dbasis accumulators.
+constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 // Minimum waves per SIMD the backward is compiled for (register budget 512 / n).
-// Two, except for 8 taps with 32 routes: there the working set exceeds 256
-// registers, and one wave per SIMD (spills to AGPRs instead of scratch
-// memory) measured 9% faster than two with scratch spills.
+// Two, except for the fused pass with 8 taps and 32 routes: there the working
+// set exceeds 256 registers, and one wave per SIMD (spills to AGPRs instead of
+// scratch memory) measured 9% faster than two with scratch spills.
 #ifndef MOC_BWD_MIN_WAVES
 #define MOC_BWD_MIN_WAVES 2
 #endif
-template <int S, int KC>
-constexpr int kBwdMinWaves = (S >= 8 && KC >= 2) ? 1 : MOC_BWD_MIN_WAVES;
+template <int S, int KC, int MODE>
+constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2) ? 1 : MOC_BWD_MIN_WAVES;
 
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT>
-__global__ void __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC>)))
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE>)))
 bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
@@ -497,29 +506,51 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   // SPLIT the single chunk kc0 = blockIdx.z (W still uses every route)
   constexpr int KX = SPLIT ? 1 : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
-  const int kc0 = SPLIT ? static_cast<int>(blockIdx.z) : 0;
+  // grid.z: route chunk (SPLIT), tap half (kBwdTaps) above it
+  const int kc0 = SPLIT ? static_cast<int>(blockIdx.z) % KC : 0;
   constexpr int EOWN = TB - (S - 1);
   constexpr int NP = MS::kParts;
   constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
   constexpr int MROW = CW + 4;        // padded LDS row of one m tile (elements)
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
+  // work of this MODE: dx rows, m products of ST taps from tap s0
+  constexpr bool DO_DX = MODE != kBwdTaps, DO_M = MODE != kBwdDx;
+  static_assert(MODE == kBwdFused || (BF && !ACT && S % 2 == 0),
+                "the partial passes are built for bf16 without activation");
+  static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
+  constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
+  const int th = MODE == kBwdTaps ? static_cast<int>(blockIdx.z) / (SPLIT ? KC : 1) : 0;
+  const int s0 = th * ST;
+  constexpr int ZDA = MODE == kBwdTaps ? 2 : 1;  // dalpha partials per workgroup column
+  const int zda = th;
+  // x window rows: every tap (P, or the fused m products), ST taps from s0, none
+  constexpr bool NEED_X = DO_M || ACT;
+  constexpr int WX = MODE == kBwdTaps ? R + ST - 1 : (NEED_X ? W : 1);
 
   // m tiles for the dalpha product.  fp32: [token][channel] tiles read as rows.
   // bf16: the dbasis operand of a (token group of 4, channel) is stored as is
   // (8 bytes) and read back transposed with ds_read_b64_tr_b16 (see TrTile).
   using TT = TrTile<NB, NC>;
-  // routing-weight rows padded by 4 bf16 (40-byte rows) so that the W operand
-  // reads of the 16 lanes of a group spread over the banks
-  constexpr int AP = BF ? KP + 4 : KP;
+  // routing-weight rows, unpadded.  bf16: the 8-byte chunk (4 routes) c of row r
+  // is stored at chunk c ^ asw(r), so that the W operand reads of a 16-lane group
+  // (one chunk of rows 8 (j/4) + j%4 + const) fall on 32 distinct banks; the
+  // transposed reads and the staging writes stay conflict-free as well
+  constexpr int AP = KP;
   __shared__ __align__(16) E a_lds[2][AROWS][AP];
+  auto acol = [](int r, int col) -> int {
+    if constexpr (!BF) return col;
+    const int sw = KP == 16 ? ((r >> 3) & 3) : (((r >> 1) & 1) | (((r >> 3) & 3) << 1));
+    return (col & 3) | (((col >> 2) ^ sw) << 2);
+  };
   __shared__ __align__(16) E m_lds[BF ? 1 : WPG][NP][BF ? 1 : TB][BF ? 1 : MROW];
-  __shared__ __align__(16) s16x4 m_tr[BF ? WPG : 1][NP][BF ? TT::kSlots : 1];
+  __shared__ __align__(16) s16x4 m_tr[BF && DO_M ? WPG : 1][NP][BF && DO_M ? TT::kSlots : 1];
   // dalpha B operands of each wave's channels (bf16, one 16-route chunk): rows
-  // (k, s), CW channels; with more routes they stay in registers
-  constexpr bool kBdaLds = BF && KX == 1;
+  // (s, k), CW channels (with rows (k, s) the reads of a 16-lane group, rows k
+  // = j at one s, hit each bank twice); with more routes they stay in registers
+  constexpr bool kBdaLds = BF && KX == 1 && DO_M;
   constexpr int BROW = CW + 4;
-  __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? 16 * KX * S : 1][kBdaLds ? BROW : 1];
-  __shared__ float da_lds[2][WPG][NB][KX][16][17];
+  __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? 16 * KX * ST : 1][kBdaLds ? BROW : 1];
+  __shared__ float da_lds[DO_M ? 2 : 1][DO_M ? WPG : 1][NB][KX][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
   const E* __restrict__ dy = static_cast<const E*>(dyv);
@@ -548,8 +579,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
 
-  // W operands: bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
+  // W operands (P, dx): bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
   Op bop[NC][S][KC];
+  if constexpr (DO_DX || ACT)
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -564,32 +596,33 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       for (int c = 0; c < NC; ++c) bop[c][s][kc] = C::make(rows[0][c], rows[1][c], rows[2][c], rows[3][c]);
     }
   }
-  // dalpha B operands: bda[s][cg][kx] = basis[16 (kc0 + kx) + j, s, d0 + 16cg + 4q + v]
-  Op bda[S][NC][KX];
+  // dalpha B operands: bda[s][cg][kx] = basis[16 (kc0 + kx) + j, s0 + s, d0 + 16cg + 4q + v]
+  Op bda[ST][NC][KX];
+  if constexpr (DO_M)
 #pragma unroll
   for (int kx = 0; kx < KX; ++kx) {
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
+    for (int s = 0; s < ST; ++s) {
 #pragma unroll
       for (int cg = 0; cg < NC; ++cg) {
         const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
-        bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ),
-                                 wave_on && ch < D),
+        bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s0 + s, 0, rb,
+                                 static_cast<uint32_t>(ch * ESZ), wave_on && ch < D),
                          e4);
         if constexpr (kBdaLds)  // read back per tap in the dalpha loop (wave-private rows)
-          Vec<E, 4>::store(&b_lds[wave][(16 * kx + j) * S + s][16 * cg + 4 * q], e4);
+          Vec<E, 4>::store(&b_lds[wave][s * 16 * KX + 16 * kx + j][16 * cg + 4 * q], e4);
         else
           bda[s][cg][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
       }
     }
   }
 
-  f32x4 dbacc[NC][S][KX];
+  f32x4 dbacc[NC][ST][KX];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+    for (int s = 0; s < ST; ++s)
 #pragma unroll
       for (int kx = 0; kx < KX; ++kx) dbacc[c][s][kx] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -598,15 +631,17 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   constexpr int AVEC = 4;                                  // elements per alpha load
   constexpr int ACHUNKS = AROWS * KP / AVEC;
   constexpr int APER = (ACHUNKS + 64 * WPG - 1) / (64 * WPG);
-  E xr[W][NC];
+  E xr[WX][NC];
   E dr[R][NC];
   E arw[APER][AVEC];
   auto fetch = [&](int64_t t0) {
     // offset of window row w = base + w rb: rows before row_lo wrap to >= 2^31
-    // and load zeros; a lane past the channel axis starts at kOffNone
+    // and load zeros; a lane past the channel axis starts at kOffNone.  The x
+    // window of the taps from s0 starts s0 rows into the full one.
     const uint32_t base = row_off(t0 + R * q - (S - 1), row_lo, rb, col, ch_ok);
+    if constexpr (NEED_X)
 #pragma unroll
-    for (int w = 0; w < W; ++w) xb.load<NC * ESZ>(base + w * rb, xr[w]);
+      for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
 #pragma unroll
     for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(base + (r + S - 1) * rb, dr[r]);
 #pragma unroll
@@ -622,8 +657,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
     for (int i = 0; i < APER; ++i) {
       const int chunk = tid + i * 64 * WPG;
+      const int row = chunk / (KP / AVEC);
       if (chunk < ACHUNKS)
-        Vec<E, AVEC>::store(&a_lds[buf][chunk / (KP / AVEC)][(chunk % (KP / AVEC)) * AVEC], arw[i]);
+        Vec<E, AVEC>::store(&a_lds[buf][row][acol(row, (chunk % (KP / AVEC)) * AVEC)], arw[i]);
     }
   };
 
@@ -641,12 +677,13 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     const int64_t own_end = (t0 + EOWN < N) ? t0 + EOWN : N;
     const int64_t trun = t0 + R * q;
 
-    float xw[W][NC];
+    float xw[WX][NC];
     float g[R][NC];
+    if constexpr (NEED_X)
 #pragma unroll
-    for (int w = 0; w < W; ++w)
+      for (int w = 0; w < WX; ++w)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
+        for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -656,8 +693,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 
     // alpha operand of token-row block b shifted by e rows (row i = j)
     auto aop = [&](int e, int b, int kc) -> Op {
-      return *reinterpret_cast<const Op*>(
-          &a_lds[buf][R * (j >> 2) + 4 * b + (j & 3) + e][16 * kc + 4 * q]);
+      const int r = R * (j >> 2) + 4 * b + (j & 3) + e;
+      return *reinterpret_cast<const Op*>(&a_lds[buf][r][acol(r, 16 * kc + 4 * q)]);
     };
 
     // uniform: does a sequence start fall where it masks a tap of the rows
@@ -674,12 +711,14 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     auto body = [&](auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
       // ok[r]: tap bits of row r of this lane's run extended by S-1 later rows
-      uint32_t ok[R + S - 1];
+      // (the later rows only for dx)
+      constexpr int NOK = DO_DX ? R + S - 1 : R;
+      uint32_t ok[NOK];
       if (MASK) {
-        tap_bits_rows<S, R + S - 1>(seq, trun, w_lo, w_hi, ok);
+        tap_bits_rows<S, NOK>(seq, trun, w_lo, w_hi, ok);
       } else {
 #pragma unroll
-        for (int r = 0; r < R + S - 1; ++r) ok[r] = (1u << S) - 1u;
+        for (int r = 0; r < NOK; ++r) ok[r] = (1u << S) - 1u;
       }
 
       if (ACT) {
@@ -725,16 +764,15 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
           }
       }
 
-      // g of the S-1 rows after this lane's run: first rows of lane group q+1
-      float gf[S - 1][NC];
-      const int src_lane = (lane + 16) & 63;
-#pragma unroll
-      for (int e = 0; e < S - 1; ++e)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) gf[e][c] = __shfl(g[e][c], src_lane, 64);
-
       // dx: taps in ascending order (with SPLIT, by the kc0 = 0 workgroups only)
-      if (dx != nullptr && kc0 == 0) {
+      if (DO_DX && dx != nullptr && kc0 == 0) {
+        // g of the S-1 rows after this lane's run: first rows of lane group q+1
+        float gf[S - 1][NC];
+        const int src_lane = (lane + 16) & 63;
+#pragma unroll
+        for (int e = 0; e < S - 1; ++e)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) gf[e][c] = __shfl(g[e][c], src_lane, 64);
         float dxa[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -785,208 +823,210 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         }
       }
 
-      // alpha^T operands of the dbasis MFMA (zero for rows that are not this
-      // super-block's own): at[b][kx][v] = alpha[trun + 4b + v, 16 (kc0 + kx) + j]
-      Op at[NB][KX];
-      if constexpr (BF) {
-        // transposed read: supplier lane 4e + a of each 16-lane group holds the
-        // 4 routing weights 16kc + 4a.. of row R q + 4b + e (ds_read_b64_tr_b16)
-        const int own_rows = static_cast<int>(own_end - t0);
+      if constexpr (DO_M) {
+        // alpha^T operands of the dbasis MFMA (zero for rows that are not this
+        // super-block's own): at[b][kx][v] = alpha[trun + 4b + v, 16 (kc0 + kx) + j]
+        Op at[NB][KX];
+        if constexpr (BF) {
+          // transposed read: supplier lane 4e + a of each 16-lane group holds the
+          // 4 routing weights 16kc + 4a.. of row R q + 4b + e (ds_read_b64_tr_b16)
+          const int own_rows = static_cast<int>(own_end - t0);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
-          const uint64_t keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
+          for (int b = 0; b < NB; ++b) {
+            const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
+            const uint64_t keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
 #pragma unroll
-          for (int kx = 0; kx < KX; ++kx) {
-            const Op v = TT::read(&a_lds[buf][R * q + 4 * b + (j >> 2)][16 * (kc0 + kx) + 4 * (j & 3)]);
-            at[b][kx] = __builtin_bit_cast(Op, __builtin_bit_cast(uint64_t, v) & keep);
+            for (int kx = 0; kx < KX; ++kx) {
+              const int r = R * q + 4 * b + (j >> 2);
+              const Op v = TT::read(&a_lds[buf][r][acol(r, 16 * (kc0 + kx) + 4 * (j & 3))]);
+              at[b][kx] = __builtin_bit_cast(Op, __builtin_bit_cast(uint64_t, v) & keep);
+            }
           }
+        } else {
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int kx = 0; kx < KX; ++kx) {
+              E e4[4];
+#pragma unroll
+              for (int v = 0; v < 4; ++v) {
+                const int row = R * q + 4 * b + v;
+                e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * (kc0 + kx) + j] : E(0);
+              }
+              at[b][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
+            }
         }
-      } else {
+        // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
+        if constexpr (BF) {
+          // both products contract 32 entries per v_mfma_f32_16x16x32_bf16: dbasis
+          // the 8 rows of this lane's run (token blocks b, b+1), dalpha the 32
+          // channels of the wave (channel groups 0, 1); A and B operands list
+          // their entries in the same order
+          static_assert(NB % 2 == 0 && NC == 2, "16x16x32 pairing");
+          // tap s: m_s -> bf16 hi / lo operands -> the wave's LDS tile and the
+          // dbasis MFMAs; the dalpha reads of tap s are issued before the m values
+          // of tap s + 1 are computed and written, so that VALU work covers the
+          // LDS latency (one tile suffices: a wave's LDS operations complete in
+          // issue order, so the writes of tap s + 1 follow the reads of tap s)
+          auto stage_m = [&](int s) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+            for (int c = 0; c < NC; ++c) {
 #pragma unroll
-          for (int kx = 0; kx < KX; ++kx) {
-            E e4[4];
+              for (int b2 = 0; b2 < NB; b2 += 2) {
+                Op mh[2], ml[2];
+#pragma unroll
+                for (int bb = 0; bb < 2; ++bb) {
+                  const int b = b2 + bb;
+                  // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
+                  uint32_t hb[4];
+                  float lo[4];
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) {
+                    const int r = 4 * b + v;
+                    const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
+                    const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                    hb[v] = __float_as_uint(mval) & 0xffff0000u;
+                    lo[v] = mval - __uint_as_float(hb[v]);
+                  }
+                  mh[bb] = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
+                  ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
+                  m_tr[wave][0][TT::wslot(j, q, b, c)] = mh[bb];
+                  m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
+                }
+#pragma unroll
+                for (int kx = 0; kx < KX; ++kx) {
+                  dbacc[c][s][kx] = mma32(mh[0], mh[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
+                  dbacc[c][s][kx] = mma32(ml[0], ml[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
+                }
+              }
+            }
+          };
+          stage_m(0);
+#pragma unroll
+          for (int s = 0; s < ST; ++s) {
+            wave_lds_sync();
+            Op ra[NB][NP][2];
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+              for (int h = 0; h < NP; ++h)
+#pragma unroll
+                for (int cg = 0; cg < 2; ++cg)
+                  ra[rb][h][cg] = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
+            // dalpha B operands of tap s: basis[16 kc + j][s][16 cg + 4 q + {0..3}]
+            Op bs[KX][2];
+#pragma unroll
+            for (int kx = 0; kx < KX; ++kx)
+#pragma unroll
+              for (int cg = 0; cg < 2; ++cg) {
+                if constexpr (kBdaLds)
+                  bs[kx][cg] = *reinterpret_cast<const Op*>(&b_lds[wave][s * 16 * KX + 16 * kx + j][16 * cg + 4 * q]);
+                else
+                  bs[kx][cg] = bda[s][cg][kx];
+              }
+            // keep the reads ahead of the next tap's VALU work
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < ST) stage_m(s + 1);
+            // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+              for (int h = 0; h < NP; ++h)
+#pragma unroll
+                for (int kx = 0; kx < KX; ++kx)
+                  dacc[rb][kx] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kx][0], bs[kx][1], dacc[rb][kx]);
+          }
+          wave_lds_sync();
+        } else {
+#pragma unroll
+        for (int s = 0; s < ST; ++s) {
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            E mv[NP][4][NC];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-              const int row = R * q + 4 * b + v;
-              e4[v] = (t0 + row < own_end) ? a_lds[buf][row][16 * (kc0 + kx) + j] : E(0);
-            }
-            at[b][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
-          }
-      }
-      // per tap: m_s = g * x[t-(S-1-s)] -> dbasis MFMA, wave-private LDS tile -> dalpha MFMA
-      if constexpr (BF) {
-        // both products contract 32 entries per v_mfma_f32_16x16x32_bf16: dbasis
-        // the 8 rows of this lane's run (token blocks b, b+1), dalpha the 32
-        // channels of the wave (channel groups 0, 1); A and B operands list
-        // their entries in the same order
-        static_assert(NB % 2 == 0 && NC == 2, "16x16x32 pairing");
-        // tap s: m_s -> bf16 hi / lo operands -> the wave's LDS tile and the
-        // dbasis MFMAs; the dalpha reads of tap s are issued before the m values
-        // of tap s + 1 are computed and written, so that VALU work covers the
-        // LDS latency (one tile suffices: a wave's LDS operations complete in
-        // issue order, so the writes of tap s + 1 follow the reads of tap s)
-        auto stage_m = [&](int s) {
+              const int r = 4 * b + v;
+              const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
+              for (int c = 0; c < NC; ++c) {
+                E parts[NP];
+                MS::split(on ? g[r][c] * xw[r + s][c] : 0.f, parts);
 #pragma unroll
-            for (int b2 = 0; b2 < NB; b2 += 2) {
-              Op mh[2], ml[2];
-#pragma unroll
-              for (int bb = 0; bb < 2; ++bb) {
-                const int b = b2 + bb;
-                // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
-                uint32_t hb[4];
-                float lo[4];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                  const int r = 4 * b + v;
-                  const bool on = !MASK || ((ok[r] >> s) & 1u);
-                  const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
-                  hb[v] = __float_as_uint(mval) & 0xffff0000u;
-                  lo[v] = mval - __uint_as_float(hb[v]);
-                }
-                mh[bb] = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
-                ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
-                m_tr[wave][0][TT::wslot(j, q, b, c)] = mh[bb];
-                m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
+                for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
               }
 #pragma unroll
-              for (int kx = 0; kx < KX; ++kx) {
-                dbacc[c][s][kx] = mma32(mh[0], mh[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
-                dbacc[c][s][kx] = mma32(ml[0], ml[1], at[b2][kx], at[b2 + 1][kx], dbacc[c][s][kx]);
-              }
+              for (int h = 0; h < NP; ++h) XV::store(&m_lds[wave][h][R * q + r][NC * j], mv[h][v]);
             }
-          }
-        };
-        stage_m(0);
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          wave_lds_sync();
-          Op ra[NB][NP][2];
-#pragma unroll
-          for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
             for (int h = 0; h < NP; ++h)
 #pragma unroll
-              for (int cg = 0; cg < 2; ++cg)
-                ra[rb][h][cg] = TT::read(&m_tr[wave][h][TT::rslot(j, q, rb, cg)]);
-          // dalpha B operands of tap s: basis[16 kc + j][s][16 cg + 4 q + {0..3}]
-          Op bs[KX][2];
+              for (int c = 0; c < NC; ++c) {
+                const Op am = C::make(mv[h][0][c], mv[h][1][c], mv[h][2][c], mv[h][3][c]);
 #pragma unroll
-          for (int kx = 0; kx < KX; ++kx)
-#pragma unroll
-            for (int cg = 0; cg < 2; ++cg) {
-              if constexpr (kBdaLds)
-                bs[kx][cg] = *reinterpret_cast<const Op*>(&b_lds[wave][(16 * kx + j) * S + s][16 * cg + 4 * q]);
-              else
-                bs[kx][cg] = bda[s][cg][kx];
-            }
-          // keep the reads ahead of the next tap's VALU work
-          __builtin_amdgcn_sched_barrier(0);
-          if (s + 1 < S) stage_m(s + 1);
+                for (int kx = 0; kx < KX; ++kx) dbacc[c][s][kx] = C::mma(am, at[b][kx], dbacc[c][s][kx]);
+              }
+          }
+          wave_lds_sync();
           // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
 #pragma unroll
           for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
             for (int h = 0; h < NP; ++h)
 #pragma unroll
-              for (int kx = 0; kx < KX; ++kx)
-                dacc[rb][kx] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kx][0], bs[kx][1], dacc[rb][kx]);
+              for (int cg = 0; cg < NC; ++cg) {
+                const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][h][16 * rb + j][16 * cg + 4 * q]);
+#pragma unroll
+                for (int kx = 0; kx < KX; ++kx) dacc[rb][kx] = C::mma(am, bda[s][cg][kx], dacc[rb][kx]);
+              }
+          wave_lds_sync();
         }
-        wave_lds_sync();
-      } else {
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          E mv[NP][4][NC];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int r = 4 * b + v;
-            const bool on = !MASK || ((ok[r] >> s) & 1u);
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              E parts[NP];
-              MS::split(on ? g[r][c] * xw[r + s][c] : 0.f, parts);
-#pragma unroll
-              for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
-            }
-#pragma unroll
-            for (int h = 0; h < NP; ++h) XV::store(&m_lds[wave][h][R * q + r][NC * j], mv[h][v]);
-          }
-#pragma unroll
-          for (int h = 0; h < NP; ++h)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-              const Op am = C::make(mv[h][0][c], mv[h][1][c], mv[h][2][c], mv[h][3][c]);
-#pragma unroll
-              for (int kx = 0; kx < KX; ++kx) dbacc[c][s][kx] = C::mma(am, at[b][kx], dbacc[c][s][kx]);
-            }
         }
-        wave_lds_sync();
-        // dalpha over this wave's channels for tap s: D[t][k] += sum_ch m[t][ch] basis[k][s][ch]
-#pragma unroll
-        for (int rb = 0; rb < NB; ++rb)
-#pragma unroll
-          for (int h = 0; h < NP; ++h)
-#pragma unroll
-            for (int cg = 0; cg < NC; ++cg) {
-              const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][h][16 * rb + j][16 * cg + 4 * q]);
-#pragma unroll
-              for (int kx = 0; kx < KX; ++kx) dacc[rb][kx] = C::mma(am, bda[s][cg][kx], dacc[rb][kx]);
-            }
-        wave_lds_sync();
-      }
       }
     };
-#ifdef MOC_INSPECT_FAST_PATH_ONLY
-    (void)interior;
-    body(std::false_type{});
-#else
     if (interior) body(std::false_type{});
     else body(std::true_type{});
-#endif
 
+    if constexpr (DO_M) {
 #pragma unroll
-    for (int rb = 0; rb < NB; ++rb)
+      for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
-      for (int kx = 0; kx < KX; ++kx)
+        for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
+          for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
+    }
     if (more) stage_alpha(buf ^ 1);
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
-    for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
-      const int rb = idx / (KX * 256);
-      const int kx = (idx / 256) % KX;
-      const int row = (idx >> 4) & 15, col = idx & 15;
-      float sum = 0.f;
+    if constexpr (DO_M) {
+      const int64_t pda = static_cast<int64_t>(blockIdx.x) * ZDA + zda;
+      for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
+        const int rb = idx / (KX * 256);
+        const int kx = (idx / 256) % KX;
+        const int row = (idx >> 4) & 15, col = idx & 15;
+        float sum = 0.f;
 #pragma unroll
-      for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kx][row][col];
-      const int64_t t = t0 + 16 * rb + row;
-      if (t < own_end)
-        part_da[(static_cast<int64_t>(blockIdx.x) * N + t) * KP + 16 * (kc0 + kx) + col] = sum;
+        for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kx][row][col];
+        const int64_t t = t0 + 16 * rb + row;
+        if (t < own_end) part_da[(pda * N + t) * KP + 16 * (kc0 + kx) + col] = sum;
+      }
     }
   }
 
   // this workgroup's dbasis partial: dbacc[c][s][kx][v] is
-  // (k = 16 (kc0 + kx) + j, s, channel d0 + NC (4q + v) + c)
-  if (wave_on) {
+  // (k = 16 (kc0 + kx) + j, s0 + s, channel d0 + NC (4q + v) + c)
+  if (DO_M && wave_on) {
     const int64_t base = static_cast<int64_t>(blockIdx.y) * KP;
 #pragma unroll
     for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
-      for (int s = 0; s < S; ++s)
+      for (int s = 0; s < ST; ++s)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
             const int64_t ch = d0 + NC * (4 * q + v) + c;
             if (ch < D)
-              part_db[((base + 16 * (kc0 + kx) + j) * S + s) * D + ch] = dbacc[c][s][kx][v];
+              part_db[((base + 16 * (kc0 + kx) + j) * S + s0 + s) * D + ch] = dbacc[c][s][kx][v];
           }
   }
 }

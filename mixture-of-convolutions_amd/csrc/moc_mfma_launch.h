@@ -76,19 +76,44 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
                      g.n_sb);
 }
 
-// With 32 routes (bf16) each workgroup accumulates dbasis / dalpha for one of
-// the two 16-route chunks (grid.z): the accumulators and dalpha operands of
-// both would not fit in registers beside the W operands.
+// The backward in two passes (bwd_kernel modes kBwdDx, then kBwdTaps with the
+// taps split over grid.z) where the fused pass does not fit two waves per SIMD
+// and no activation needs P: bf16, 32 routes, 8 taps.
+constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
+  return bf && !act && KC == 2 && S == 8;
+}
+// dalpha partials per workgroup column of bwd_grid
+inline int bwd_da_halves(const Problem& p) {
+  return bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16), p.activation != 0,
+                      p.x_dt == DT_BF16) ? 2 : 1;
+}
+
+// Fused pass with 32 routes (bf16): each workgroup accumulates dbasis / dalpha
+// for one of the two 16-route chunks (grid.z), as the accumulators and dalpha
+// operands of both would not fit in registers beside the W operands.
 template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
              void* dx, float* part_da, float* part_db, hipStream_t st) {
   using E = typename CT<BF>::elem;
-  constexpr bool kSplit = BF && KC == 2;
   const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
-  hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit>),
-                     dim3(g.gx, g.gy, kSplit ? KC : 1), dim3(64 * kBwdWPG), 0, st, x, dy,
-                     static_cast<const E*>(a_c), static_cast<const E*>(b_c), dx, part_da, part_db,
-                     p.seq, p.D, g.n_sb);
+  const auto* a = static_cast<const E*>(a_c);
+  const auto* b = static_cast<const E*>(b_c);
+  if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
+    if (dx != nullptr)
+      hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
+                         dim3(g.gx, g.gy, 1), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
+                         part_db, p.seq, p.D, g.n_sb);
+    // (splitting the route chunks over grid.z as well forms every m product
+    // twice again: measured slower than the register spills it avoids)
+    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdTaps>),
+                       dim3(g.gx, g.gy, 2), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, nullptr,
+                       part_da, part_db, p.seq, p.D, g.n_sb);
+  } else {
+    constexpr bool kSplit = BF && KC == 2;
+    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
+                       dim3(g.gx, g.gy, kSplit ? KC : 1), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx,
+                       part_da, part_db, p.seq, p.D, g.n_sb);
+  }
 }
 
 // Dispatch over (KC, activation, dtype) for one S.

@@ -159,9 +159,11 @@ def test_config5_qkv_triple():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 32), (8, 32), (8, 5)])
-def test_mfma_matches_generic(dtype, S, K):
-    """Mid-size problems through both kernel families, fixed and packed."""
+@pytest.mark.parametrize("S,K,act", [(2, 8, "silu"), (3, 16, "silu"), (4, 16, "silu"), (4, 32, "silu"),
+                                     (8, 32, "silu"), (8, 32, None), (8, 5, "silu")])
+def test_mfma_matches_generic(dtype, S, K, act):
+    """Mid-size problems through both kernel families, fixed and packed (bf16,
+    8 taps, 32 routes, no activation: the two-pass backward)."""
     g = gen(S * 100 + K)
     D, Bt, T = 192, 3, 333
     x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
@@ -172,15 +174,15 @@ def test_mfma_matches_generic(dtype, S, K):
     def run(**kw):
         xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
         if "cu_seqlens" in kw:
-            y, _ = moc_triton(xx.view(-1, D), aa.view(-1, K), bb, activation="silu", **kw)
+            y, _ = moc_triton(xx.view(-1, D), aa.view(-1, K), bb, activation=act, **kw)
             y.backward(dy.view(-1, D))
         else:
-            y, _ = moc_triton(xx, aa, bb, activation="silu")
+            y, _ = moc_triton(xx, aa, bb, activation=act)
             y.backward(dy)
         return y.detach().reshape(x.shape), xx.grad, aa.grad, bb.grad
 
     rx, ra, rb = O.reference_inputs(x, a, b, dtype)
-    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), "silu")
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), act)
     got = run()
     other = _with_path("generic", run)
     for n, u, v, r in zip(("y", "dx", "dalpha", "dbasis"), got, other, ref):
@@ -191,7 +193,7 @@ def test_mfma_matches_generic(dtype, S, K):
     assert cu[-1] == Bt * T
     gv = run(cu_seqlens=cu, max_seqlen=400)
     refv = O.moc_varlen_grads_ref(rx.detach().view(-1, D), ra.detach().view(-1, K), rb.detach(),
-                                  cu.cpu(), dy.float().cpu().view(-1, D), "silu")
+                                  cu.cpu(), dy.float().cpu().view(-1, D), act)
     for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), gv, refv):
         assert_close("varlen " + n, u.reshape(r.shape), r, dtype)
 
