@@ -41,15 +41,45 @@ struct CacheRow {
     const uint32_t sh = 16 * (e & 1);
     w[e >> 1] = (w[e >> 1] & ~(0xffffu << sh)) | (static_cast<uint32_t>(v) << sh);
   }
+  // whole rows per access (16 or 8 bytes; 4-byte words for 3 slots): a 16-lane
+  // group then moves one contiguous span of rows per instruction
+  static constexpr int kVec = kWords % 4 == 0 ? 4 : (kWords % 2 == 0 ? 2 : 1);
+  static __device__ __forceinline__ int at(uint32_t off, int i) {
+    return static_cast<int>(off == kOffNone ? off : off + 4 * kVec * i);
+  }
   __device__ __forceinline__ void load(const Buf& b, uint32_t off) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int i = 0; i < kWords; ++i)
-      w[i] = __builtin_amdgcn_raw_buffer_load_b32(b.r, static_cast<int>(off == kOffNone ? off : off + 4 * i), 0, 0);
+    for (int i = 0; i < kWords / kVec; ++i) {
+      if constexpr (kVec == 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(b.r, at(off, i), 0, 0);
+        __builtin_memcpy(&w[4 * i], &v, 16);
+      } else if constexpr (kVec == 2) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(b.r, at(off, i), 0, 0);
+        __builtin_memcpy(&w[2 * i], &v, 8);
+      } else {
+        w[i] = __builtin_amdgcn_raw_buffer_load_b32(b.r, at(off, i), 0, 0);
+      }
+    }
   }
   __device__ __forceinline__ void store(const Buf& b, uint32_t off) const {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int i = 0; i < kWords; ++i)
-      __builtin_amdgcn_raw_buffer_store_b32(w[i], b.r, static_cast<int>(off == kOffNone ? off : off + 4 * i), 0, 0);
+    for (int i = 0; i < kWords / kVec; ++i) {
+      if constexpr (kVec == 4) {
+        u32x4 v;
+        __builtin_memcpy(&v, &w[4 * i], 16);
+        __builtin_amdgcn_raw_buffer_store_b128(v, b.r, at(off, i), 0, 0);
+      } else if constexpr (kVec == 2) {
+        u32x2 v;
+        __builtin_memcpy(&v, &w[2 * i], 8);
+        __builtin_amdgcn_raw_buffer_store_b64(v, b.r, at(off, i), 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b32(w[i], b.r, at(off, i), 0, 0);
+      }
+    }
   }
 };
 
