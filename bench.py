@@ -219,28 +219,30 @@ def bench_decode(dev):
         zp = torch.randn(c["B"], c["prompt"], c["Z"], generator=g).to(dev, torch.bfloat16)
         _, cache = m(xp, zp, output_final_state=True)
         del xp, zp
-        xs = torch.randn(c["B"], c["steps"], c["D"], generator=g).to(dev, torch.bfloat16)
-        zs = torch.randn(c["B"], c["steps"], c["Z"], generator=g).to(dev, torch.bfloat16)
+        # step t's inputs as a decode loop holds them: the current token's
+        # activations, each a contiguous [B, 1, D] / [B, 1, Z] tensor
+        xs = torch.randn(c["steps"], c["B"], 1, c["D"], generator=g).to(dev, torch.bfloat16)
+        zs = torch.randn(c["steps"], c["B"], 1, c["Z"], generator=g).to(dev, torch.bfloat16)
         for t in range(8):  # warm-up on a scratch copy
-            m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache.clone())
+            m.step(xs[t], zs[t], cache=cache.clone())
         torch.cuda.synchronize()
         per_step = []
         for t in range(c["steps"]):
             t0 = time.perf_counter()
-            y, _ = m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache, output_final_state=True)
+            y, _ = m.step(xs[t], zs[t], cache=cache, output_final_state=True)
             torch.cuda.synchronize()
             per_step.append((time.perf_counter() - t0) * 1e6)
         # back to back, one synchronisation at the end: what a decode loop sees
         # when it does not wait for each token on the host
         t0 = time.perf_counter()
         for t in range(c["steps"]):
-            m.step(xs[:, t:t + 1], zs[:, t:t + 1], cache=cache)
+            m.step(xs[t], zs[t], cache=cache)
         torch.cuda.synchronize()
         async_us = (time.perf_counter() - t0) * 1e6 / c["steps"]
         # MoC.step itself captured in a HIP graph (static x / z buffers, cache
         # updated in place): 32 module steps per graph launch
-        xin = xs[:, :1].clone()
-        zin = zs[:, :1].clone()
+        xin = xs[0].clone()
+        zin = zs[0].clone()
         gcache = cache.clone()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -256,8 +258,8 @@ def bench_decode(dev):
         module_graph_us = time_region(mgraph.replay, 20, 3) * 1e3 / 32
         # kernel-only: 32 launches of the one-launch decode step that MoC.step
         # runs (router GEMM + softmax + update), captured in one HIP graph
-        xt = xs[:, 0].contiguous()
-        zt = zs[:, 0].contiguous()
+        xt = xs[0, :, 0].contiguous()
+        zt = zs[0, :, 0].contiguous()
         basis = m.conv_bases.detach()
         router = m.router.detach()
         scratch = cache.clone()

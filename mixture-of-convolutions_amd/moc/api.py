@@ -473,13 +473,12 @@ class MoC(nn.Module):
                 and ops.decode_step_supported(x, z, self.router, self.conv_bases, cache)):
             # single-token step: router GEMM, router activation and cache update
             # in one launch (the step is not differentiable, as in the reference)
-            activation_flag(self.activation)
             if cu_seqlens_cpu is not None or chunk_indices is not None:
                 raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
-            y = ops.launch_decode_step(x[:, 0], z[:, 0], self.router, self.conv_bases, cache,
+            y = ops.launch_decode_step(x, z, self.router, self.conv_bases, cache,
                                        activation_flag=activation_flag(self.activation),
                                        routing=_ROUTING_CODES[self.router_activation])
-            return y[:, None], (cache if output_final_state else None)
+            return y, (cache if output_final_state else None)
         if (cache is None and self.router.shape[0] <= ops.ROUTER_MAX_ROUTED_K
                 and ops.router_supported(z, self.router)):
             return self._forward_kernels(x, z, output_final_state, cu_seqlens, max_seqlen,

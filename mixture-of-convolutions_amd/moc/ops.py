@@ -401,19 +401,20 @@ def launch_decode_step(x: torch.Tensor, z: torch.Tensor, router: torch.Tensor,
                        basis: torch.Tensor, cache: torch.Tensor, *, activation_flag: int,
                        routing: int) -> torch.Tensor:
     """One decode step of the MoC layer in one launch: router GEMM, softmax / exp
-    and the cache update (MoC.step, moc/api.py:403-425).  x [B,D], z [B,Z];
-    ``cache`` [B,D,S] contiguous, updated in place; returns y [B,D]."""
+    and the cache update (MoC.step, moc/api.py:403-425).  x [B,D] or [B,1,D],
+    z [B,Z] or [B,1,Z]; ``cache`` [B,D,S] contiguous, updated in place; returns
+    y shaped as x."""
     L = _lib.lib()
     x = x.contiguous()
     z = z.contiguous()
     r = router.contiguous()
     b = basis.contiguous()
-    B, D = x.shape
+    B, D = x.shape[0], x.shape[-1]
     K, S, _ = b.shape
     out = torch.empty_like(x)
     with _lib.device_guard(x.device):
         rc = L.moc_decode_step(z.data_ptr(), r.data_ptr(), x.data_ptr(), b.data_ptr(),
-                               cache.data_ptr(), out.data_ptr(), B, z.shape[1], D, K, S,
+                               cache.data_ptr(), out.data_ptr(), B, z.shape[-1], D, K, S,
                                int(activation_flag), int(routing), _lib.stream_ptr(x.device))
     _lib.check(rc, "moc_decode_step")
     return out
