@@ -469,12 +469,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Routing weights of the super-block (TB + S - 1 rows) are staged in LDS,
 // double buffered; x / dy rows of the next super-block are loaded before the
 // current one is computed.
-// Outputs: dx (own rows), part_da[blockIdx.x][t][KP], part_db[blockIdx.y][KP][S][D].
+// Outputs: dx (own rows), part_da[bx][t][KP], part_db[by][KP][S][D] for channel
+// group bx and token range by.
 //
 // MODE selects the work: kBwdFused does all of the above; kBwdDx only dx;
 // kBwdTaps only the m products (dalpha / dbasis) of the taps
-// [blockIdx.z * S/2, (blockIdx.z + 1) * S/2), writing dalpha partial
-// 2 blockIdx.x + blockIdx.z.  The two partial modes (no activation) keep the
+// [zh * S/2, (zh + 1) * S/2) for tap half zh, writing dalpha partial 2 bx + zh.  The two partial modes (no activation) keep the
 // working set of 8 taps x 32 routes within two waves per SIMD: the fused pass
 // needs the W operands of every tap beside the dbasis accumulators.
 constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
@@ -485,8 +485,12 @@ constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 #ifndef MOC_BWD_MIN_WAVES
 #define MOC_BWD_MIN_WAVES 2
 #endif
+#ifndef MOC_BWD_TAPS_WAVES
+#define MOC_BWD_TAPS_WAVES MOC_BWD_MIN_WAVES
+#endif
 template <int S, int KC, int MODE>
-constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2) ? 1 : MOC_BWD_MIN_WAVES;
+constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2) ? 1
+                             : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
 __global__ void __launch_bounds__(64 * WPG)
@@ -495,7 +499,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
-           int n_sb) {
+           int n_sb, int gx, int gy) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -503,11 +507,27 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   using MS = MSplit<BF>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
   // route chunks of dbasis / dalpha this workgroup accumulates: all KC, or with
-  // SPLIT the single chunk kc0 = blockIdx.z (W still uses every route)
+  // SPLIT the single chunk kc0 = zh (W still uses every route)
   constexpr int KX = SPLIT ? 1 : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
-  // grid.z: route chunk (SPLIT), tap half (kBwdTaps) above it
-  const int kc0 = SPLIT ? static_cast<int>(blockIdx.z) % KC : 0;
+  static_assert(!SPLIT || KC == 2, "the route split halves two route chunks");
+  // Workgroup -> (channel group bx, token range by, half zh).  Split in halves
+  // (route chunks with SPLIT, taps in kBwdTaps), the grid is 1-D and the two
+  // halves of a tile are 8 workgroup ids apart: ids go round-robin over the 8
+  // XCDs, so both halves run on one XCD at about the same time and the second
+  // finds the tile's x / dy rows in that XCD's L2.
+  constexpr bool ZS = SPLIT || MODE == kBwdTaps;
+  static_assert(!(SPLIT && MODE == kBwdTaps), "one split at a time");
+  int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y), zh = 0;
+  if constexpr (ZS) {
+    const int L = static_cast<int>(blockIdx.x);
+    const int t = (L >> 4) * 8 + (L & 7);
+    if (t >= gx * gy) return;  // whole workgroup, before any barrier
+    zh = (L >> 3) & 1;
+    bx = t % gx;
+    by = t / gx;
+  }
+  const int kc0 = SPLIT ? zh : 0;
   constexpr int EOWN = TB - (S - 1);
   constexpr int NP = MS::kParts;
   constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
@@ -519,7 +539,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
   constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
-  const int th = MODE == kBwdTaps ? static_cast<int>(blockIdx.z) / (SPLIT ? KC : 1) : 0;
+  const int th = MODE == kBwdTaps ? zh : 0;
   const int s0 = th * ST;
   constexpr int ZDA = MODE == kBwdTaps ? 2 : 1;  // dalpha partials per workgroup column
   const int zda = th;
@@ -547,10 +567,14 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   // dalpha B operands of each wave's channels (bf16, one 16-route chunk): rows
   // (s, k), CW channels (with rows (k, s) the reads of a 16-lane group, rows k
   // = j at one s, hit each bank twice); with more routes they stay in registers
-  constexpr bool kBdaLds = BF && KX == 1 && DO_M;
+  // (the taps pass keeps them in LDS for both chunks, and its dalpha tiles
+  // single-buffered, one more barrier per super-block, to stay within two
+  // waves per SIMD without register spills)
+  constexpr bool kBdaLds = BF && DO_M && (KX == 1 || MODE == kBwdTaps);
   constexpr int BROW = CW + 4;
   __shared__ __align__(16) E b_lds[kBdaLds ? WPG : 1][kBdaLds ? 16 * KX * ST : 1][kBdaLds ? BROW : 1];
-  __shared__ float da_lds[DO_M ? 2 : 1][DO_M ? WPG : 1][NB][KX][16][17];
+  constexpr int DAB = MODE == kBwdTaps ? 1 : 2;  // dalpha tile buffers
+  __shared__ float da_lds[DO_M ? DAB : 1][DO_M ? WPG : 1][NB][KX][16][17];
 
   const E* __restrict__ x = static_cast<const E*>(xv);
   const E* __restrict__ dy = static_cast<const E*>(dyv);
@@ -559,13 +583,13 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const int lane = tid & 63, wave = tid >> 6;
   const int j = lane & 15, q = lane >> 4;
   const int64_t N = seq.n_tokens;
-  const int64_t d0 = (static_cast<int64_t>(blockIdx.x) * WPG + wave) * CW;
+  const int64_t d0 = (static_cast<int64_t>(bx) * WPG + wave) * CW;
   const bool wave_on = d0 < D;
   const int64_t dl = d0 + NC * j;
   const bool ch_ok = wave_on && dl < D;
 
   constexpr int ESZ = static_cast<int>(sizeof(E));
-  const int64_t first = static_cast<int64_t>(blockIdx.y) * n_sb * EOWN;
+  const int64_t first = static_cast<int64_t>(by) * n_sb * EOWN;
   // buffers over the rows this workgroup touches: x / dy / dx rows [row_lo, row_hi),
   // alpha rows [first, a_hi)
   const int64_t last_t0 = first + static_cast<int64_t>(n_sb - 1) * EOWN;
@@ -987,25 +1011,27 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     else body(std::true_type{});
 
     if constexpr (DO_M) {
+      // one tile buffer: every wave has summed the previous super-block's tiles
+      if constexpr (DAB == 1) __syncthreads();
 #pragma unroll
       for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
         for (int kx = 0; kx < KX; ++kx)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) da_lds[buf][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
+          for (int v = 0; v < 4; ++v) da_lds[buf % DAB][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
     }
     if (more) stage_alpha(buf ^ 1);
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
     if constexpr (DO_M) {
-      const int64_t pda = static_cast<int64_t>(blockIdx.x) * ZDA + zda;
+      const int64_t pda = static_cast<int64_t>(bx) * ZDA + zda;
       for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
         const int rb = idx / (KX * 256);
         const int kx = (idx / 256) % KX;
         const int row = (idx >> 4) & 15, col = idx & 15;
         float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < WPG; ++w) sum += da_lds[buf][w][rb][kx][row][col];
+        for (int w = 0; w < WPG; ++w) sum += da_lds[buf % DAB][w][rb][kx][row][col];
         const int64_t t = t0 + 16 * rb + row;
         if (t < own_end) part_da[(pda * N + t) * KP + 16 * (kc0 + kx) + col] = sum;
       }
@@ -1015,7 +1041,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   // this workgroup's dbasis partial: dbacc[c][s][kx][v] is
   // (k = 16 (kc0 + kx) + j, s0 + s, channel d0 + NC (4q + v) + c)
   if (DO_M && wave_on) {
-    const int64_t base = static_cast<int64_t>(blockIdx.y) * KP;
+    const int64_t base = static_cast<int64_t>(by) * KP;
 #pragma unroll
     for (int kx = 0; kx < KX; ++kx)
 #pragma unroll

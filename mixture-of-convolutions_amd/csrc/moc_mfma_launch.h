@@ -77,7 +77,7 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
 }
 
 // The backward in two passes (bwd_kernel modes kBwdDx, then kBwdTaps with the
-// taps split over grid.z) where the fused pass does not fit two waves per SIMD
+// taps split in halves) where the fused pass does not fit two waves per SIMD
 // and no activation needs P: bf16, 32 routes, 8 taps.
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && KC == 2 && S == 8;
@@ -89,8 +89,8 @@ inline int bwd_da_halves(const Problem& p) {
 }
 
 // Fused pass with 32 routes (bf16): each workgroup accumulates dbasis / dalpha
-// for one of the two 16-route chunks (grid.z), as the accumulators and dalpha
-// operands of both would not fit in registers beside the W operands.
+// for one of the two 16-route chunks, as the accumulators and dalpha operands
+// of both would not fit in registers beside the W operands.
 template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
              void* dx, float* part_da, float* part_db, hipStream_t st) {
@@ -98,21 +98,24 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
   const auto* a = static_cast<const E*>(a_c);
   const auto* b = static_cast<const E*>(b_c);
+  const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
+  // a grid split in halves is 1-D: 16 workgroups per 8 tiles (see bwd_kernel)
+  const dim3 halves(static_cast<unsigned>(16 * cdiv(static_cast<int64_t>(gx) * gy, 8)));
   if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
     if (dx != nullptr)
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
-                         dim3(g.gx, g.gy, 1), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
-                         part_db, p.seq, p.D, g.n_sb);
-    // (splitting the route chunks over grid.z as well forms every m product
-    // twice again: measured slower than the register spills it avoids)
+                         dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
+                         part_db, p.seq, p.D, g.n_sb, gx, gy);
+    // (splitting the route chunks as well forms every m product twice again:
+    // measured slower than the register spills it avoids)
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdTaps>),
-                       dim3(g.gx, g.gy, 2), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, nullptr,
-                       part_da, part_db, p.seq, p.D, g.n_sb);
+                       halves, dim3(64 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da, part_db,
+                       p.seq, p.D, g.n_sb, gx, gy);
   } else {
     constexpr bool kSplit = BF && KC == 2;
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
-                       dim3(g.gx, g.gy, kSplit ? KC : 1), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx,
-                       part_da, part_db, p.seq, p.D, g.n_sb);
+                       kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b,
+                       dx, part_da, part_db, p.seq, p.D, g.n_sb, gx, gy);
   }
 }
 
