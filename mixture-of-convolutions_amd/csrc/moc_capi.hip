@@ -191,8 +191,6 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
 size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                     int64_t kernel_size, int x_dtype, int routing) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
-  // sized without activation: the most the backward needs (two dalpha partials
-  // per channel group where it runs in two passes, which it does only then)
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, routing);
   return backward_bytes(p);

@@ -473,10 +473,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 // group bx and token range by.
 //
 // MODE selects the work: kBwdFused does all of the above; kBwdDx only dx;
-// kBwdTaps only the m products (dalpha / dbasis) of the taps
-// [zh * S/2, (zh + 1) * S/2) for tap half zh, writing dalpha partial 2 bx + zh.  The two partial modes (no activation) keep the
-// working set of 8 taps x 32 routes within two waves per SIMD: the fused pass
-// needs the W operands of every tap beside the dbasis accumulators.
+// kBwdTaps only the m products (dalpha / dbasis), its waves in two sets over
+// the same channels, one per half of the taps.  The two partial modes (no
+// activation) keep the working set of 8 taps x 32 routes within two waves per
+// SIMD: the fused pass needs the W operands of every tap beside the dbasis
+// accumulators.
 constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 // Minimum waves per SIMD the backward is compiled for (register budget 512 / n).
 // Two, except for the fused pass with 8 taps and 32 routes: there the working
@@ -511,12 +512,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   constexpr int KX = SPLIT ? 1 : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
   static_assert(!SPLIT || KC == 2, "the route split halves two route chunks");
-  // Workgroup -> (channel group bx, token range by, half zh).  Split in halves
-  // (route chunks with SPLIT, taps in kBwdTaps), the grid is 1-D and the two
-  // halves of a tile are 8 workgroup ids apart: ids go round-robin over the 8
-  // XCDs, so both halves run on one XCD at about the same time and the second
-  // finds the tile's x / dy rows in that XCD's L2.
-  constexpr bool ZS = SPLIT || MODE == kBwdTaps;
+  // Workgroup -> (channel group bx, token range by, route half zh).  Split in
+  // route halves (SPLIT), the grid is 1-D and the two halves of a tile are 8
+  // workgroup ids apart: ids go round-robin over the 8 XCDs, so both halves run
+  // on one XCD at about the same time and the second finds the tile's x / dy
+  // rows in that XCD's L2.
+  constexpr bool ZS = SPLIT;
   static_assert(!(SPLIT && MODE == kBwdTaps), "one split at a time");
   int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y), zh = 0;
   if constexpr (ZS) {
@@ -539,10 +540,14 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
   constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
-  const int th = MODE == kBwdTaps ? zh : 0;
+  // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, S/2) and
+  // [S/2, S): x and dy rows are read once per workgroup and the dalpha sum over
+  // the workgroup's waves covers every tap (one partial per channel group)
+  static_assert(MODE != kBwdTaps || WPG % 2 == 0, "tap halves pair the waves");
+  constexpr int WCH = MODE == kBwdTaps ? WPG / 2 : WPG;  // waves across channels
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int th = MODE == kBwdTaps ? wave / WCH : 0;
   const int s0 = th * ST;
-  constexpr int ZDA = MODE == kBwdTaps ? 2 : 1;  // dalpha partials per workgroup column
-  const int zda = th;
   // x window rows: every tap (P, or the fused m products), ST taps from s0, none
   constexpr bool NEED_X = DO_M || ACT;
   constexpr int WX = MODE == kBwdTaps ? R + ST - 1 : (NEED_X ? W : 1);
@@ -580,10 +585,10 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const E* __restrict__ dy = static_cast<const E*>(dyv);
   E* __restrict__ dx = static_cast<E*>(dxv);
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
   const int j = lane & 15, q = lane >> 4;
   const int64_t N = seq.n_tokens;
-  const int64_t d0 = (static_cast<int64_t>(bx) * WPG + wave) * CW;
+  const int64_t d0 = (static_cast<int64_t>(bx) * WCH + wave % WCH) * CW;
   const bool wave_on = d0 < D;
   const int64_t dl = d0 + NC * j;
   const bool ch_ok = wave_on && dl < D;
@@ -1024,7 +1029,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
     if constexpr (DO_M) {
-      const int64_t pda = static_cast<int64_t>(bx) * ZDA + zda;
+      const int64_t pda = bx;
       for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
         const int rb = idx / (KX * 256);
         const int kx = (idx / 256) % KX;

@@ -216,7 +216,7 @@ Plan plan(const Problem& p, bool backward) {
   if (backward) {
     pl.bg = bwd_grid(p.n_tokens, p.D, p.S);
     pl.off_pda = off;
-    off += al(static_cast<size_t>(pl.bg.gx) * bwd_da_halves(p) * p.n_tokens * pl.KP * 4);
+    off += al(static_cast<size_t>(pl.bg.gx) * p.n_tokens * pl.KP * 4);
     pl.off_pdb = off;
     off += al(static_cast<size_t>(pl.bg.gy) * pl.KP * p.S * p.D * 4);
   }
@@ -322,7 +322,7 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
                          ? reinterpret_cast<const float*>(ws + pl.off_ar) : nullptr;
   const auto* a_w = static_cast<const uint16_t*>(alpha);
   const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
-  const int64_t n_da = static_cast<int64_t>(pl.bg.gx) * bwd_da_halves(p);
+  const int64_t n_da = pl.bg.gx;
   if (pl.KP == 16) {
     hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda, n_da, pdb,
                        static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,

@@ -82,11 +82,6 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && KC == 2 && S == 8;
 }
-// dalpha partials per workgroup column of bwd_grid
-inline int bwd_da_halves(const Problem& p) {
-  return bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16), p.activation != 0,
-                      p.x_dt == DT_BF16) ? 2 : 1;
-}
 
 // Fused pass with 32 routes (bf16): each workgroup accumulates dbasis / dalpha
 // for one of the two 16-route chunks, as the accumulators and dalpha operands
@@ -106,11 +101,12 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
                          dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
                          part_db, p.seq, p.D, g.n_sb, gx, gy);
-    // (splitting the route chunks as well forms every m product twice again:
-    // measured slower than the register spills it avoids)
-    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdTaps>),
-                       halves, dim3(64 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da, part_db,
-                       p.seq, p.D, g.n_sb, gx, gy);
+    // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
+    // chunks as well forms every m product twice again: measured slower than
+    // the register spills it avoids)
+    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
+                       dim3(g.gx, g.gy), dim3(128 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da,
+                       part_db, p.seq, p.D, g.n_sb, gx, gy);
   } else {
     constexpr bool kSplit = BF && KC == 2;
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
