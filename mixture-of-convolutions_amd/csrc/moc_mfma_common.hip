@@ -197,9 +197,11 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15)
 
 bool direct(const Problem& p, const void* alpha, const void* basis, const void* dalpha) {
   static const bool prep_forced = std::getenv("MOC_MFMA_PREP") != nullptr;
+  // K = 16 or 32: the caller's [N, K] weights and [K, S, D] basis are then the
+  // kernels' padded operand layouts (KP = K) as they are
   return !prep_forced && route_form(p.routing) == ROUTE_ALPHA && p.x_dt == DT_BF16 &&
-         p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && p.K == 16 && aligned16(alpha) &&
-         aligned16(basis) && aligned16(dalpha);
+         p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && (p.K == 16 || p.K == 32) &&
+         aligned16(alpha) && aligned16(basis) && aligned16(dalpha);
 }
 
 Plan plan(const Problem& p, bool backward) {
