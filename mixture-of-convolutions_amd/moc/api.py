@@ -469,16 +469,19 @@ class MoC(nn.Module):
                 max_seqlen: Optional[int] = None, cu_seqlens_cpu: Optional[torch.Tensor] = None,
                 chunk_indices: Optional[torch.Tensor] = None
                 ) -> tuple[torch.Tensor, torch.Tensor | None]:
-        if (cache is not None and cu_seqlens is None
-                and ops.decode_step_supported(x, z, self.router, self.conv_bases, cache)):
+        if cache is not None and cu_seqlens is None:
             # single-token step: router GEMM, router activation and cache update
-            # in one launch (the step is not differentiable, as in the reference)
-            if cu_seqlens_cpu is not None or chunk_indices is not None:
-                raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
-            y = ops.launch_decode_step(x, z, self.router, self.conv_bases, cache,
-                                       activation_flag=activation_flag(self.activation),
-                                       routing=_ROUTING_CODES[self.router_activation])
-            return y, (cache if output_final_state else None)
+            # in one launch (the step is not differentiable, as in the reference);
+            # the parameters are fetched once (each module attribute lookup costs
+            # about as much as a tensor check on this per-token path)
+            router, basis = self.router, self.conv_bases
+            if ops.decode_step_supported(x, z, router, basis, cache):
+                if cu_seqlens_cpu is not None or chunk_indices is not None:
+                    raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+                y = ops.launch_decode_step(x, z, router, basis, cache,
+                                           activation_flag=activation_flag(self.activation),
+                                           routing=_ROUTING_CODES[self.router_activation])
+                return y, (cache if output_final_state else None)
         if (cache is None and self.router.shape[0] <= ops.ROUTER_MAX_ROUTED_K
                 and ops.router_supported(z, self.router)):
             return self._forward_kernels(x, z, output_final_state, cu_seqlens, max_seqlen,
