@@ -783,17 +783,28 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
             if (!MASK || ((ok[r] >> s) & 1u)) p[r][c] = fmaf(xw[r + s][c], wq[jb][v], p[r][c]);
           }
         }
+        // g *= silu'(P) = sg (1 + P (1 - sg)), sg = sigmoid(P) as sigmoid_f forms
+        // it, in stages over all R x NC values so that the latencies of their
+        // independent transcendentals overlap
+        float sg[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int c = 0; c < NC; ++c) {
-            const float pv = p[r][c];
-            const float sg = sigmoid_f(pv);
-            g[r][c] = g[r][c] * (sg * (1.0f + pv * (1.0f - sg)));
-          }
+          for (int c = 0; c < NC; ++c) sg[r][c] = __builtin_amdgcn_exp2f(-p[r][c] * 1.4426950408889634f);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) sg[r][c] = __builtin_amdgcn_rcpf(1.0f + sg[r][c]);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            g[r][c] = g[r][c] * (sg[r][c] * (1.0f + p[r][c] * (1.0f - sg[r][c])));
       }
 
-      // dx: taps in ascending order (with SPLIT, by the kc0 = 0 workgroups only)
+      // dx: taps in descending order, so that the first jobs (shift 0) need none
+      // of the rows gf brings from the next lane group (with SPLIT, by the
+      // kc0 = 0 workgroups only)
       if (DO_DX && dx != nullptr && kc0 == 0) {
         // g of the S-1 rows after this lane's run: first rows of lane group q+1
         float gf[S - 1][NC];
@@ -810,7 +821,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
         constexpr int NJ = S * NB * NC;
         f32x4 wq[NJ];
         auto issue = [&](int jb) {
-          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
+          const int s = S - 1 - jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
           if constexpr (BF && KC == 2) {
             w4 = C::mma2(aop(S - 1 - s, b, 0), aop(S - 1 - s, b, 1), bop[c][s][0], bop[c][s][1], w4);
@@ -825,7 +836,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
         for (int jb = 0; jb < NJ; ++jb) {
           if (jb + kLead < NJ) issue(jb + kLead);
-          const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
+          const int s = S - 1 - jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           const int off = S - 1 - s;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
