@@ -1039,7 +1039,26 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     if (more) stage_alpha(buf ^ 1);
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
-    if constexpr (DO_M) {
+    if constexpr (DO_M && BF) {
+      // unrolled (every thread sums the same number of elements), so that all
+      // of its LDS reads are in flight together; fp32 keeps the loop below
+      // (LLVM's AGPR rewrite fails on the unrolled form of its 8-tap kernel)
+      constexpr int NSUM = NB * KX * 256 / (64 * WPG);
+      static_assert(NB * KX * 256 % (64 * WPG) == 0, "dalpha tile elements per thread");
+      float* __restrict__ pd = part_da + (static_cast<int64_t>(bx) * N + t0) * KP + 16 * kc0;
+      const int n_own = static_cast<int>(own_end - t0);
+#pragma unroll
+      for (int i = 0; i < NSUM; ++i) {
+        const int idx = tid + i * 64 * WPG;
+        const int rb = idx / (KX * 256);
+        const int kx = (idx / 256) % KX;
+        const int row = (idx >> 4) & 15, col = idx & 15;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) sum += da_lds[buf % DAB][w][rb][kx][row][col];
+        if (16 * rb + row < n_own) pd[(16 * rb + row) * KP + 16 * kx + col] = sum;
+      }
+    } else if constexpr (DO_M) {
       const int64_t pda = bx;
       for (int idx = tid; idx < NB * KX * 256; idx += 64 * WPG) {
         const int rb = idx / (KX * 256);
