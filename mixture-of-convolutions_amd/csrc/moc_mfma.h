@@ -453,7 +453,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Backward, stage 1.  A workgroup of WPG waves covers WPG * CW channels and a
-// range of n_sb super-blocks; all its waves walk the same super-blocks, one
+// range of super-blocks (ranges by < gy1 share n_old of them, the later ones
+// the rest: the launch may give the workgroups dispatched first longer ranges,
+// as the SIMD favours their waves); all its waves walk the same super-blocks, one
 // workgroup barrier per super-block.  Super-block i covers rows [t0, t0 + TB)
 // with t0 = i * EOWN, EOWN = TB - (S-1): its first EOWN rows are its own, the
 // last S-1 rows only provide the later g / W the own rows' dx needs (they are
@@ -500,7 +502,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
-           int n_sb, int gx, int gy) {
+           int gx, int gy, int gy1, int n_old, int n_total) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -594,10 +596,17 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const bool ch_ok = wave_on && dl < D;
 
   constexpr int ESZ = static_cast<int>(sizeof(E));
-  const int64_t first = static_cast<int64_t>(by) * n_sb * EOWN;
+  // super-blocks [sb_lo, sb_hi) of this range: ranges by < gy1 share the first
+  // n_old, the others the rest
+  const int64_t sb_lo = by < gy1 ? static_cast<int64_t>(by) * n_old / gy1
+                                 : n_old + static_cast<int64_t>(by - gy1) * (n_total - n_old) / (gy - gy1);
+  const int64_t sb_hi = by < gy1 ? static_cast<int64_t>(by + 1) * n_old / gy1
+                                 : n_old + static_cast<int64_t>(by + 1 - gy1) * (n_total - n_old) / (gy - gy1);
+  const int nsb = static_cast<int>(sb_hi - sb_lo);
+  const int64_t first = sb_lo * EOWN;
   // buffers over the rows this workgroup touches: x / dy / dx rows [row_lo, row_hi),
   // alpha rows [first, a_hi)
-  const int64_t last_t0 = first + static_cast<int64_t>(n_sb - 1) * EOWN;
+  const int64_t last_t0 = first + static_cast<int64_t>(nsb - 1) * EOWN;
   const int64_t row_lo = (first - (S - 1) > 0) ? first - (S - 1) : 0;
   const int64_t row_hi = (last_t0 + TB < N) ? last_t0 + TB : N;
   const int64_t a_hi = (last_t0 + AROWS < N) ? last_t0 + AROWS : N;
@@ -699,7 +708,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   __syncthreads();
 
   StartCursor cursor;
-  for (int sb = 0; sb < n_sb; ++sb) {
+  for (int sb = 0; sb < nsb; ++sb) {
     const int64_t t0 = first + static_cast<int64_t>(sb) * EOWN;
     if (t0 >= N) break;  // uniform over the workgroup
     const int buf = sb & 1;
@@ -717,7 +726,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int c = 0; c < NC; ++c) g[r][c] = C::to_f(dr[r][c]);
-    const bool more = (sb + 1 < n_sb) && (t0 + EOWN < N);
+    const bool more = (sb + 1 < nsb) && (t0 + EOWN < N);
     if (more) fetch(t0 + EOWN);
 
     // alpha operand of token-row block b shifted by e rows (row i = j)

@@ -3,6 +3,8 @@
 // library sees them through the extern declarations at the bottom.
 #pragma once
 
+#include <atomic>
+
 #include "moc_kernels.h"
 #include "moc_mfma.h"
 
@@ -28,7 +30,10 @@ constexpr int64_t kBwdTargetWG = MOC_BWD_TARGET_WG;
 
 struct Grid2 {
   unsigned gx, gy;
-  int n_sb;
+  int n_sb;        // super-blocks per range (at most)
+  int gy1 = 0;      // backward: ranges y < gy1 share the first n_old super-blocks,
+  int n_old = 0;    // the others the remaining n_total - n_old; the counts of a
+  int n_total = 0;  // tier's ranges differ by at most one
 };
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -62,8 +67,60 @@ inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S) {
   // bytes (4-byte elements assumed), i.e. more, shorter ranges for long inputs
   const int64_t max_sb = ((int64_t(1) << 30) / (D * 4) - 16 * kBwdNB) / eown;
   if (n_sb > max_sb) n_sb = max_sb > 1 ? max_sb : 1;
-  return Grid2{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
-               static_cast<int>(n_sb)};
+  Grid2 g{static_cast<unsigned>(gx), static_cast<unsigned>(cdiv(n_super, n_sb)),
+          static_cast<int>(n_sb)};
+  g.gy1 = static_cast<int>(g.gy);
+  g.n_old = static_cast<int>(n_sb * static_cast<int64_t>(g.gy));
+  g.n_total = g.n_old;
+  return g;
+}
+
+// Number of compute units of the current device (cached per device).
+inline int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Backward ranges in two tiers.  A grid of 2 n_cu workgroups with two of them
+// resident per CU is dispatched one per CU first: workgroups y < gy1 = n_cu / gx
+// are the older of each CU's pair, and the SIMD issues the older wave first
+// whenever both are ready.  Measured on the headline shape: the older wave
+// takes 3.6 us per super-block, the younger 5.4 us while both run and 3.3 us
+// alone, so with equal ranges the younger workgroups run their last quarter
+// alone.  The older ranges share kBwdOldShare percent of the super-blocks
+// instead, so that both tiers finish at about the same time.  Other grids, or
+// a CU count that gx does not divide, keep equal ranges.
+#ifndef MOC_BWD_OLD_SHARE
+#define MOC_BWD_OLD_SHARE 62
+#endif
+constexpr int64_t kBwdOldShare = MOC_BWD_OLD_SHARE;
+
+inline Grid2 bwd_grid_tiered(int64_t N, int64_t D, int64_t S, int n_cu) {
+  Grid2 g = bwd_grid(N, D, S);
+  if (n_cu <= 0 || n_cu % static_cast<int64_t>(g.gx) != 0) return g;
+  const int64_t gy1 = n_cu / static_cast<int64_t>(g.gx);
+  const int64_t gy = g.gy;
+  if (gy != 2 * gy1) return g;
+  const int64_t eown = 16 * kBwdNB - (S - 1);
+  const int64_t n_super = cdiv(N, eown);
+  const int64_t max_sb = ((int64_t(1) << 30) / (D * 4) - 16 * kBwdNB) / eown;
+  const int64_t n_old = (n_super * kBwdOldShare + 50) / 100;
+  const int64_t n1 = cdiv(n_old, gy1), n2 = cdiv(n_super - n_old, gy - gy1);
+  if (n1 > max_sb || n2 < 1 || n2 > n1) return g;
+  g.n_sb = static_cast<int>(n1);
+  g.gy1 = static_cast<int>(gy1);
+  g.n_old = static_cast<int>(n_old);
+  g.n_total = static_cast<int>(n_super);
+  return g;
 }
 
 template <int S, int KC, bool ACT, bool BF>
@@ -90,7 +147,10 @@ template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
              void* dx, float* part_da, float* part_db, hipStream_t st) {
   using E = typename CT<BF>::elem;
-  const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
+  constexpr bool kSplit = BF && KC == 2;
+  // tiers for the fused pass at two resident workgroups per CU (not split in halves)
+  constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused> == 2;
+  const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, p.D, S, device_cu_count()) : bwd_grid(p.n_tokens, p.D, S);
   const auto* a = static_cast<const E*>(a_c);
   const auto* b = static_cast<const E*>(b_c);
   const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
@@ -100,18 +160,17 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     if (dx != nullptr)
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
                          dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
-                         part_db, p.seq, p.D, g.n_sb, gx, gy);
+                         part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
     // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
                        dim3(g.gx, g.gy), dim3(128 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da,
-                       part_db, p.seq, p.D, g.n_sb, gx, gy);
+                       part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
   } else {
-    constexpr bool kSplit = BF && KC == 2;
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b,
-                       dx, part_da, part_db, p.seq, p.D, g.n_sb, gx, gy);
+                       dx, part_da, part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
   }
 }
 
