@@ -216,7 +216,7 @@ Plan plan(const Problem& p, bool backward) {
   pl.off_ar = off;
   if (route_grad(p.routing) != ROUTE_ALPHA) off += al(static_cast<size_t>(p.n_tokens) * p.K * 4);
   if (backward) {
-    pl.bg = bwd_grid(p.n_tokens, p.D, p.S);
+    pl.bg = bwd_partials_grid(p);
     pl.off_pda = off;
     off += al(static_cast<size_t>(pl.bg.gx) * p.n_tokens * pl.KP * 4);
     pl.off_pdb = off;

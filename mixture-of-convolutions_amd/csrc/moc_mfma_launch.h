@@ -56,11 +56,11 @@ inline Grid2 fwd_grid(int64_t N, int64_t D) {
                static_cast<int>(n_sb)};
 }
 
-inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S) {
+inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S, int64_t target_wg = kBwdTargetWG) {
   const int64_t gx = cdiv(D, kBwdWPG * 16 * kBwdNC);
   const int64_t eown = 16 * kBwdNB - (S - 1);
   const int64_t n_super = cdiv(N, eown);
-  int64_t gy_target = kBwdTargetWG / gx;
+  int64_t gy_target = target_wg / gx;
   if (gy_target < 1) gy_target = 1;
   int64_t n_sb = cdiv(n_super, gy_target);
   // a workgroup's x / dy buffers span its token range: keep them under 2^30
@@ -123,6 +123,31 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t D, int64_t S, int n_cu) {
   return g;
 }
 
+// The backward in two passes (bwd_kernel modes kBwdDx, then kBwdTaps with the
+// taps split in halves) where the fused pass does not fit two waves per SIMD
+// and no activation needs P: bf16, 32 routes, 8 taps.
+constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
+  return bf && !act && KC == 2 && S == 8;
+}
+inline bool bwd_two_pass(const Problem& p) {
+  return bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16), p.activation != 0,
+                      p.x_dt == DT_BF16);
+}
+
+// The taps pass holds one workgroup per CU (its LDS), so it runs as one round
+// of n_cu workgroups, with ranges twice as long as the default grid's.  Two
+// rounds measured slower: each round pays a prologue of about 6 us, and the
+// second round's workgroups started 15-20 us after the first round's ended.
+inline Grid2 bwd_taps_grid(int64_t N, int64_t D, int64_t S, int n_cu) {
+  return bwd_grid(N, D, S, n_cu > 0 ? n_cu : kBwdTargetWG / 2);
+}
+
+// The grid whose ranges own the dalpha / dbasis partials (workspace, stage 2).
+inline Grid2 bwd_partials_grid(const Problem& p) {
+  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, p.D, p.S, device_cu_count())
+                         : bwd_grid(p.n_tokens, p.D, p.S);
+}
+
 template <int S, int KC, bool ACT, bool BF>
 void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
              hipStream_t st) {
@@ -131,13 +156,6 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
   hipLaunchKernelGGL((fwd_kernel<S, KC, kFwdNB, kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256), 0,
                      st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq, p.D,
                      g.n_sb);
-}
-
-// The backward in two passes (bwd_kernel modes kBwdDx, then kBwdTaps with the
-// taps split in halves) where the fused pass does not fit two waves per SIMD
-// and no activation needs P: bf16, 32 routes, 8 taps.
-constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
-  return bf && !act && KC == 2 && S == 8;
 }
 
 // Fused pass with 32 routes (bf16): each workgroup accumulates dbasis / dalpha
@@ -164,9 +182,12 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
+    // (one round of n_cu workgroups: bwd_taps_grid)
+    const Grid2 gt = bwd_taps_grid(p.n_tokens, p.D, S, device_cu_count());
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
-                       dim3(g.gx, g.gy), dim3(128 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da,
-                       part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
+                       dim3(gt.gx, gt.gy), dim3(128 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da,
+                       part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
+                       gt.n_old, gt.n_total);
   } else {
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b,
