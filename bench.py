@@ -45,7 +45,7 @@ CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
 # 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
 # 131072 KiB -> factor 1.0)
-TRAFFIC_BWD = 241_366_016
+TRAFFIC_BWD = 241_440_768
 DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
 
 
