@@ -9,7 +9,6 @@
 // dz with K = 16); accumulation is fp32, results are rounded to bf16 once.
 // drouter is reduced in a fixed order (per-range partials, then one sum), so it
 // is bitwise reproducible.  bf16 data only; K % 4 == 0, K <= 32, Z % 64 == 0.
-#include <cstdlib>
 
 #include "moc_kernels.h"
 #include "moc_mfma.h"
@@ -733,7 +732,7 @@ void router_backward(const void* z, const void* r, const void* dl, void* dz, voi
   const router::BwdPlan pl = router::bwd_plan(N, Z);
   float* part = static_cast<float*>(workspace);
   // both outputs, K <= 32: one pass over z and dz
-  if (dz != nullptr && dr != nullptr && K <= 32 && std::getenv("MOC_ROUTER_SPLIT") == nullptr) {
+  if (dz != nullptr && dr != nullptr && K <= 32) {
     const dim3 grid(static_cast<unsigned>(Z / 64), static_cast<unsigned>(pl.ranges));
     auto* op = static_cast<uint16_t*>(dz);
     if (K <= 16)
