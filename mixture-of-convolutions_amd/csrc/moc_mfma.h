@@ -672,7 +672,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   E xr[WX][NC];
   E dr[R][NC];
   E arw[APER][AVEC];
-  auto fetch = [&](int64_t t0) {
+  auto fetch_xdy = [&](int64_t t0) {
     // offset of window row w = base + w rb: rows before row_lo wrap to >= 2^31
     // and load zeros; a lane past the channel axis starts at kOffNone.  The x
     // window of the taps from s0 starts s0 rows into the full one.
@@ -682,14 +682,25 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
       for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
 #pragma unroll
     for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(base + (r + S - 1) * rb, dr[r]);
+  };
+  auto fetch_a = [&](int64_t t0) {
+    // taps pass: the per-lane terms are formed here each time (an opaque copy
+    // of the thread id keeps them from being hoisted out of the loop, where
+    // they were spilled and reloaded before every fetch)
+    int tid_f = tid;
+    if constexpr (MODE == kBwdTaps) asm volatile("" : "+v"(tid_f));
 #pragma unroll
     for (int i = 0; i < APER; ++i) {
-      const int chunk = tid + i * 64 * WPG;
+      const int chunk = tid_f + i * 64 * WPG;
       const int64_t tok = t0 + chunk / (KP / AVEC);
       ab.load<AVEC * ESZ>(row_off(tok, first, KP * ESZ, (chunk % (KP / AVEC)) * AVEC * ESZ,
                                   chunk < ACHUNKS),
                           arw[i]);
     }
+  };
+  auto fetch = [&](int64_t t0) {
+    fetch_xdy(t0);
+    fetch_a(t0);
   };
   auto stage_alpha = [&](int buf) {
 #pragma unroll
@@ -727,7 +738,12 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
 #pragma unroll
       for (int c = 0; c < NC; ++c) g[r][c] = C::to_f(dr[r][c]);
     const bool more = (sb + 1 < nsb) && (t0 + EOWN < N);
-    if (more) fetch(t0 + EOWN);
+    // the taps pass loads the next x / dy rows after its m products, where
+    // fewer registers are live (issued here, they were spilled in the body)
+    if (more) {
+      if constexpr (MODE == kBwdTaps) fetch_a(t0 + EOWN);
+      else fetch(t0 + EOWN);
+    }
 
     // alpha operand of token-row block b shifted by e rows (row i = j)
     auto aop = [&](int e, int b, int kc) -> Op {
@@ -1034,6 +1050,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
     };
     if (interior) body(std::false_type{});
     else body(std::true_type{});
+    if constexpr (MODE == kBwdTaps) {
+      if (more) fetch_xdy(t0 + EOWN);
+    }
 
     if constexpr (DO_M) {
       // one tile buffer: every wave has summed the previous super-block's tiles
