@@ -336,3 +336,39 @@ def test_module_step_graph_capture():
         assert torch.equal(yg, ye[t]), t
         (xs.float() * 2).sum().item()  # eager work between replays
     assert torch.equal(cg, ce)
+
+
+def test_bwd_two_tier_ranges():
+    """A backward grid of two workgroups per CU on a 256-CU part (D 2048: 16
+    channel groups; 1827 tokens: 63 super-blocks over 32 ranges) runs with the
+    ranges in two tiers, here of 2-3 and 1-2 super-blocks: fixed-length and
+    packed inputs against the oracle."""
+    dtype, D, K, S, act = torch.bfloat16, 2048, 16, 4, "silu"
+    g = gen(1827)
+    N = 1827
+    x = randn(g, 1, N, D, scale=0.5).to(DEV, dtype)
+    a = torch.softmax(randn(g, 1, N, K), -1).to(DEV, dtype)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
+    dy = randn(g, 1, N, D).to(DEV, dtype)
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
+
+    def run(**kw):
+        xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
+        if "cu_seqlens" in kw:
+            y, _ = moc_triton(xx.view(-1, D), aa.view(-1, K), bb, activation=act, **kw)
+            y.backward(dy.view(-1, D))
+        else:
+            y, _ = moc_triton(xx, aa, bb, activation=act)
+            y.backward(dy)
+        return y.detach().reshape(x.shape), xx.grad, aa.grad, bb.grad
+
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), act)
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), run(), ref):
+        assert_close(n, u, r, dtype)
+    lengths = [300, 1, 640, 29, 857]
+    cu = torch.tensor([0, *itertools.accumulate(lengths)], device=DEV, dtype=torch.int64)
+    assert cu[-1] == N
+    refv = O.moc_varlen_grads_ref(rx.detach().view(-1, D), ra.detach().view(-1, K), rb.detach(),
+                                  cu.cpu(), dy.float().cpu().view(-1, D), act)
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), run(cu_seqlens=cu, max_seqlen=857), refv):
+        assert_close("varlen " + n, u.reshape(r.shape), r, dtype)
