@@ -222,9 +222,11 @@ __global__ void __launch_bounds__(256) router_fwd_kernel(const uint16_t* __restr
 // the result lane (j, q) holds columns 8 q + {0..7} (tiles 0, 1) and
 // 32 + 8 q + {0..7} (tiles 2, 3) of token t_j: two 16-byte stores, and each
 // store instruction writes 64 contiguous bytes of every token row.
-// token blocks per wave: 8 up to 32 routes, 4 above (registers)
+// token blocks per wave: 8 up to 32 routes, 16 above (the router operands,
+// 4 KC gathered loads per lane, are loaded once per wave; the dl operands one
+// block ahead)
 template <int KC>
-constexpr int kDzBlocks = KC <= 2 ? 8 : 4;
+constexpr int kDzBlocks = KC <= 2 ? 8 : 16;
 
 __device__ __forceinline__ int dz_col(int tl, int r) {
   return 32 * (tl >> 1) + 8 * (r >> 2) + 4 * (tl & 1) + (r & 3);
@@ -265,17 +267,19 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
   const Buf ob(dz, N * Z * 2);
   constexpr int NBLK = kDzBlocks<KC>;
   const int64_t tb = static_cast<int64_t>(blockIdx.y) * NBLK * 16;
-  // B operands of all blocks first: rows past N load zeros
-  s16x4 bop[NBLK][KC];
-#pragma unroll
-  for (int b = 0; b < NBLK; ++b)
+  // B operands (dl) of block b, rows past N load zeros: block 0 now, each
+  // next block while the current one is multiplied
+  auto load_b = [&](s16x4 (&bo)[KC], int b) {
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) {
       const int k = 16 * kc + 4 * qq;
       const int64_t t = tb + 16 * b + i;
       const uint32_t off = (k < K) ? static_cast<uint32_t>((t * K + k) * 2) : kOffNone;
-      bop[b][kc] = __builtin_bit_cast(s16x4, load8(db, off));
+      bo[kc] = __builtin_bit_cast(s16x4, load8(db, off));
     }
+  };
+  s16x4 bop[2][KC];
+  load_b(bop[0], 0);
   s16x4 aop[4][KC];
 #pragma unroll
   for (int tl = 0; tl < 4; ++tl)
@@ -293,10 +297,11 @@ __global__ void __launch_bounds__(256) router_dz_kernel(const uint16_t* __restri
     }
 #pragma unroll
   for (int b = 0; b < NBLK; ++b) {
+    if (b + 1 < NBLK) load_b(bop[(b + 1) & 1], b + 1);
     const int64_t t = tb + 16 * b + i;
     f32x4 acc[4];
 #pragma unroll
-    for (int tl = 0; tl < 4; ++tl) acc[tl] = dz_tile<KC>(aop[tl], bop[b]);
+    for (int tl = 0; tl < 4; ++tl) acc[tl] = dz_tile<KC>(aop[tl], bop[b & 1]);
     // rows past N lie outside the buffer: their stores are dropped
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
