@@ -3,7 +3,7 @@ the CPU oracle on identical seeded inputs.
 
 Covers the reference's verify.py matrix (moc/../verify.py:243-285: {bf16, fp32} x
 S in {2,4} x {plain, SiLU} x {fixed, varlen in both forms, step} plus mixed
-storage dtypes) and what it leaves out (SURVEY D12): the MoC module with
+storage dtypes) and what it leaves out: the MoC module with
 softmax / exp routing, prefill from a cache, final states, need_x=False, int64
 cu_seqlens, sequences shorter than S, D not a multiple of any tile, odd K and
 S, bitwise varlen isolation, bitwise determinism.  Tolerances: tests/_parity.py.
