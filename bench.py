@@ -41,11 +41,14 @@ HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 VALU_PEAK = 157.3e12       # flop/s, MI355X fp32 vector (packed)
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
-# FETCH_SIZE (68654 KiB) and WRITE_SIZE (98373 KiB) per dispatch of
+# FETCH_SIZE (68700 KiB) and WRITE_SIZE (98382 KiB) per dispatch of
 # `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
 # 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
-# 131072 KiB -> factor 1.0)
+# 131072 KiB -> factor 1.0); profiles/traffic_fwd_bwd_config2.md
 TRAFFIC_BWD = 241_440_768
+# input sets the timed loops cycle through: 3 x (x, z) = 402 MB at CFG, more
+# than the 256 MB last-level cache, so each step reads its inputs from HBM
+ROTATE = 3
 DECODE = dict(B=256, D=2048, Z=2048, K=16, S=4, prompt=1024, steps=512)
 
 
@@ -65,7 +68,10 @@ def flops_bwd(N, D, K, S, silu=True):
     return N * D * S * (6 * K + 3 + 2 * int(silu))
 
 
-def build_layer(dev, dtype=torch.bfloat16, cfg=CFG, seed=0):
+def build_layer(dev, dtype=torch.bfloat16, cfg=CFG, seed=0, n_sets=1):
+    """The headline layer and ``n_sets`` input pairs (x, z): the first drawn
+    from the seeded CPU generator (the BASELINE configs[1] recipe), the others
+    on the GPU (same distribution, only there to rotate through)."""
     import moc
     g = torch.Generator().manual_seed(seed)
     torch.manual_seed(seed)
@@ -75,7 +81,25 @@ def build_layer(dev, dtype=torch.bfloat16, cfg=CFG, seed=0):
     m = m.to(dev, dtype)
     x = (torch.randn(cfg["B"], cfg["T"], cfg["D"], generator=g)).to(dev, dtype).requires_grad_()
     z = (torch.randn(cfg["B"], cfg["T"], cfg["Z"], generator=g)).to(dev, dtype).requires_grad_()
-    return m, x, z
+    sets = [(x, z)]
+    gd = torch.Generator(device=dev).manual_seed(seed + 1)
+    for _ in range(n_sets - 1):
+        xi = torch.randn(x.shape, generator=gd, device=dev).to(dtype).requires_grad_()
+        zi = torch.randn(z.shape, generator=gd, device=dev).to(dtype).requires_grad_()
+        sets.append((xi, zi))
+    return m, sets
+
+
+class _Cycle:
+    """Round-robin over a list (the input sets of a timed loop)."""
+
+    def __init__(self, items):
+        self.items, self.i = items, 0
+
+    def next(self):
+        v = self.items[self.i % len(self.items)]
+        self.i += 1
+        return v
 
 
 def time_region(fn, steps, warmup):
@@ -91,10 +115,12 @@ def time_region(fn, steps, warmup):
     return start.elapsed_time(stop) / steps  # ms
 
 
-def bench_layer(dev, steps, warmup):
-    m, x, z = build_layer(dev)
+def bench_layer(dev, steps, warmup, rotate=ROTATE):
+    m, sets = build_layer(dev, n_sets=rotate)
+    cyc = _Cycle(sets)
 
     def step():
+        x, z = cyc.next()
         m.zero_grad(set_to_none=True)
         x.grad = None
         z.grad = None
@@ -155,30 +181,40 @@ def time_kernel(fn, steps, warmup):
     return ms
 
 
-def entry_calls(dev):
+def entry_calls(dev, rotate=ROTATE):
     """The forward and backward C-ABI entries as the layer calls them, as two
     zero-argument callables (fwd, bwd): on the routing weights the router
     kernel forms (softmax of the bf16 logits), routing "softmax weights given",
-    so the backward returns the logits gradient."""
+    so the backward returns the logits gradient.  The backward gets a full
+    (contiguous) dy, the general case, not the broadcast row of y.sum().  Each
+    call takes the next of ``rotate`` input sets."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX, ROUTE_SOFTMAX_WEIGHTS
-    m, x, z = build_layer(dev)
+    m, sets = build_layer(dev, n_sets=rotate)
+    basis = m.conv_bases.detach()
+    args = []
     with torch.no_grad():
-        weights = ops.router_forward(z, m.router, routing=ROUTE_SOFTMAX)
-        basis = m.conv_bases.detach()
-        xd = x.detach()
-        dy = torch.ones_like(xd)
-    fwd = lambda: ops.launch_forward(xd, weights, basis, activation_flag=1,  # noqa: E731
-                                     routing=ROUTE_SOFTMAX_WEIGHTS)
-    bwd = lambda: ops.launch_backward(xd, weights, basis, dy, activation_flag=1,  # noqa: E731
-                                      need_x=True, routing=ROUTE_SOFTMAX_WEIGHTS)
+        for x, z in sets:
+            weights = ops.router_forward(z, m.router, routing=ROUTE_SOFTMAX)
+            xd = x.detach()
+            args.append((xd, weights, torch.ones_like(xd)))
+    cf, cb = _Cycle(args), _Cycle(args)
+
+    def fwd():
+        xd, w, _ = cf.next()
+        return ops.launch_forward(xd, w, basis, activation_flag=1, routing=ROUTE_SOFTMAX_WEIGHTS)
+
+    def bwd():
+        xd, w, dy = cb.next()
+        return ops.launch_backward(xd, w, basis, dy, activation_flag=1, need_x=True,
+                                   routing=ROUTE_SOFTMAX_WEIGHTS)
     return fwd, bwd
 
 
-def bench_entries(dev, steps, warmup):
+def bench_entries(dev, steps, warmup, rotate=ROTATE):
     """Forward and backward C-ABI entries alone, as the layer calls them:
     (entry ms fwd, entry ms bwd, main-kernel ms fwd, main-kernel ms bwd)."""
-    fwd, bwd = entry_calls(dev)
+    fwd, bwd = entry_calls(dev, rotate)
     return (time_region(fwd, steps, warmup), time_region(bwd, steps, warmup),
             time_kernel(fwd, steps, warmup), time_kernel(bwd, steps, warmup))
 
@@ -193,7 +229,7 @@ def counter_run(dev, which, reps=3):
         b = torch.empty_like(a)
         fn = lambda: b.copy_(a)  # noqa: E731
     else:
-        fwd, bwd = entry_calls(dev)
+        fwd, bwd = entry_calls(dev, 1)
         fn = fwd if which == "fwd" else bwd
     torch.cuda.synchronize()
     for _ in range(reps):
@@ -413,6 +449,9 @@ def main():
     ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
                     help="2: the headline line (default); 3 / 5: one JSON line for BASELINE "
                          "configs[2] (varlen) / configs[4] (QKV triple) instead")
+    ap.add_argument("--rotate", type=int, default=ROTATE,
+                    help="input sets the timed loops cycle through (1: one set reused, "
+                         "which the last-level cache partly holds across steps)")
     ap.add_argument("--counters", choices=("fwd", "bwd", "copy"), default=None,
                     help="only run 3 calls of one entry (or the calibration copy) "
                          "for a rocprofv3 --pmc pass; prints no JSON")
@@ -437,8 +476,8 @@ def main():
     N = CFG["B"] * CFG["T"]
     D, K, S = CFG["D"], CFG["K"], CFG["S"]
 
-    ms = bench_layer(dev, args.steps, args.warmup)
-    t_fwd, t_bwd, k_fwd, k_bwd = bench_entries(dev, args.steps, args.warmup)
+    ms = bench_layer(dev, args.steps, args.warmup, args.rotate)
+    t_fwd, t_bwd, k_fwd, k_bwd = bench_entries(dev, args.steps, args.warmup, args.rotate)
     fb, bb = bytes_fwd(N, D, K, S), bytes_bwd(N, D, K, S)
     roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / 2.5e15)
                + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / 2.5e15)) * 1e6
@@ -465,6 +504,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) x, z; router N(0,0.02); basis U(+-0.002*sqrt(3)))",
+        "input_sets": args.rotate,
         "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[1]", "B": CFG["B"],
                    "T": CFG["T"], "D": D, "z_dim": CFG["Z"], "K": K, "S": S,
                    "activation": "silu", "routing": "softmax", "loss": "y.sum()"},

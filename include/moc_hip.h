@@ -65,6 +65,21 @@ int moc_abi_version(void);
 const char* moc_last_error(void);
 
 /*
+ * Kernel family override; it has no counterpart in the reference (whose Triton
+ * autotuner picks configurations itself).  AUTO runs the matrix-core kernels
+ * wherever they are built for the shape and the generic kernels elsewhere;
+ * GENERIC runs the generic kernels for every shape (to cross-check the two);
+ * MFMA_PREP runs the matrix-core kernels with their operands always converted
+ * by the prep launch (an A/B switch).  Process-wide; workspace sizes follow the
+ * family, so do not change it between a *_workspace_bytes query and the launch
+ * it sizes.  Returns the previous value, or MOC_ERR_ARG.
+ */
+#define MOC_PATH_AUTO      0
+#define MOC_PATH_GENERIC   1
+#define MOC_PATH_MFMA_PREP 2
+int moc_set_kernel_path(int path);
+
+/*
  * Sequence description shared by forward / backward:
  *   cu_seqlens == NULL: fixed length, n_tokens = B*T tokens, sequences of
  *                       seq_len = T tokens each ([B,T,D] viewed as [B*T,D]);
@@ -105,6 +120,10 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
  * launch_backward (moc/ops.py:216-338) and the preact recompute it needed
  * (moc/ops.py:197-213), i.e. _moc_bwd_dx_kernel (moc/kernels.py:156-279) and
  * _moc_bwd_dalpha_dbasis_dot_kernel (moc/kernels.py:282-439).
+ *   dy     : token rows dy_row_stride elements apart: dim (contiguous), or 0
+ *            when one row of dim elements is the gradient of every token (the
+ *            broadcast gradient of y.sum(), which the reference copied into a
+ *            contiguous tensor with dy.contiguous(), moc/api.py:171)
  *   dx     : [n_tokens, dim] in x_dtype, or NULL to skip it (need_x = False)
  *   dalpha : [n_tokens, k] in alpha_dtype; d/dalpha for MOC_ROUTE_ALPHA, or
  *            d/dlogits with the softmax / exp gradient fused in (routing 1-4;
@@ -114,13 +133,14 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
  * reproducible run to run (the reference used relaxed fp32 atomics).
  */
 int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy,
-                 void* dx, void* dalpha, void* dbasis,
+                 int64_t dy_row_stride, void* dx, void* dalpha, void* dbasis,
                  const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
                  int64_t n_tokens, int64_t seq_len,
                  int64_t dim, int64_t k, int64_t kernel_size,
                  int x_dtype, int alpha_dtype, int basis_dtype,
                  int activation, int routing,
                  void* workspace, size_t workspace_bytes, void* stream);
+
 
 /*
  * One decode step, in place.  Replaces launch_update (moc/ops.py:341-362) and

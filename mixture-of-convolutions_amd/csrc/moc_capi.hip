@@ -2,10 +2,9 @@
 // workspace carving and dispatch to the kernels.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
-#include <cstdlib>
-#include <cstring>
 
 #include "../../include/moc_hip.h"
 #include "moc_kernels.h"
@@ -15,6 +14,8 @@ namespace {
 thread_local char g_err[512] = "";
 thread_local hipEvent_t g_prof_start = nullptr;
 thread_local hipEvent_t g_prof_stop = nullptr;
+// kernel family override of moc_set_kernel_path (process-wide)
+std::atomic<int> g_path{MOC_PATH_AUTO};
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -97,6 +98,8 @@ moc::Problem make_problem(const void* cu, int cu64, int64_t n_seqs, int64_t n_to
   p.b_dt = b_dt;
   p.activation = activation;
   p.routing = routing;
+  p.dy_stride = dim;
+  p.path = g_path.load(std::memory_order_relaxed);
   p.prof_start = g_prof_start;
   p.prof_stop = g_prof_stop;
   return p;
@@ -111,11 +114,10 @@ int check_seq(const void* cu, int64_t n_seqs, int64_t seq_len) {
 }
 
 // Kernel family for a problem: the MFMA kernels where they are instantiated,
-// the generic kernels otherwise.  MOC_HIP_PATH=generic forces the generic
-// kernels (used to cross-check the two families).
+// the generic kernels otherwise, or the generic kernels for every problem while
+// moc_set_kernel_path(MOC_PATH_GENERIC) holds (used to cross-check the two).
 bool use_mfma(const moc::Problem& p) {
-  const char* env = std::getenv("MOC_HIP_PATH");
-  if (env != nullptr && std::strcmp(env, "generic") == 0) return false;
+  if (p.path == MOC_PATH_GENERIC) return false;
   return moc::mfma::supported(p);
 }
 
@@ -137,9 +139,15 @@ int hip_status(const char* what) {
 
 extern "C" {
 
-int moc_abi_version(void) { return 1; }
+int moc_abi_version(void) { return 2; }
 
 const char* moc_last_error(void) { return g_err; }
+
+int moc_set_kernel_path(int path) {
+  if (path != MOC_PATH_AUTO && path != MOC_PATH_GENERIC && path != MOC_PATH_MFMA_PREP)
+    return fail(MOC_ERR_ARG, "kernel path must be 0, 1 or 2, got %d", path);
+  return g_path.exchange(path, std::memory_order_relaxed);
+}
 
 int moc_profile_events(void* start_event, void* stop_event) {
   g_prof_start = static_cast<hipEvent_t>(start_event);
@@ -196,43 +204,77 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
   return backward_bytes(p);
 }
 
-int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy, void* dx,
-                 void* dalpha, void* dbasis, const void* cu_seqlens, int cu_seqlens_i64,
-                 int64_t n_seqs, int64_t n_tokens, int64_t seq_len, int64_t dim, int64_t k,
-                 int64_t kernel_size, int x_dtype, int alpha_dtype, int basis_dtype,
-                 int activation, int routing, void* workspace, size_t workspace_bytes,
-                 void* stream) {
-  g_err[0] = '\0';
+}  // extern "C"
+
+namespace {
+
+// Checks of moc_backward / moc_backward_noalloc; fills p.
+int backward_problem(const void* x, const void* alpha, const void* basis, const void* dy,
+                     int64_t dy_row_stride, void* dalpha, void* dbasis, const void* cu_seqlens,
+                     int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens, int64_t seq_len,
+                     int64_t dim, int64_t k, int64_t kernel_size, int x_dtype, int alpha_dtype,
+                     int basis_dtype, int activation, int routing, moc::Problem& p) {
   int rc;
   if ((rc = check_dims(n_tokens, dim, k, kernel_size)) != MOC_OK) return rc;
   if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
   if ((rc = check_seq(cu_seqlens, n_seqs, seq_len)) != MOC_OK) return rc;
   if (!x || !alpha || !basis || !dy || !dalpha || !dbasis)
     return fail(MOC_ERR_ARG, "null tensor pointer");
+  if (dy_row_stride != 0 && dy_row_stride != dim)
+    return fail(MOC_ERR_ARG, "dy_row_stride must be dim (%lld) or 0, got %lld", (long long)dim,
+                (long long)dy_row_stride);
   if ((n_tokens + 255) / 256 > 65535)
     return fail(MOC_ERR_ARG, "n_tokens too large for the backward grid: %lld", (long long)n_tokens);
-  moc::Problem p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k,
-                                kernel_size, x_dtype, alpha_dtype, basis_dtype, activation,
-                                routing);
-  const size_t need = backward_bytes(p);
-  if (workspace_bytes < need || !workspace)
-    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
-                workspace_bytes);
-  hipStream_t st = static_cast<hipStream_t>(stream);
+  p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k, kernel_size,
+                   x_dtype, alpha_dtype, basis_dtype, activation, routing);
+  p.dy_stride = dy_row_stride;
+  return MOC_OK;
+}
+
+// Launches of a checked backward problem on a workspace of backward_bytes(p).
+int backward_launch(const moc::Problem& p, const void* x, const void* alpha, const void* basis,
+                    const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+                    hipStream_t st) {
   if (use_mfma(p)) {
     moc::mfma::backward(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
     return hip_status("moc_backward launch");
   }
   Carve cv{static_cast<char*>(workspace), 0};
-  float* a_r = cv.take<float>(size_t(n_tokens * k));
-  float* basis_c = cv.take<float>(size_t(k * kernel_size * dim));
-  float* scratch = cv.take<float>(moc::generic_bwd_scratch_floats(p));
+  float* a_r = cv.take<float>(size_t(p.n_tokens * p.K));
+  float* basis_c = cv.take<float>(size_t(p.K * p.S * p.D));
+  float* scratch_g = cv.take<float>(moc::generic_bwd_scratch_floats(p));
   moc::launch_prep(p, alpha, basis, a_r, basis_c, st);
   moc::prof_begin(p, st);
-  moc::launch_backward_generic(p, x, dy, dx, dalpha, dbasis, a_r, basis_c, scratch, st);
+  moc::launch_backward_generic(p, x, dy, dx, dalpha, dbasis, a_r, basis_c, scratch_g, st);
   moc::prof_end(p, st);
   return hip_status("moc_backward launch");
 }
+
+}  // namespace
+
+extern "C" {
+
+int moc_backward(const void* x, const void* alpha, const void* basis, const void* dy,
+                 int64_t dy_row_stride, void* dx, void* dalpha, void* dbasis,
+                 const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens,
+                 int64_t seq_len, int64_t dim, int64_t k, int64_t kernel_size, int x_dtype,
+                 int alpha_dtype, int basis_dtype, int activation, int routing, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem p;
+  int rc = backward_problem(x, alpha, basis, dy, dy_row_stride, dalpha, dbasis, cu_seqlens,
+                            cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k, kernel_size,
+                            x_dtype, alpha_dtype, basis_dtype, activation, routing, p);
+  if (rc != MOC_OK) return rc;
+  const size_t need = backward_bytes(p);
+  if (workspace_bytes < need || !workspace)
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  return backward_launch(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace,
+                         static_cast<hipStream_t>(stream));
+}
+
+
 
 int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
                int64_t cache_stride_b, int64_t cache_stride_d, int64_t cache_stride_s, void* y,
@@ -244,8 +286,7 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
   if (batch > kMaxBatch) return fail(MOC_ERR_ARG, "batch too large: %lld", (long long)batch);
   if (!x || !alpha || !basis || !cache || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
-  const char* env = std::getenv("MOC_HIP_PATH");
-  const bool force_generic = env != nullptr && std::strcmp(env, "generic") == 0;
+  const bool force_generic = g_path.load(std::memory_order_relaxed) == MOC_PATH_GENERIC;
   if (!force_generic && moc::decode_supported(batch, dim, k, kernel_size, x_dtype, alpha_dtype,
                                               basis_dtype, cache_stride_b, cache_stride_d,
                                               cache_stride_s)) {

@@ -89,17 +89,18 @@ __global__ void fwd_generic_kernel(const void* __restrict__ x, int x_dt,
 }
 
 // ---------------------------------------------------------------------------
-// Backward.  g = dy * silu'(P) (or dy), kept in fp32 scratch.
-__global__ void bwd_g_kernel(const void* __restrict__ x, const void* __restrict__ dy, int x_dt,
-                             const float* __restrict__ a_r, const float* __restrict__ basis_c,
-                             float* __restrict__ g, SeqLayout seq, int64_t D, int64_t K,
-                             int64_t S, int activation) {
+// Backward.  g = dy * silu'(P) (or dy), kept in fp32 scratch; dy rows are
+// dys elements apart (0: one row for every token).
+__global__ void bwd_g_kernel(const void* __restrict__ x, const void* __restrict__ dy, int64_t dys,
+                             int x_dt, const float* __restrict__ a_r,
+                             const float* __restrict__ basis_c, float* __restrict__ g,
+                             SeqLayout seq, int64_t D, int64_t K, int64_t S, int activation) {
   const int64_t total = seq.n_tokens * D;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    float gv = load_any(dy, x_dt, i);
+    const int64_t t = i / D, d = i - t * D;
+    float gv = load_any(dy, x_dt, t * dys + d);
     if (activation) {
-      const int64_t t = i / D, d = i - t * D;
       int64_t lo, hi;
       seq.bounds(t, lo, hi);
       const float p = preact_at(x, x_dt, a_r, basis_c, t, d, t - lo, K, S, D, x_dt);
@@ -335,8 +336,8 @@ void launch_backward_generic(const Problem& p, const void* x, const void* dy, vo
   float* part = scratch + p.n_tokens * p.D;
   const int64_t n_chunks = (p.n_tokens + kTokChunk - 1) / kTokChunk;
   const unsigned ge = grid_for(p.n_tokens * p.D, 256);
-  hipLaunchKernelGGL(bwd_g_kernel, dim3(ge), dim3(256), 0, st, x, dy, p.x_dt, a_r, basis_c, g,
-                     p.seq, p.D, p.K, p.S, p.activation);
+  hipLaunchKernelGGL(bwd_g_kernel, dim3(ge), dim3(256), 0, st, x, dy, p.dy_stride, p.x_dt, a_r,
+                     basis_c, g, p.seq, p.D, p.K, p.S, p.activation);
   if (dx != nullptr) {
     hipLaunchKernelGGL(bwd_dx_kernel, dim3(ge), dim3(256), 0, st, g, a_r, basis_c, dx, p.x_dt,
                        p.seq, p.D, p.K, p.S);

@@ -9,6 +9,9 @@
 
 namespace moc {
 
+// Kernel family a call runs on (moc_set_kernel_path).
+enum KernelPath : int { PATH_AUTO = 0, PATH_GENERIC = 1, PATH_MFMA_PREP = 2 };
+
 struct Problem {
   SeqLayout seq;     // token axis layout (n_tokens lives here)
   int64_t n_tokens;
@@ -16,6 +19,8 @@ struct Problem {
   int x_dt, a_dt, b_dt;
   int activation;    // 0 = none, 1 = SiLU
   int routing;       // Route
+  int64_t dy_stride = 0;  // backward: elements between token rows of dy (D, or 0 = one row for all)
+  int path = PATH_AUTO;   // PATH_MFMA_PREP: MFMA kernels, operands always through prep
   hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set
   hipEvent_t prof_stop = nullptr;
 };
@@ -34,6 +39,7 @@ void launch_prep(const Problem& p, const void* alpha, const void* basis, float* 
 void launch_forward_generic(const Problem& p, const void* x, const float* a_r,
                             const float* basis_c, void* y, hipStream_t st);
 size_t generic_bwd_scratch_floats(const Problem& p);
+// dy rows are p.dy_stride elements apart
 void launch_backward_generic(const Problem& p, const void* x, const void* dy, void* dx,
                              void* dalpha, void* dbasis, const float* a_r,
                              const float* basis_c, float* scratch, hipStream_t st);

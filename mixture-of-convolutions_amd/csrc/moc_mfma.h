@@ -471,6 +471,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Routing weights of the super-block (TB + S - 1 rows) are staged in LDS,
 // double buffered; x / dy rows of the next super-block are loaded before the
 // current one is computed.
+// dy rows are dys elements apart: D, or 0 when one row serves every token (the
+// broadcast gradient of a sum).
 // Outputs: dx (own rows), part_da[bx][t][KP], part_db[by][KP][S][D] for channel
 // group bx and token range by.
 //
@@ -482,23 +484,25 @@ __device__ __forceinline__ void wave_lds_sync() {
 // accumulators.
 constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 // Minimum waves per SIMD the backward is compiled for (register budget 512 / n).
-// Two, except for the fused pass with 8 taps and 32 routes: there the working
-// set exceeds 256 registers, and one wave per SIMD (spills to AGPRs instead of
-// scratch memory) measured 9% faster than two with scratch spills.
+// Two, except for the bf16 fused pass with 8 taps and 32 routes: there the
+// working set exceeds 256 registers, and one wave per SIMD (spills to AGPRs
+// instead of scratch memory) measured 9% faster than two with scratch spills.
+// (The fp32 form of that pass stays at two: LLVM's AGPR-copy rewrite crashes
+// on its one-wave form.)
 #ifndef MOC_BWD_MIN_WAVES
 #define MOC_BWD_MIN_WAVES 2
 #endif
 #ifndef MOC_BWD_TAPS_WAVES
 #define MOC_BWD_TAPS_WAVES MOC_BWD_MIN_WAVES
 #endif
-template <int S, int KC, int MODE>
-constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2) ? 1
+template <int S, int KC, int MODE, bool BF>
+constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2 && BF) ? 1
                              : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE>)))
-bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
+bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
@@ -613,7 +617,9 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   const uint32_t rb = static_cast<uint32_t>(D * ESZ);
   const uint32_t col = static_cast<uint32_t>(dl * ESZ);
   const Buf xb(x + row_lo * D, (row_hi - row_lo) * D * ESZ);
-  const Buf dyb(dy + row_lo * D, (row_hi - row_lo) * D * ESZ);
+  // dy rows [row_lo, row_hi): rows dys apart, the last one D elements long
+  const uint32_t drb = static_cast<uint32_t>(dys * ESZ);
+  const Buf dyb(dy + row_lo * dys, ((row_hi - row_lo - 1) * dys + D) * ESZ);
   const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
 
@@ -675,13 +681,15 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv,
   auto fetch_xdy = [&](int64_t t0) {
     // offset of window row w = base + w rb: rows before row_lo wrap to >= 2^31
     // and load zeros; a lane past the channel axis starts at kOffNone.  The x
-    // window of the taps from s0 starts s0 rows into the full one.
+    // window of the taps from s0 starts s0 rows into the full one.  dy rows are
+    // t0 + R q + r >= row_lo (never before the buffer, also with dys = 0)
     const uint32_t base = row_off(t0 + R * q - (S - 1), row_lo, rb, col, ch_ok);
     if constexpr (NEED_X)
 #pragma unroll
       for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
+    const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, ch_ok);
 #pragma unroll
-    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(base + (r + S - 1) * rb, dr[r]);
+    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
   };
   auto fetch_a = [&](int64_t t0) {
     // taps pass: the per-lane terms are formed here each time (an opaque copy

@@ -1,6 +1,4 @@
 // MFMA path: operand preparation, backward stage 2, workspace plans, dispatch.
-#include <cstdlib>
-
 #include "moc_mfma_launch.h"
 
 namespace moc {
@@ -196,10 +194,10 @@ struct Plan {
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 bool direct(const Problem& p, const void* alpha, const void* basis, const void* dalpha) {
-  static const bool prep_forced = std::getenv("MOC_MFMA_PREP") != nullptr;
   // K = 16 or 32: the caller's [N, K] weights and [K, S, D] basis are then the
-  // kernels' padded operand layouts (KP = K) as they are
-  return !prep_forced && route_form(p.routing) == ROUTE_ALPHA && p.x_dt == DT_BF16 &&
+  // kernels' padded operand layouts (KP = K) as they are; PATH_MFMA_PREP forces
+  // the prep launch (an A/B switch)
+  return p.path != PATH_MFMA_PREP && route_form(p.routing) == ROUTE_ALPHA && p.x_dt == DT_BF16 &&
          p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && (p.K == 16 || p.K == 32) &&
          aligned16(alpha) && aligned16(basis) && aligned16(dalpha);
 }

@@ -167,7 +167,7 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   using E = typename CT<BF>::elem;
   constexpr bool kSplit = BF && KC == 2;
   // tiers for the fused pass at two resident workgroups per CU (not split in halves)
-  constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused> == 2;
+  constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
   const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, p.D, S, device_cu_count()) : bwd_grid(p.n_tokens, p.D, S);
   const auto* a = static_cast<const E*>(a_c);
   const auto* b = static_cast<const E*>(b_c);
@@ -177,7 +177,7 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
     if (dx != nullptr)
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
-                         dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b, dx, part_da,
+                         dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx, part_da,
                          part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
     // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
     // chunks as well forms every m product twice again: measured slower than
@@ -185,13 +185,13 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     // (one round of n_cu workgroups: bwd_taps_grid)
     const Grid2 gt = bwd_taps_grid(p.n_tokens, p.D, S, device_cu_count());
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
-                       dim3(gt.gx, gt.gy), dim3(128 * kBwdWPG), 0, st, x, dy, a, b, nullptr, part_da,
+                       dim3(gt.gx, gt.gy), dim3(128 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
                        gt.n_old, gt.n_total);
   } else {
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
-                       kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, a, b,
-                       dx, part_da, part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
+                       kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a,
+                       b, dx, part_da, part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
   }
 }
 

@@ -7,25 +7,27 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
-import os
 import threading
 from pathlib import Path
 
 import torch
 
-# MOC_HIP_LIB selects another build of the library (e.g. a tuning variant).
-LIB_PATH = Path(os.environ.get("MOC_HIP_LIB") or Path(__file__).resolve().parent / "libmoc_hip.so")
+LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
+ABI_VERSION = 2
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
 # alpha holds softmax / exp weights already; the backward returns d/dlogits
 ROUTE_SOFTMAX_WEIGHTS, ROUTE_EXP_WEIGHTS = 3, 4
+# kernel families (moc_set_kernel_path)
+PATH_AUTO, PATH_GENERIC, PATH_MFMA_PREP = 0, 1, 2
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float16: DT_F16}
 
 EXPORTED_SYMBOLS = (
     "moc_abi_version",
     "moc_last_error",
+    "moc_set_kernel_path",
     "moc_forward_workspace_bytes",
     "moc_forward",
     "moc_backward_workspace_bytes",
@@ -70,17 +72,19 @@ def _declare(lib: ctypes.CDLL) -> None:
         _p, _z, _p,                # workspace, bytes, stream
     ]
     lib.moc_forward.restype = _i
-    lib.moc_backward.argtypes = [
-        _p, _p, _p, _p,            # x, alpha, basis, dy
+    bwd = [
+        _p, _p, _p, _p, _l,        # x, alpha, basis, dy, dy_row_stride
         _p, _p, _p,                # dx, dalpha, dbasis
         _p, _i, _l,
         _l, _l,
         _l, _l, _l,
         _i, _i, _i,
         _i, _i,
-        _p, _z, _p,
     ]
+    lib.moc_backward.argtypes = bwd + [_p, _z, _p]   # workspace, bytes, stream
     lib.moc_backward.restype = _i
+    lib.moc_set_kernel_path.argtypes = [_i]
+    lib.moc_set_kernel_path.restype = _i
     lib.moc_update.argtypes = [
         _p, _p, _p, _p,            # x, alpha, basis, cache
         _l, _l, _l,                # cache strides (elements)
@@ -124,8 +128,28 @@ def lib() -> ctypes.CDLL:
                     )
                 handle = ctypes.CDLL(str(LIB_PATH))
                 _declare(handle)
+                if handle.moc_abi_version() != ABI_VERSION:
+                    raise RuntimeError(
+                        f"{LIB_PATH} has ABI version {handle.moc_abi_version()}, this package "
+                        f"binds version {ABI_VERSION}; rebuild it with "
+                        "`python mixture-of-convolutions_amd/build_lib.py`")
                 _lib = handle
     return _lib
+
+
+@contextlib.contextmanager
+def kernel_path(path: int):
+    """Run the enclosed calls on kernel family ``path`` (PATH_GENERIC to
+    cross-check the generic kernels against the matrix-core ones), then restore
+    the previous family.  Process-wide."""
+    L = lib()
+    old = L.moc_set_kernel_path(int(path))
+    if old < 0:
+        check(old, "moc_set_kernel_path")
+    try:
+        yield
+    finally:
+        L.moc_set_kernel_path(old)
 
 
 def check(rc: int, what: str) -> None:

@@ -105,6 +105,23 @@ def _seq_args(x: torch.Tensor, cu_seqlens: torch.Tensor | None):
             cu_seqlens.numel() - 1, N, 0, D)
 
 
+def dy_operand(dy: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+    """(dy tensor, row stride in elements) for moc_backward.  A gradient that is
+    one row broadcast over every token (stride 0 over all token dimensions, as
+    autograd hands over the gradient of ``y.sum()``) is passed as that single
+    row with row stride 0, instead of the [n_tokens, D] copy that
+    ``dy.contiguous()`` would make (the reference's moc/api.py:171); anything
+    else is made contiguous, rows D apart."""
+    D = dy.shape[-1]
+    if dy.ndim >= 2 and dy.numel() > D and all(st == 0 for st in dy.stride()[:-1]):
+        row = dy[(0,) * (dy.ndim - 1)]
+        return row.to(dtype).contiguous(), 0
+    dy = dy.contiguous()
+    if dy.dtype != dtype:
+        dy = dy.to(dtype)
+    return dy, D
+
+
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
@@ -132,9 +149,10 @@ def launch_forward(
     cu_ptr, cu64, n_seqs, n_tokens, seq_len, D = _seq_args(x, cu_seqlens)
     out = torch.empty_like(x)
     x_dt = _lib.dtype_code(x.dtype)
-    nbytes = L.moc_forward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
-    ws = _workspace(nbytes, x.device)
     with _lib.device_guard(x.device):
+        # the size depends on the launch device (its CU count): queried there
+        nbytes = L.moc_forward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
+        ws = _workspace(nbytes, x.device)
         rc = L.moc_forward(
             x.data_ptr(), a.data_ptr(), b.data_ptr(), out.data_ptr(),
             cu_ptr, cu64, n_seqs, n_tokens, seq_len, D, K, S,
@@ -185,9 +203,7 @@ def launch_backward(
     del preact, cu_seqlens_cpu, chunk_indices
     L = _lib.lib()
     x = x.contiguous()
-    dy = moc_dy.contiguous()
-    if dy.dtype != x.dtype:
-        dy = dy.to(x.dtype)
+    dy, dy_stride = dy_operand(moc_dy, x.dtype)
     a = _operand(alpha)
     b = _operand(basis)
     K, S, _ = b.shape
@@ -196,11 +212,12 @@ def launch_backward(
     dalpha = torch.empty_like(a)
     dbasis = torch.empty_like(b)
     x_dt = _lib.dtype_code(x.dtype)
-    nbytes = L.moc_backward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
-    ws = _workspace(nbytes, x.device)
     with _lib.device_guard(x.device):
+        # the size depends on the launch device (its CU count): queried there
+        nbytes = L.moc_backward_workspace_bytes(n_tokens, D, K, S, x_dt, routing)
+        ws = _workspace(nbytes, x.device)
         rc = L.moc_backward(
-            x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(),
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(), dy_stride,
             None if dx is None else dx.data_ptr(), dalpha.data_ptr(), dbasis.data_ptr(),
             cu_ptr, cu64, n_seqs, n_tokens, seq_len, D, K, S,
             x_dt, _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
@@ -245,6 +262,7 @@ def launch_update(
 
 
 _router_support_cache: dict[tuple, bool] = {}
+ROUTER_MAX_TOKENS = 65535 * 64   # grid bound of the router kernels (include/moc_hip.h)
 
 
 def router_supported(z: torch.Tensor, router: torch.Tensor) -> bool:
@@ -261,8 +279,9 @@ def _router_shape_supported(z: torch.Tensor, K: int, Z: int) -> bool:
     if z.shape[-1] != Z or z.numel() == 0:
         return False
     N = z.numel() // Z
-    # the answer depends on N only through the 2^31-byte buffer bound
-    key = (Z, K, N * Z * 2 < (1 << 31))
+    # the answer depends on N only through the 2^31-byte buffer bound and the
+    # grid bound of the kernels (N <= 65535 * 64)
+    key = (Z, K, N * Z * 2 < (1 << 31), N <= ROUTER_MAX_TOKENS)
     hit = _router_support_cache.get(key)
     if hit is None:
         hit = bool(_lib.lib().moc_router_supported(N, Z, K, _lib.DT_BF16))
@@ -354,9 +373,9 @@ def router_backward(z: torch.Tensor, router: torch.Tensor, dlogits: torch.Tensor
     N = z.numel() // Z
     dz = torch.empty_like(z) if need_z else None
     dr = torch.empty_like(r) if need_router else None
-    nbytes = L.moc_router_backward_workspace_bytes(N, Z, K, _lib.DT_BF16) if need_router else 0
-    ws = _workspace(nbytes, z.device)
     with _lib.device_guard(z.device):
+        nbytes = L.moc_router_backward_workspace_bytes(N, Z, K, _lib.DT_BF16) if need_router else 0
+        ws = _workspace(nbytes, z.device)
         rc = L.moc_router_backward(
             z.data_ptr(), r.data_ptr(), dl.data_ptr(),
             None if dz is None else dz.data_ptr(), None if dr is None else dr.data_ptr(),

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.EXPORTED_SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.moc_abi_version() == 1
+    assert L.moc_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_header_constants_match_binding():
@@ -87,12 +87,16 @@ def test_status_maps_to_runtime_error():
 
 def test_backward_and_update_reject_bad_arguments():
     L = _lib.lib()
-    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, None, None, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, 16, None, None, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
                         1, 1, 1, 0, 0, FAKE, 1 << 30, None)
     assert rc == -1 and b"null" in L.moc_last_error()
-    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, 16, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
                         1, 1, 1, 0, 0, FAKE, 8, None)
     assert rc == -3
+    # dy rows are dim (contiguous) or 0 (one broadcast row) elements apart
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, 7, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+                        1, 1, 1, 0, 0, FAKE, 1 << 30, None)
+    assert rc == -1 and b"dy_row_stride" in L.moc_last_error()
     rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 70000, 16, 4, 4, 1, 1, 1, 0, 0, None)
     assert rc == -1
     rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 2, 16, 4, 4, 1, 9, 1, 0, 0, None)
@@ -130,3 +134,16 @@ def test_router_grouped_rejects_bad_groups():
     assert call([16], [1], outs=[FAKE + 2]) == -1   # misaligned output
     assert call([16], [1], Z=48) == -1              # z_dim % 64 != 0
     assert b"group" in L.moc_last_error() or b"z_dim" in L.moc_last_error()
+
+
+def test_kernel_path_switch():
+    """moc_set_kernel_path returns the previous family and rejects unknown ones;
+    the workspace size follows the family (generic kernels: fp32 scratch)."""
+    L = _lib.lib()
+    auto = L.moc_backward_workspace_bytes(4096, 256, 16, 4, _lib.DT_BF16, 1)
+    assert L.moc_set_kernel_path(7) == -1 and b"kernel path" in L.moc_last_error()
+    with _lib.kernel_path(_lib.PATH_GENERIC):
+        assert L.moc_set_kernel_path(_lib.PATH_GENERIC) == _lib.PATH_GENERIC
+        generic = L.moc_backward_workspace_bytes(4096, 256, 16, 4, _lib.DT_BF16, 1)
+    assert L.moc_set_kernel_path(_lib.PATH_AUTO) == _lib.PATH_AUTO
+    assert generic != auto and generic >= 4096 * 256 * 4

@@ -3,19 +3,18 @@
 At these sizes the oracle (oracle/moc_oracle.py, plain torch) runs in fp32 on
 the GPU itself; it is the same restatement the CPU tests pin.  Every HIP result
 is also compared with the other kernel family (MFMA vs generic VALU kernels,
-selected with MOC_HIP_PATH), and the decode loop is checked against the full
+selected with moc_set_kernel_path), and the decode loop is checked against the full
 forward with the cache compared bit for bit.  Tolerances: tests/_parity.py.
 """
 from __future__ import annotations
 
 import itertools
-import os
 
 import pytest
 import torch
 
 import moc
-from moc import MoC, moc_triton
+from moc import MoC, _lib, moc_triton
 from oracle import moc_oracle as O
 from tests._parity import assert_close, gen, randn, ulp_allowance
 
@@ -80,15 +79,11 @@ def _hip_layer(m, x, z, dy, **kw):
 
 
 def _with_path(path, fn):
-    old = os.environ.get("MOC_HIP_PATH")
-    os.environ["MOC_HIP_PATH"] = path
-    try:
+    """fn() on the generic kernels (path "generic") through the library's
+    kernel-family switch."""
+    assert path == "generic"
+    with _lib.kernel_path(_lib.PATH_GENERIC):
         return fn()
-    finally:
-        if old is None:
-            del os.environ["MOC_HIP_PATH"]
-        else:
-            os.environ["MOC_HIP_PATH"] = old
 
 
 NAMES = ("y", "dx", "dz", "drouter", "dbasis")
@@ -144,18 +139,40 @@ def test_config3_varlen_layer():
 
 
 def test_config5_qkv_triple():
-    """q/k/v MoC layers routed by one x_norm, K32 S8, fan-in init,
-    exp for q/k and softmax for v; loss = sum of the three outputs."""
-    B, T, Dm = 2, 2048, 4096  # T reduced from 8192 to bound the fp32 oracle's memory
+    """configs[4] at its stated size: q / k / v MoC layers (4096 / 1024 / 1024
+    channels) routed by one x_norm [2, 8192, 4096] through MoCGroup (the path
+    bench.py --config 5 times), K32 S8, fan-in init, exp routing for q and k,
+    softmax for v, no SiLU, loss = sum of the three y.sum().  Each layer's y,
+    dx, drouter and dbasis against the fp32 oracle layer; dz (one router
+    backward over the three layers' logits gradients) against the sum of the
+    three oracle router gradients."""
+    B, T, Dm = 2, 8192, 4096
+    specs = ((4096, "exp"), (1024, "exp"), (1024, "softmax"))
     g = gen(7)
     xn = randn(g, B, T, Dm).to(DEV, torch.bfloat16)
-    for dim, route in ((4096, "exp"), (1024, "exp"), (1024, "softmax")):
+    layers, vs = [], []
+    for dim, route in specs:
         m, g2 = _layer(dim, Dm, 32, 8, None, route, None, torch.bfloat16, seed=dim)
-        v = randn(g2, B, T, dim).to(DEV, torch.bfloat16)
-        dy = torch.ones_like(v)
-        got = _hip_layer(m, v, xn, dy)
-        ref = _oracle_layer(m, v, xn, dy, route, None)
-        _check_layer(f"({dim}, {route})", m, got, ref, torch.bfloat16)
+        layers.append(m)
+        vs.append(randn(g2, B, T, dim).to(DEV, torch.bfloat16))
+    grp = moc.MoCGroup(*layers)
+    assert grp._grouped(vs, xn, None)
+    xs = [v.detach().requires_grad_() for v in vs]
+    z = xn.detach().requires_grad_()
+    outs = grp(xs, z)
+    sum(y.sum() for y, _ in outs).backward()
+    dz_ref = torch.zeros(B, T, Dm, device=DEV)
+    extra = torch.zeros(B, T, Dm, device=DEV)
+    for m, v, xg, (y, _), (dim, route) in zip(layers, vs, xs, outs, specs):
+        ref = _oracle_layer(m, v, xn, torch.ones_like(v), route, None)
+        got = (y.detach(), xg.grad, None, m.router.grad, m.conv_bases.grad)
+        for n, a, b in zip(NAMES, got, ref):
+            if n != "dz":
+                assert_close(f"{n} ({dim}, {route})", a, b, torch.bfloat16)
+        dz_ref += ref[2]
+        extra += ulp_allowance(_oracle_layer.last_dlogits, m.router)
+        del ref
+    assert_close("dz (group)", z.grad, dz_ref, torch.bfloat16, extra=extra)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -271,26 +288,32 @@ def alpha_pad(alpha, S):
 
 
 def test_config4_decode():
-    """prefill a 1024-token prompt, then single-token steps; y against the
-    full forward (rows subsampled), cache bit-exact."""
-    B, D, Z, K, S, P, steps = 256, 2048, 2048, 16, 4, 1024, 64
-    m, g = _layer(D, Z, K, S, "silu", "softmax", None, torch.bfloat16)
-    x = randn(g, B, P + steps, D).to(DEV, torch.bfloat16)
-    z = randn(g, B, P + steps, Z).to(DEV, torch.bfloat16)
+    """configs[3] at its stated size: a batch-256 layer (D 2048, z_dim 2048, K16,
+    S4, softmax, SiLU) prefilled from a 1024-token prompt, then 512 single-token
+    steps; every step's y on every batch row against the fp32 oracle forward
+    over all 1536 tokens, the final cache bit-exact (the last S inputs)."""
+    B, D, Z, K, S, P, steps = 256, 2048, 2048, 16, 4, 1024, 512
+    m, _ = _layer(D, Z, K, S, "silu", "softmax", None, torch.bfloat16)
+    gd = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(B, P + steps, D, generator=gd, device=DEV).to(torch.bfloat16)
+    z = torch.randn(B, P + steps, Z, generator=gd, device=DEV).to(torch.bfloat16)
+    y_steps = torch.empty(B, steps, D, device=DEV, dtype=torch.bfloat16)
     with torch.no_grad():
         _, cache = m(x[:, :P], z[:, :P], output_final_state=True)
-        outs = []
-        for t in range(P, P + steps):
-            y, cache = m.step(x[:, t:t + 1], z[:, t:t + 1], cache=cache, output_final_state=True)
-            outs.append(y)
-        y_steps = torch.cat(outs, 1)
+        for i, t in enumerate(range(P, P + steps)):
+            y, c2 = m.step(x[:, t:t + 1], z[:, t:t + 1], cache=cache, output_final_state=True)
+            assert c2 is cache
+            y_steps[:, i:i + 1] = y
     assert torch.equal(cache, x[:, -S:].transpose(1, 2))
-    rows = torch.arange(0, B, 37, device=DEV)
-    with torch.no_grad():
-        logits = moc.router_linear(z[rows], m.router)
-        alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
-        full = O.moc_ref(x[rows].float(), alpha, m.conv_bases.float(), "silu")
-    assert_close("decode y", y_steps[rows], full[:, P:], torch.bfloat16)
+    basis = m.conv_bases.detach().float()
+    for r0 in range(0, B, 64):   # the oracle in row blocks (its W is [rows, T, D, S] fp32)
+        rows = slice(r0, r0 + 64)
+        with torch.no_grad():
+            logits = moc.router_linear(z[rows], m.router)
+            alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
+            full = O.moc_ref(x[rows].float(), alpha, basis, "silu")
+        assert_close(f"decode y rows {r0}..{r0 + 63}", y_steps[rows], full[:, P:], torch.bfloat16)
+        del full, alpha, logits
 
 
 def test_module_step_graph_capture():

@@ -178,22 +178,35 @@ def test_module_routed_fwd_bwd(route, act, dtype):
 
 
 @pytest.mark.parametrize("T1,T2", [(10, 7), (2, 9), (3, 2)])
-def test_prefill_from_cache_and_final_state(T1, T2):
-    dtype, S, act = torch.bfloat16, 4, "silu"
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_prefill_from_cache_and_final_state(T1, T2, dtype):
+    """Prefill continuing from a cache (moc/api.py:299-309): y, the final states
+    and the gradients of x, alpha, basis and the cache against autograd of the
+    oracle's formulation (moc_prefill_ref: the cache prepended to x, zero
+    weights prepended to alpha, the first S outputs dropped)."""
+    S, act = 4, "silu"
     g, x, a, dy, *_ = _verify_inputs()
     b = randn(g, K, S, D, scale=0.1).to(DEV, dtype)
     kx = x[:, :T1 + T2].to(DEV, dtype)
     ka = a[:, :T1 + T2].to(DEV, dtype)
     y1, st1 = moc_triton(kx[:, :T1], ka[:, :T1], b, output_final_state=True, activation=act)
     assert torch.equal(st1, O.final_state(kx[:, :T1], None, S))
-    x2 = kx[:, T1:].clone().requires_grad_()
-    y2, st2 = moc_triton(x2, ka[:, T1:], b, cache=st1, output_final_state=True, activation=act)
+    x2, a2, b2, c2 = (t.clone().requires_grad_() for t in (kx[:, T1:], ka[:, T1:], b, st1))
+    y2, st2 = moc_triton(x2, a2, b2, cache=c2, output_final_state=True, activation=act)
     assert torch.equal(st2, O.final_state(kx, None, S))
+    dy2 = dy[:, :T2].to(DEV, dtype)
+    y2.backward(dy2)
     ref = O.moc_ref(kx.float().cpu(), ka.float().cpu(), b.float().cpu(), act)
     assert_close("prefill y", y2, ref[:, T1:], dtype)
     assert_close("first y", y1, ref[:, :T1], dtype)
-    y2.sum().backward()
-    assert x2.grad is not None and torch.isfinite(x2.grad.float()).all()
+    rx, ra, rb, rc = (t.detach().float().cpu().requires_grad_() for t in (x2, a2, b2, c2))
+    ry = O.moc_prefill_ref(rx, ra, rb, rc, act)
+    ry.backward(dy2.float().cpu())
+    assert_close("prefill y (oracle prefill)", y2, ry, dtype)
+    assert_close("prefill dx", x2.grad, rx.grad, dtype)
+    assert_close("prefill dalpha", a2.grad, ra.grad, dtype)
+    assert_close("prefill dbasis", b2.grad, rb.grad, dtype)
+    assert_close("prefill dcache", c2.grad, rc.grad, dtype)
 
 
 def test_need_x_false_and_alpha_only_grads():
@@ -345,6 +358,98 @@ def test_module_varlen_routed():
     assert_close("dx", x.grad, rx.grad, torch.float32)
     assert_close("dz", z.grad, rz.grad, torch.float32)
     assert_close("drouter", m.router.grad, rr.grad, torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_varlen_with_cu_seqlens_cpu_and_chunk_indices(dtype):
+    """Valid packed calls that pass cu_seqlens_cpu or chunk_indices
+    (moc/api.py:117-128): checked as the reference checks them, then the same
+    results as the call without them (bit for bit) and as the oracle."""
+    from moc import ops
+    g, _, _, _, xv, av, dyv = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1).to(DEV, dtype)
+    cu = _cu(VARLEN_LENGTHS).to(DEV)
+    extra = [dict(), dict(cu_seqlens_cpu=cu.cpu()),
+             dict(chunk_indices=ops.prepare_chunk_indices(cu)),
+             dict(cu_seqlens_cpu=cu.cpu().long(), chunk_indices=ops.prepare_chunk_indices(cu, 64, cu.cpu()))]
+    outs = []
+    for kw in extra:
+        kx = xv.to(DEV, dtype).requires_grad_()
+        ka = av.to(DEV, dtype).requires_grad_()
+        kb = b.clone().requires_grad_()
+        y, _ = moc_triton(kx, ka, kb, cu_seqlens=cu, max_seqlen=max(VARLEN_LENGTHS),
+                          activation="silu", **kw)
+        y.backward(dyv.to(DEV, dtype))
+        outs.append((y.detach(), kx.grad, ka.grad, kb.grad))
+    for other in outs[1:]:
+        for u, v in zip(outs[0], other):
+            assert torch.equal(u, v)
+    rx, ra, rb = O.reference_inputs(xv.to(dtype), av.to(dtype), b, dtype)
+    ref = O.moc_varlen_grads_ref(rx, ra, rb, cu.cpu(), dyv.to(dtype).float(), "silu")
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), outs[0], ref):
+        assert_close(n, u, r, dtype)
+
+
+def test_module_varlen_with_cu_seqlens_cpu_and_chunk_indices():
+    """The bf16 module on the router kernels (one autograd node) with
+    cu_seqlens_cpu / chunk_indices: the same results as without them."""
+    from moc import ops
+    torch.manual_seed(0)
+    Z = 64
+    m = MoC(D, Z, 4, 16, activation="silu", init_std=0.1)
+    g = gen(17)
+    with torch.no_grad():
+        m.router.copy_(randn(g, 16, Z, scale=0.1))
+    m = m.to(DEV, torch.bfloat16)
+    cu = _cu(VARLEN_LENGTHS).to(DEV)
+    N = sum(VARLEN_LENGTHS)
+    x = randn(g, 1, N, D).to(DEV, torch.bfloat16)
+    z = randn(g, 1, N, Z).to(DEV, torch.bfloat16)
+    outs = []
+    for kw in (dict(), dict(cu_seqlens_cpu=cu.cpu()), dict(chunk_indices=ops.prepare_chunk_indices(cu))):
+        m.zero_grad(set_to_none=True)
+        xi, zi = x.clone().requires_grad_(), z.clone().requires_grad_()
+        y, st = m(xi, zi, cu_seqlens=cu, max_seqlen=max(VARLEN_LENGTHS), **kw)
+        assert st is None and y.shape == x.shape
+        y.float().square().sum().backward()
+        outs.append((y.detach(), xi.grad, zi.grad, m.router.grad, m.conv_bases.grad))
+    for other in outs[1:]:
+        for u, v in zip(outs[0], other):
+            assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("varlen", [False, True])
+def test_broadcast_dy_matches_materialised(dtype, varlen):
+    """The gradient of y.sum() reaches the backward as one row broadcast over
+    every token (stride 0); the kernels read that row in place (row stride 0)
+    instead of a copied [n_tokens, D] tensor.  dx, dalpha and dbasis equal those
+    from the materialised ones tensor bit for bit, and the oracle's."""
+    g, x, a, _, xv, av, _ = _verify_inputs()
+    b = randn(g, K, 4, D, scale=0.1).to(DEV, dtype)
+    xs, as_ = (xv, av) if varlen else (x, a)
+    kw = dict(cu_seqlens=_cu(VARLEN_LENGTHS).to(DEV), max_seqlen=31) if varlen else {}
+
+    def run(broadcast):
+        kx = xs.to(DEV, dtype).requires_grad_()
+        ka = as_.to(DEV, dtype).requires_grad_()
+        kb = b.clone().requires_grad_()
+        y, _ = moc_triton(kx, ka, kb, activation="silu", **kw)
+        if broadcast:
+            y.sum().backward()
+        else:
+            y.backward(torch.ones_like(y))
+        return kx.grad, ka.grad, kb.grad
+
+    got, mat = run(True), run(False)
+    for n, u, v in zip(("dx", "dalpha", "dbasis"), got, mat):
+        assert torch.equal(u, v), n
+    rx, ra, rb = O.reference_inputs(xs.to(dtype), as_.to(dtype), b, dtype)
+    ones = torch.ones(xs.shape)
+    ref = (O.moc_varlen_grads_ref(rx, ra, rb, kw["cu_seqlens"].cpu(), ones, "silu") if varlen
+           else O.moc_grads_ref(rx, ra, rb, ones, "silu"))
+    for n, u, r in zip(("dx", "dalpha", "dbasis"), got, ref[1:]):
+        assert_close(n, u, r, dtype)
 
 
 def test_moc_triton_name_is_hip_path():
