@@ -141,6 +141,27 @@ int moc_backward(const void* x, const void* alpha, const void* basis, const void
                  int activation, int routing,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * moc_backward without a workspace argument; it has no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops and harnesses that forbid hipMalloc): the
+ * scratch (dalpha / dbasis partial sums, prepared operands) is a device array
+ * of MOC_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held from the
+ * first call on that GPU until the process ends.  Same arguments, results and
+ * kernels as moc_backward.  A problem whose moc_backward_workspace_bytes exceed
+ * MOC_NOALLOC_SCRATCH_BYTES is rejected with MOC_ERR_WORKSPACE.  Every call on
+ * a GPU shares that GPU's scratch: calls that overlap on one GPU (different
+ * streams, or host threads without ordering) race and must not be made.
+ * The call itself performs no allocation.
+ */
+#define MOC_NOALLOC_SCRATCH_BYTES (64u << 20)
+int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, const void* dy,
+                         int64_t dy_row_stride, void* dx, void* dalpha, void* dbasis,
+                         const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                         int64_t n_tokens, int64_t seq_len,
+                         int64_t dim, int64_t k, int64_t kernel_size,
+                         int x_dtype, int alpha_dtype, int basis_dtype,
+                         int activation, int routing, void* stream);
 
 /*
  * One decode step, in place.  Replaces launch_update (moc/ops.py:341-362) and

@@ -5,6 +5,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/moc_hip.h"
 #include "moc_kernels.h"
@@ -250,6 +251,38 @@ int backward_launch(const moc::Problem& p, const void* x, const void* alpha, con
   return hip_status("moc_backward launch");
 }
 
+// Device scratch of moc_backward_noalloc: part of this library's code object,
+// so each GPU the library runs on holds one copy from its first use until the
+// process ends.  Host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns (the name itself is a host-side stand-in).
+static __device__ __align__(256) unsigned char scratch[MOC_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (looked up once per device).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MOC_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MOC_ERR_ARG, "device index %d out of range", dev);
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || ptr == nullptr)
+        return fail(MOC_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                    hipGetErrorString(e));
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return MOC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -274,6 +307,29 @@ int moc_backward(const void* x, const void* alpha, const void* basis, const void
                          static_cast<hipStream_t>(stream));
 }
 
+int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, const void* dy,
+                         int64_t dy_row_stride, void* dx, void* dalpha, void* dbasis,
+                         const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                         int64_t n_tokens, int64_t seq_len, int64_t dim, int64_t k,
+                         int64_t kernel_size, int x_dtype, int alpha_dtype, int basis_dtype,
+                         int activation, int routing, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem p;
+  int rc = backward_problem(x, alpha, basis, dy, dy_row_stride, dalpha, dbasis, cu_seqlens,
+                            cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k, kernel_size,
+                            x_dtype, alpha_dtype, basis_dtype, activation, routing, p);
+  if (rc != MOC_OK) return rc;
+  const size_t need = backward_bytes(p);
+  if (need > MOC_NOALLOC_SCRATCH_BYTES)
+    return fail(MOC_ERR_WORKSPACE,
+                "problem needs %zu bytes of scratch; moc_backward_noalloc holds %zu "
+                "(call moc_backward with a workspace instead)",
+                need, static_cast<size_t>(MOC_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws)) != MOC_OK) return rc;
+  return backward_launch(p, x, alpha, basis, dy, dx, dalpha, dbasis, ws,
+                         static_cast<hipStream_t>(stream));
+}
 
 
 int moc_update(const void* x, const void* alpha, const void* basis, void* cache,

@@ -21,6 +21,8 @@ ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
 ROUTE_SOFTMAX_WEIGHTS, ROUTE_EXP_WEIGHTS = 3, 4
 # kernel families (moc_set_kernel_path)
 PATH_AUTO, PATH_GENERIC, PATH_MFMA_PREP = 0, 1, 2
+# device scratch of moc_backward_noalloc
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _DTYPE_CODES = {torch.float32: DT_F32, torch.bfloat16: DT_BF16, torch.float16: DT_F16}
 
@@ -32,6 +34,7 @@ EXPORTED_SYMBOLS = (
     "moc_forward",
     "moc_backward_workspace_bytes",
     "moc_backward",
+    "moc_backward_noalloc",
     "moc_update",
     "moc_profile_events",
     "moc_decode_step_supported",
@@ -83,6 +86,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     ]
     lib.moc_backward.argtypes = bwd + [_p, _z, _p]   # workspace, bytes, stream
     lib.moc_backward.restype = _i
+    lib.moc_backward_noalloc.argtypes = bwd + [_p]   # stream
+    lib.moc_backward_noalloc.restype = _i
     lib.moc_set_kernel_path.argtypes = [_i]
     lib.moc_set_kernel_path.restype = _i
     lib.moc_update.argtypes = [

@@ -147,3 +147,19 @@ def test_kernel_path_switch():
         generic = L.moc_backward_workspace_bytes(4096, 256, 16, 4, _lib.DT_BF16, 1)
     assert L.moc_set_kernel_path(_lib.PATH_AUTO) == _lib.PATH_AUTO
     assert generic != auto and generic >= 4096 * 256 * 4
+
+
+def test_backward_noalloc_rejects_before_touching_the_device():
+    """The no-allocation backward validates like moc_backward and rejects a
+    problem whose workspace exceeds its device scratch, before any device call."""
+    L = _lib.lib()
+    args = [FAKE, FAKE, FAKE, FAKE, 2048, FAKE, FAKE, FAKE, None, 0, 0]
+    rc = L.moc_backward_noalloc(*args, 8, 8, 2048, 4, 4, 9, 1, 1, 0, 0, None)
+    assert rc == -2 and b"x dtype" in L.moc_last_error()
+    big = 1 << 20   # 1 M tokens x 2048 channels: partial sums far above the scratch
+    need = L.moc_backward_workspace_bytes(big, 2048, 16, 4, _lib.DT_BF16, 3)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    rc = L.moc_backward_noalloc(*args, big, 4096, 2048, 16, 4, 1, 1, 1, 1, 3, None)
+    assert rc == -3 and b"moc_backward_noalloc holds" in L.moc_last_error()
+    small = L.moc_backward_workspace_bytes(16384, 2048, 16, 4, _lib.DT_BF16, 3)
+    assert small <= _lib.NOALLOC_SCRATCH_BYTES    # the headline shape fits
