@@ -220,22 +220,63 @@ def bench_entries(dev, steps, warmup, rotate=ROTATE):
 
 
 def counter_run(dev, which, reps=3):
-    """A short program for hardware-counter passes (rocprofv3 --pmc): `reps`
-    calls of one entry at the headline config, or of a bf16 copy of 128 MiB
-    (`copy`), the kernel of known traffic that calibrates FETCH_SIZE and
-    WRITE_SIZE."""
+    """A short program for profiler passes (rocprofv3 --pmc or --kernel-trace):
+    `reps` calls, after two untimed ones, of
+      fwd / bwd  one C-ABI entry at the headline config (entry_calls);
+      step       the headline layer step (bench_layer's step, inputs rotated);
+      decode     the one-launch decode step of configs[3] (batch 256);
+      c5         the configs[4] QKV triple step through MoCGroup;
+      copy       a bf16 copy of 128 MiB, the kernel of known traffic that
+                 calibrates FETCH_SIZE and WRITE_SIZE."""
     if which == "copy":
         a = torch.randn(64 * 1024 * 1024, device=dev).bfloat16()
         b = torch.empty_like(a)
         fn = lambda: b.copy_(a)  # noqa: E731
-    else:
+    elif which in ("fwd", "bwd"):
         fwd, bwd = entry_calls(dev, 1)
         fn = fwd if which == "fwd" else bwd
+    elif which == "step":
+        m, sets = build_layer(dev, n_sets=ROTATE)
+        cyc = _Cycle(sets)
+
+        def fn():
+            x, z = cyc.next()
+            m.zero_grad(set_to_none=True)
+            x.grad = None
+            z.grad = None
+            y, _ = m(x, z)
+            y.sum().backward()
+    elif which == "decode":
+        fn = decode_step_call(dev)
+    else:
+        fn = config5_step(dev)[0](True)
+    for _ in range(2):
+        fn()
     torch.cuda.synchronize()
     for _ in range(reps):
         fn()
     torch.cuda.synchronize()
     print(f"counter run: {reps} x {which}", flush=True)
+
+
+def decode_step_call(dev):
+    """One launch of the decode step MoC.step runs at configs[3] (batch 256,
+    D 2048, z_dim 2048, K 16, S 4, softmax, SiLU) on a scratch cache."""
+    import moc
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX
+    c = DECODE
+    g = torch.Generator().manual_seed(0)
+    m = moc.MoC(c["D"], c["Z"], c["S"], c["K"], activation="silu")
+    with torch.no_grad():
+        m.router.copy_(torch.randn(c["K"], c["Z"], generator=g) * 0.02)
+    m = m.to(dev, torch.bfloat16)
+    xt = torch.randn(c["B"], c["D"], generator=g).to(dev, torch.bfloat16)
+    zt = torch.randn(c["B"], c["Z"], generator=g).to(dev, torch.bfloat16)
+    cache = torch.randn(c["B"], c["D"], c["S"], generator=g).to(dev, torch.bfloat16)
+    basis, router = m.conv_bases.detach(), m.router.detach()
+    return lambda: ops.launch_decode_step(xt, zt, router, basis, cache, activation_flag=1,
+                                          routing=ROUTE_SOFTMAX)
 
 
 def bench_decode(dev):
@@ -397,11 +438,12 @@ def bench_config3(dev, steps, warmup):
                        "z_dim": Z, "K": K, "S": S, "routing": "exp", "activation": None}}
 
 
-def bench_config5(dev, steps, warmup):
-    """the QKV triple, three MoC layers (q 4096, k 1024, v 1024
-    channels) on one routing input x_norm [2, 8192, 4096], K=32, S=8, bf16, exp
-    routing for q and k, softmax for v, no SiLU, fan-in init, loss = sum of the
-    three y.sum(); the layers called one by one and as one MoCGroup."""
+def config5_step(dev):
+    """(step(grouped) -> callable, B, T, Dm): the configs[4] QKV triple step,
+    three MoC layers (q 4096, k 1024, v 1024 channels) on one routing input
+    x_norm [2, 8192, 4096], K=32, S=8, bf16, exp routing for q and k, softmax
+    for v, no SiLU, fan-in init, loss = sum of the three y.sum(); the layers
+    called one by one (grouped False) or as one MoCGroup."""
     import moc
     g = torch.Generator().manual_seed(0)
     torch.manual_seed(0)
@@ -428,6 +470,13 @@ def bench_config5(dev, steps, warmup):
             sum(y.sum() for y, _ in outs).backward()
         return run
 
+    return step, B, T, Dm
+
+
+def bench_config5(dev, steps, warmup):
+    """the QKV triple step (config5_step), the layers one by one and
+    as one MoCGroup."""
+    step, B, T, Dm = config5_step(dev)
     ms_sep = time_region(step(False), steps, warmup)
     ms_grp = time_region(step(True), steps, warmup)
     return {"metric": "configs[4] QKV triple fwd+bwd Mtok/s (MoCGroup)",
@@ -452,9 +501,11 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE,
                     help="input sets the timed loops cycle through (1: one set reused, "
                          "which the last-level cache partly holds across steps)")
-    ap.add_argument("--counters", choices=("fwd", "bwd", "copy"), default=None,
-                    help="only run 3 calls of one entry (or the calibration copy) "
-                         "for a rocprofv3 --pmc pass; prints no JSON")
+    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c5", "copy"),
+                    default=None,
+                    help="only run --reps calls of one workload (see counter_run) for a "
+                         "rocprofv3 --pmc or --kernel-trace pass; prints no JSON")
+    ap.add_argument("--reps", type=int, default=3, help="calls of the --counters workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
@@ -465,7 +516,7 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     if args.counters:
-        counter_run(dev, args.counters)
+        counter_run(dev, args.counters, args.reps)
         return
     if args.config != 2:
         fn = bench_config3 if args.config == 3 else bench_config5

@@ -164,6 +164,55 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
                          int activation, int routing, void* stream);
 
 /*
+ * Several MoC layers on one token axis in one launch per pass: the q / k / v
+ * pattern of the reference README (README.md:80-129), three MoC.forward calls
+ * (moc/api.py:372-400) whose forward / backward launches each cover one layer.
+ * A MocLayer names one layer's tensors; the layers share cu_seqlens /
+ * n_tokens / seq_len, k, kernel_size, x_dtype and activation, and each has its
+ * own dim, routing and alpha / basis dtypes.  Fields are those of
+ * moc_forward (x, alpha, basis, y) and moc_backward (dy, dy_row_stride, dx or
+ * NULL, dalpha, dbasis); each entry uses its own.  When every layer is bf16 and
+ * on the matrix-core kernels, each pass (forward; backward stage 1; stage 2)
+ * is one launch over all layers' channels; otherwise the layers run one by
+ * one.  Results equal moc_forward / moc_backward per layer bit for bit.
+ * 1 <= n_layers <= 4.
+ */
+typedef struct MocLayer {
+  const void* x;
+  const void* alpha;
+  const void* basis;
+  void* y;
+  const void* dy;
+  int64_t dy_row_stride;
+  void* dx;
+  void* dalpha;
+  void* dbasis;
+  int64_t dim;
+  int routing;
+  int alpha_dtype;
+  int basis_dtype;
+} MocLayer;
+
+#define MOC_MAX_LAYERS 4
+
+size_t moc_forward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
+                                          int64_t k, int64_t kernel_size, int x_dtype,
+                                          int activation);
+int moc_forward_layers(const MocLayer* layers, int n_layers,
+                       const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                       int64_t n_tokens, int64_t seq_len, int64_t k, int64_t kernel_size,
+                       int x_dtype, int activation,
+                       void* workspace, size_t workspace_bytes, void* stream);
+size_t moc_backward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
+                                           int64_t k, int64_t kernel_size, int x_dtype,
+                                           int activation);
+int moc_backward_layers(const MocLayer* layers, int n_layers,
+                        const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
+                        int64_t n_tokens, int64_t seq_len, int64_t k, int64_t kernel_size,
+                        int x_dtype, int activation,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * One decode step, in place.  Replaces launch_update (moc/ops.py:341-362) and
  * _moc_update_kernel (moc/kernels.py:442-550).
  *   x     : [batch, dim] contiguous, x_dtype

@@ -332,6 +332,159 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
 }
 
 
+}  // extern "C"
+
+namespace {
+
+// Problems of a layer set (checked); n_layers in [1, MOC_MAX_LAYERS].
+int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu64,
+                   int64_t n_seqs, int64_t n_tokens, int64_t seq_len, int64_t k, int64_t ks,
+                   int x_dt, int activation, bool backward, moc::Problem* ps) {
+  if (n_layers < 1 || n_layers > MOC_MAX_LAYERS)
+    return fail(MOC_ERR_ARG, "n_layers must be in [1, %d], got %d", MOC_MAX_LAYERS, n_layers);
+  if (!layers) return fail(MOC_ERR_ARG, "null layer array");
+  int rc;
+  if ((rc = check_seq(cu, n_seqs, seq_len)) != MOC_OK) return rc;
+  for (int i = 0; i < n_layers; ++i) {
+    const MocLayer& l = layers[i];
+    if ((rc = check_dims(n_tokens, l.dim, k, ks)) != MOC_OK) return rc;
+    if ((rc = check_common(x_dt, l.alpha_dtype, l.basis_dtype, activation, l.routing)) != MOC_OK)
+      return rc;
+    ps[i] = make_problem(cu, cu64, n_seqs, n_tokens, seq_len, l.dim, k, ks, x_dt, l.alpha_dtype,
+                         l.basis_dtype, activation, l.routing);
+    if (backward) {
+      if (l.dy_row_stride != 0 && l.dy_row_stride != l.dim)
+        return fail(MOC_ERR_ARG, "layer %d: dy_row_stride must be dim (%lld) or 0, got %lld", i,
+                    (long long)l.dim, (long long)l.dy_row_stride);
+      ps[i].dy_stride = l.dy_row_stride;
+    }
+  }
+  if (backward && (n_tokens + 255) / 256 > 65535)
+    return fail(MOC_ERR_ARG, "n_tokens too large for the backward grid: %lld", (long long)n_tokens);
+  return MOC_OK;
+}
+
+bool grouped(const moc::Problem* ps, int n) {
+  for (int i = 0; i < n; ++i)
+    if (!use_mfma(ps[i])) return false;
+  return moc::mfma::layers_grouped(ps, n);
+}
+
+size_t layers_bytes(const moc::Problem* ps, int n, bool backward) {
+  if (grouped(ps, n))
+    return backward ? moc::mfma::backward_layers_workspace(ps, n)
+                    : moc::mfma::forward_layers_workspace(ps, n);
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) total += align_up(backward ? backward_bytes(ps[i]) : forward_bytes(ps[i]));
+  return total;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t moc_forward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
+                                          int64_t k, int64_t kernel_size, int x_dtype,
+                                          int activation) {
+  moc::Problem ps[MOC_MAX_LAYERS];
+  const char saved = g_err[0];
+  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, k, kernel_size, x_dtype,
+                     activation, false, ps) != MOC_OK) {
+    g_err[0] = saved;
+    return 0;
+  }
+  return layers_bytes(ps, n_layers, false);
+}
+
+size_t moc_backward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
+                                           int64_t k, int64_t kernel_size, int x_dtype,
+                                           int activation) {
+  moc::Problem ps[MOC_MAX_LAYERS];
+  const char saved = g_err[0];
+  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, k, kernel_size, x_dtype,
+                     activation, false, ps) != MOC_OK) {
+    g_err[0] = saved;
+    return 0;
+  }
+  return layers_bytes(ps, n_layers, true);
+}
+
+int moc_forward_layers(const MocLayer* layers, int n_layers, const void* cu_seqlens,
+                       int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens, int64_t seq_len,
+                       int64_t k, int64_t kernel_size, int x_dtype, int activation,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem ps[MOC_MAX_LAYERS];
+  int rc = layer_problems(layers, n_layers, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len,
+                          k, kernel_size, x_dtype, activation, false, ps);
+  if (rc != MOC_OK) return rc;
+  for (int i = 0; i < n_layers; ++i)
+    if (!layers[i].x || !layers[i].alpha || !layers[i].basis || !layers[i].y)
+      return fail(MOC_ERR_ARG, "layer %d: null tensor pointer", i);
+  const size_t need = layers_bytes(ps, n_layers, false);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if (grouped(ps, n_layers)) {
+    moc::mfma::LayerIO io[MOC_MAX_LAYERS] = {};
+    for (int i = 0; i < n_layers; ++i)
+      io[i] = moc::mfma::LayerIO{layers[i].x, layers[i].alpha, layers[i].basis, layers[i].y,
+                                 nullptr, nullptr, nullptr, nullptr};
+    moc::mfma::forward_layers(ps, io, n_layers, ws, st);
+    return hip_status("moc_forward_layers launch");
+  }
+  for (int i = 0; i < n_layers; ++i) {
+    const MocLayer& l = layers[i];
+    const size_t nb = align_up(forward_bytes(ps[i]));
+    rc = moc_forward(l.x, l.alpha, l.basis, l.y, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens,
+                     seq_len, l.dim, k, kernel_size, x_dtype, l.alpha_dtype, l.basis_dtype,
+                     activation, l.routing, nb ? ws : nullptr, nb, stream);
+    if (rc != MOC_OK) return rc;
+    ws += nb;
+  }
+  return MOC_OK;
+}
+
+int moc_backward_layers(const MocLayer* layers, int n_layers, const void* cu_seqlens,
+                        int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens, int64_t seq_len,
+                        int64_t k, int64_t kernel_size, int x_dtype, int activation,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem ps[MOC_MAX_LAYERS];
+  int rc = layer_problems(layers, n_layers, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len,
+                          k, kernel_size, x_dtype, activation, true, ps);
+  if (rc != MOC_OK) return rc;
+  for (int i = 0; i < n_layers; ++i) {
+    const MocLayer& l = layers[i];
+    if (!l.x || !l.alpha || !l.basis || !l.dy || !l.dalpha || !l.dbasis)
+      return fail(MOC_ERR_ARG, "layer %d: null tensor pointer", i);
+  }
+  const size_t need = layers_bytes(ps, n_layers, true);
+  if (workspace_bytes < need || !workspace)
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if (grouped(ps, n_layers)) {
+    moc::mfma::LayerIO io[MOC_MAX_LAYERS] = {};
+    for (int i = 0; i < n_layers; ++i)
+      io[i] = moc::mfma::LayerIO{layers[i].x, layers[i].alpha, layers[i].basis, nullptr,
+                                 layers[i].dy, layers[i].dx, layers[i].dalpha, layers[i].dbasis};
+    moc::mfma::backward_layers(ps, io, n_layers, ws, st);
+    return hip_status("moc_backward_layers launch");
+  }
+  for (int i = 0; i < n_layers; ++i) {
+    const size_t nb = align_up(backward_bytes(ps[i]));
+    rc = backward_launch(ps[i], layers[i].x, layers[i].alpha, layers[i].basis, layers[i].dy,
+                         layers[i].dx, layers[i].dalpha, layers[i].dbasis, ws, st);
+    if (rc != MOC_OK) return rc;
+    ws += nb;
+  }
+  return MOC_OK;
+}
+
 int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
                int64_t cache_stride_b, int64_t cache_stride_d, int64_t cache_stride_s, void* y,
                int64_t batch, int64_t dim, int64_t k, int64_t kernel_size, int x_dtype,

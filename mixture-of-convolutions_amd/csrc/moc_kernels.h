@@ -58,6 +58,26 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
 void backward(const Problem& p, const void* x, const void* alpha, const void* basis,
               const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
               hipStream_t st);
+
+// Grouped layers: layer i is problem ps[i] (one token axis; K, S, activation
+// shared) on tensors io[i]; layers_grouped tells whether they can run as one
+// launch per pass (bf16, at most 4 layers).
+struct LayerIO {
+  const void* x;
+  const void* alpha;
+  const void* basis;
+  void* y;        // forward
+  const void* dy; // backward (rows ps[i].dy_stride apart)
+  void* dx;
+  void* dalpha;
+  void* dbasis;
+};
+bool layers_grouped(const Problem* ps, int n);
+size_t forward_layers_workspace(const Problem* ps, int n);
+size_t backward_layers_workspace(const Problem* ps, int n);
+void forward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace, hipStream_t st);
+void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace,
+                     hipStream_t st);
 }  // namespace mfma
 
 // decode step on the matrix cores (moc_decode.hip): bf16 x, logits / weights

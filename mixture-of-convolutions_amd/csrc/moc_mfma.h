@@ -209,15 +209,71 @@ __device__ __forceinline__ void tap_bits_rows(const SeqLayout& seq, int64_t row0
 }
 
 // ---------------------------------------------------------------------------
+// Layer tables of a grouped launch.  The MoC layers of one launch share the
+// token axis (sequence layout), K, S, activation and compute dtype; each has its
+// own tensors, channel count and the grid its own launch would use, and the
+// launch is the concatenation of those grids: layer i owns the 1-D block ids
+// [blk0, blk0 + its block count), mapped onto its grid as its own launch maps
+// them (x fastest).  So each workgroup does exactly the work it does in the
+// layer's own launch, and results equal those launches bit for bit.  A
+// workgroup finds its layer with uniform selects (the table stays in scalar
+// registers).
+constexpr int kMaxLayers = 4;
+
+struct FwdLayer {
+  const void* x;
+  const void* a;   // routing operands [n_tokens, KP] in the compute dtype
+  const void* b;   // basis operands [KP, S, D] in the compute dtype
+  void* y;
+  int64_t D;
+  int gx, n_sb, blk0;
+};
+struct FwdLayers {
+  int n;
+  FwdLayer l[kMaxLayers];
+};
+
+struct BwdLayer {
+  const void* x;
+  const void* dy;
+  int64_t dys;     // dy row stride (elements): D, or 0 for one broadcast row
+  const void* a;
+  const void* b;
+  void* dx;
+  float* part_da;  // [gx, n_tokens, KP]
+  float* part_db;  // [gy, KP, S, D]
+  int64_t D;
+  int gx, gy, gy1, n_old, n_total, blk0;
+};
+struct BwdLayers {
+  int n;
+  BwdLayer l[kMaxLayers];
+};
+
+// Index of the layer owning 1-D block id blk of a grouped launch (uniform; the
+// kernels then read that layer's fields from the kernel-argument table, where
+// the compiler can reload them instead of keeping copies live).
+template <typename LT>
+__device__ __forceinline__ int layer_index(const LT& ly, int blk) {
+  int li = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxLayers; ++i)
+    if (i < ly.n && blk >= ly.l[i].blk0) li = i;
+  return __builtin_amdgcn_readfirstlane(li);
+}
+
+// ---------------------------------------------------------------------------
 // Forward.  Grid: x = channel groups of 4 waves (4 * CW channels), y = token
 // ranges of n_sb super-blocks.  No LDS, no barriers: every wave walks its
 // super-blocks on its own, loading the rows of super-block i+1 (x window and
-// routing weights, raw) before it computes super-block i.
+// routing weights, raw) before it computes super-block i.  fwd_tile is the
+// work of workgroup (bx, by) of one layer.
 template <int S, int KC, int NB, int NC, bool ACT, bool BF>
-__global__ void __launch_bounds__(256)
-fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict__ a_c,
-           const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ yv, SeqLayout seq,
-           int64_t D, int n_sb) {
+__device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
+                                         const typename CT<BF>::elem* __restrict__ a_c,
+                                         const typename CT<BF>::elem* __restrict__ b_c,
+                                         void* __restrict__ yv, SeqLayout seq, int64_t D, int n_sb,
+                                         int bx, int by) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -227,13 +283,13 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
   const int64_t N = seq.n_tokens;
-  const int64_t d0 = (static_cast<int64_t>(blockIdx.x) * 4 + wave) * CW;
+  const int64_t d0 = (static_cast<int64_t>(bx) * 4 + wave) * CW;
   if (d0 >= D) return;  // whole wave past the channel axis; no barriers below
   const int64_t dl = d0 + NC * j;
   const bool ch_ok = dl < D;
 
   constexpr int ESZ = static_cast<int>(sizeof(E));
-  const int64_t tbase = static_cast<int64_t>(blockIdx.y) * n_sb * TB;
+  const int64_t tbase = static_cast<int64_t>(by) * n_sb * TB;
   // buffers over the rows this wave touches: x / y rows [row_lo, row_hi), alpha rows [tbase, row_hi)
   const int64_t row_lo = (tbase - (S - 1) > 0) ? tbase - (S - 1) : 0;
   const int64_t row_hi = (tbase + static_cast<int64_t>(n_sb) * TB < N) ? tbase + static_cast<int64_t>(n_sb) * TB : N;
@@ -348,6 +404,33 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
     if (interior) body(std::false_type{});
     else body(std::true_type{});
   }
+}
+
+template <int S, int KC, int NB, int NC, bool ACT, bool BF>
+__global__ void __launch_bounds__(256)
+fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict__ a_c,
+           const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ yv, SeqLayout seq,
+           int64_t D, int n_sb) {
+  fwd_tile<S, KC, NB, NC, ACT, BF>(xv, a_c, b_c, yv, seq, D, n_sb, static_cast<int>(blockIdx.x),
+                                   static_cast<int>(blockIdx.y));
+}
+
+// Several layers in one launch (1-D grid, the layers' grids one after another).
+template <int S, int KC, int NB, int NC, bool ACT, bool BF>
+__global__ void __launch_bounds__(256)
+fwd_layers_kernel(FwdLayers ly, SeqLayout seq) {
+  using E = typename CT<BF>::elem;
+  const int blk = static_cast<int>(blockIdx.x);
+  const FwdLayer* Lp = &ly.l[layer_index(ly, blk)];
+  int local = blk - Lp->blk0, row = 0;
+  const int gxl = Lp->gx;
+  while (local >= gxl) {  // scalar: local < gx gy, at most gy - 1 steps
+    local -= gxl;
+    ++row;
+  }
+  fwd_tile<S, KC, NB, NC, ACT, BF>(Lp->x, static_cast<const E*>(Lp->a),
+                                   static_cast<const E*>(Lp->b), Lp->y, seq, Lp->D, Lp->n_sb, local,
+                                   row);
 }
 
 // ---------------------------------------------------------------------------
@@ -499,14 +582,15 @@ template <int S, int KC, int MODE, bool BF>
 constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2 && BF) ? 1
                              : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
+// bwd_tile is the work of workgroup (bx, by) (route half zh with SPLIT) of
+// one layer; the __global__ wrappers below map the grid onto it.
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
-__global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
-bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
-           const typename CT<BF>::elem* __restrict__ a_c,
-           const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
-           float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
-           int gx, int gy, int gy1, int n_old, int n_total) {
+__device__ __forceinline__ void
+bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
+         const typename CT<BF>::elem* __restrict__ a_c,
+         const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
+         float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
+         int bx, int by, int zh, int gy, int gy1, int n_old, int n_total) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -518,22 +602,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
   constexpr int KX = SPLIT ? 1 : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
   static_assert(!SPLIT || KC == 2, "the route split halves two route chunks");
-  // Workgroup -> (channel group bx, token range by, route half zh).  Split in
-  // route halves (SPLIT), the grid is 1-D and the two halves of a tile are 8
-  // workgroup ids apart: ids go round-robin over the 8 XCDs, so both halves run
-  // on one XCD at about the same time and the second finds the tile's x / dy
-  // rows in that XCD's L2.
-  constexpr bool ZS = SPLIT;
   static_assert(!(SPLIT && MODE == kBwdTaps), "one split at a time");
-  int bx = static_cast<int>(blockIdx.x), by = static_cast<int>(blockIdx.y), zh = 0;
-  if constexpr (ZS) {
-    const int L = static_cast<int>(blockIdx.x);
-    const int t = (L >> 4) * 8 + (L & 7);
-    if (t >= gx * gy) return;  // whole workgroup, before any barrier
-    zh = (L >> 3) & 1;
-    bx = t % gx;
-    by = t / gx;
-  }
   const int kc0 = SPLIT ? zh : 0;
   constexpr int EOWN = TB - (S - 1);
   constexpr int NP = MS::kParts;
@@ -726,6 +795,15 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
   }
   __syncthreads();
 
+  // own-row masks of the dbasis alpha^T operands of a super-block with all
+  // EOWN own rows (every one but possibly the last of the token axis)
+  uint64_t keep_full[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int n_ok = min(max(EOWN - (R * q + 4 * b), 0), 4);
+    keep_full[b] = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
+  }
+
   StartCursor cursor;
   for (int sb = 0; sb < nsb; ++sb) {
     const int64_t t0 = first + static_cast<int64_t>(sb) * EOWN;
@@ -831,8 +909,11 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int c = 0; c < NC; ++c)
-            g[r][c] = g[r][c] * (sg[r][c] * (1.0f + p[r][c] * (1.0f - sg[r][c])));
+          for (int c = 0; c < NC; ++c) {
+            // silu'(P) = sg + P sg (1 - sg): two FMAs on sg
+            const float v = fmaf(-sg[r][c], sg[r][c], sg[r][c]);
+            g[r][c] = g[r][c] * fmaf(p[r][c], v, sg[r][c]);
+          }
       }
 
       // dx: taps in descending order, so that the first jobs (shift 0) need none
@@ -906,8 +987,11 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
           const int own_rows = static_cast<int>(own_end - t0);
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
-            const uint64_t keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
+            uint64_t keep = keep_full[b];
+            if (own_rows != EOWN) {  // uniform: the last super-block of the token axis
+              const int n_ok = min(max(own_rows - (R * q + 4 * b), 0), 4);
+              keep = n_ok >= 4 ? ~0ull : ((1ull << (16 * n_ok)) - 1ull);
+            }
 #pragma unroll
             for (int kx = 0; kx < KX; ++kx) {
               const int r = R * q + 4 * b + (j >> 2);
@@ -1126,6 +1210,72 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
               part_db[((base + 16 * (kc0 + kx) + j) * S + s0 + s) * D + ch] = dbacc[c][s][kx][v];
           }
   }
+}
+
+// Workgroup -> (channel group bx, token range by, route half zh) over a grid of
+// gx channel groups.  Split in route halves (SPLIT), the grid is 1-D and the two
+// halves of a tile are 8 workgroup ids apart: ids go round-robin over the 8
+// XCDs, so both halves run on one XCD at about the same time and the second
+// finds the tile's x / dy rows in that XCD's L2.  Returns false for the ids of
+// the 1-D grid past the last tile.
+// Block (x id, y id) of a 2-D grid, or id L of the 1-D grid of a split one.
+template <bool SPLIT>
+__device__ __forceinline__ bool bwd_block(int gx, int gy, int idx, int idy, int& bx, int& by,
+                                          int& zh) {
+  bx = idx;
+  by = idy;
+  zh = 0;
+  if constexpr (SPLIT) {
+    const int L = idx;
+    const int t = (L >> 4) * 8 + (L & 7);
+    if (t >= gx * gy) return false;
+    zh = (L >> 3) & 1;
+    bx = t % gx;
+    by = t / gx;
+  }
+  return true;
+}
+
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
+bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
+           const typename CT<BF>::elem* __restrict__ a_c,
+           const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
+           float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
+           int gx, int gy, int gy1, int n_old, int n_total) {
+  int bx, by, zh;
+  if (!bwd_block<SPLIT>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), bx,
+                        by, zh))
+    return;  // whole workgroup, before any barrier
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(xv, dyv, dys, a_c, b_c, dxv, part_da, part_db,
+                                                     seq, D, bx, by, zh, gy, gy1, n_old, n_total);
+}
+
+// Several layers in one launch (1-D grid, the layers' grids one after another:
+// gx gy blocks of layer i, or its split grid's ids).
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
+bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
+  using E = typename CT<BF>::elem;
+  const int blk = static_cast<int>(blockIdx.x);
+  const BwdLayer* Lp = &ly.l[layer_index(ly, blk)];
+  int local = blk - Lp->blk0;
+  int row = 0;
+  if constexpr (!SPLIT) {
+    const int gxl = Lp->gx;
+    while (local >= gxl) {  // scalar: local < gx gy, at most gy - 1 steps
+      local -= gxl;
+      ++row;
+    }
+  }
+  int bx, by, zh;
+  if (!bwd_block<SPLIT>(Lp->gx, Lp->gy, local, row, bx, by, zh))
+    return;  // whole workgroup, before any barrier
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(
+      Lp->x, Lp->dy, Lp->dys, static_cast<const E*>(Lp->a), static_cast<const E*>(Lp->b), Lp->dx,
+      Lp->part_da, Lp->part_db, seq, Lp->D, bx, by, zh, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total);
 }
 
 }  // namespace mfma

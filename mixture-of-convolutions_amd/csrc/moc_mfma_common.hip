@@ -102,17 +102,18 @@ __device__ __forceinline__ void stage2_db(const float* __restrict__ part_db, int
 //     alpha dtype;
 //   other blocks: one lane per basis element; dbasis = sum of the n_db token
 //     partials in order, stored in the basis dtype.
+// stage2_block is block blk of one layer's stage 2.
 template <int KC>
-__global__ void __launch_bounds__(256)
-stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __restrict__ part_db,
-              int64_t n_db, const float* __restrict__ a_r, const uint16_t* __restrict__ a_w,
-              void* __restrict__ dalpha, int a_dt, int routing, void* __restrict__ dbasis,
-              int b_dt, int64_t N, int K, int S, int64_t D, int64_t da_blocks) {
+__device__ __forceinline__ void
+stage2_block(const float* __restrict__ part_da, int64_t n_da, const float* __restrict__ part_db,
+             int64_t n_db, const float* __restrict__ a_r, const uint16_t* __restrict__ a_w,
+             void* __restrict__ dalpha, int a_dt, int routing, void* __restrict__ dbasis,
+             int b_dt, int64_t N, int K, int S, int64_t D, int64_t da_blocks, int64_t blk) {
   // the weights of the activation gradient: a_r (fp32) or, if a_r is null,
   // a_w (the caller's bf16 weights)
   constexpr int KP = 16 * KC;
-  if (static_cast<int64_t>(blockIdx.x) < da_blocks) {
-    const int64_t t = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+  if (blk < da_blocks) {
+    const int64_t t = (blk * 256 + threadIdx.x) >> 4;
     const int i = threadIdx.x & 15;
     const bool live = t < N;
     float da[KC], a[KC];
@@ -166,9 +167,49 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
       }
     }
   } else {
-    stage2_db<KP>(part_db, n_db, dbasis, b_dt, K, S, D,
-                  (static_cast<int64_t>(blockIdx.x) - da_blocks) * 256 + threadIdx.x);
+    stage2_db<KP>(part_db, n_db, dbasis, b_dt, K, S, D, (blk - da_blocks) * 256 + threadIdx.x);
   }
+}
+
+template <int KC>
+__global__ void __launch_bounds__(256)
+stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __restrict__ part_db,
+              int64_t n_db, const float* __restrict__ a_r, const uint16_t* __restrict__ a_w,
+              void* __restrict__ dalpha, int a_dt, int routing, void* __restrict__ dbasis,
+              int b_dt, int64_t N, int K, int S, int64_t D, int64_t da_blocks) {
+  stage2_block<KC>(part_da, n_da, part_db, n_db, a_r, a_w, dalpha, a_dt, routing, dbasis, b_dt, N,
+                   K, S, D, da_blocks, static_cast<int64_t>(blockIdx.x));
+}
+
+// Stage 2 of several layers in one launch: layer i owns blocks [blk0, blk0 +
+// da_blocks + its dbasis blocks) of the grid.
+struct Stage2Layer {
+  const float* part_da;
+  int64_t n_da, n_db;
+  const float* a_r;
+  const uint16_t* a_w;
+  void* dalpha;
+  int a_dt, routing;
+  void* dbasis;
+  int b_dt;
+  const float* part_db;
+  int64_t D, blk0;
+};
+struct Stage2Layers {
+  int n;
+  Stage2Layer l[kMaxLayers];
+};
+
+template <int KC>
+__global__ void __launch_bounds__(256)
+stage2_layers_kernel(Stage2Layers ly, int64_t N, int K, int S, int64_t da_blocks) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x);
+  Stage2Layer L = ly.l[0];
+#pragma unroll
+  for (int i = 1; i < kMaxLayers; ++i)
+    if (i < ly.n && b >= ly.l[i].blk0) L = ly.l[i];
+  stage2_block<KC>(L.part_da, L.n_da, L.part_db, L.n_db, L.a_r, L.a_w, L.dalpha, L.a_dt,
+                   L.routing, L.dbasis, L.b_dt, N, K, S, L.D, da_blocks, b - L.blk0);
 }
 
 // ---------------------------------------------------------------------------
@@ -334,6 +375,128 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
                        p.b_dt, p.n_tokens,
                        static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped layers: bf16 layers on one token axis with the same K, S and
+// activation run every pass as one launch over all their channel groups.
+
+bool layers_grouped(const Problem* ps, int n) {
+  if (n < 1 || n > kMaxLayers) return false;
+  for (int i = 0; i < n; ++i) {
+    const Problem& p = ps[i];
+    if (!supported(p) || p.x_dt != DT_BF16) return false;
+    if (p.K != ps[0].K || p.S != ps[0].S || p.activation != ps[0].activation ||
+        p.n_tokens != ps[0].n_tokens || p.path != ps[0].path)
+      return false;
+  }
+  return true;
+}
+
+size_t forward_layers_workspace(const Problem* ps, int n) {
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) total += plan(ps[i], false).total;
+  return total;
+}
+
+// Each layer keeps the partials of its own grid (the grouped backward runs the
+// layers' own grids), so the workspace is the layers' workspaces side by side.
+size_t backward_layers_workspace(const Problem* ps, int n) {
+  size_t total = 0;
+  for (int i = 0; i < n; ++i) total += plan(ps[i], true).total;
+  return total;
+}
+
+void forward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace,
+                    hipStream_t st) {
+  LayerOps L[kMaxLayers] = {};
+  char* ws = static_cast<char*>(workspace);
+  for (int i = 0; i < n; ++i) {
+    const Plan pl = plan(ps[i], false);
+    L[i].x = io[i].x;
+    L[i].a_c = io[i].alpha;
+    L[i].b_c = io[i].basis;
+    if (!direct(ps[i], io[i].alpha, io[i].basis, nullptr)) {
+      launch_prep(ps[i], pl, io[i].alpha, io[i].basis, ws, false, st);
+      L[i].a_c = ws + pl.off_ac;
+      L[i].b_c = ws + pl.off_bc;
+    }
+    L[i].y = io[i].y;
+    L[i].D = ps[i].D;
+    ws += pl.total;
+  }
+  prof_begin(ps[0], st);
+  switch (ps[0].S) {
+    case 2: launch_fwd_layers<2>(ps[0], L, n, st); break;
+    case 3: launch_fwd_layers<3>(ps[0], L, n, st); break;
+    case 4: launch_fwd_layers<4>(ps[0], L, n, st); break;
+    case 8: launch_fwd_layers<8>(ps[0], L, n, st); break;
+    default: break;
+  }
+  prof_end(ps[0], st);
+}
+
+void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace,
+                     hipStream_t st) {
+  LayerOps L[kMaxLayers] = {};
+  Stage2Layers s2{};
+  s2.n = n;
+  char* ws = static_cast<char*>(workspace);
+  const int64_t N = ps[0].n_tokens;
+  const int64_t da_blocks = cdiv(N * 16, 256);
+  int64_t blk = 0;
+  for (int i = 0; i < n; ++i) {
+    const Problem& p = ps[i];
+    const Plan pl = plan(p, true);
+    const bool dir = direct(p, io[i].alpha, io[i].basis, io[i].dalpha);
+    L[i].x = io[i].x;
+    L[i].a_c = io[i].alpha;
+    L[i].b_c = io[i].basis;
+    if (!dir) {
+      launch_prep(p, pl, io[i].alpha, io[i].basis, ws, true, st);
+      L[i].a_c = ws + pl.off_ac;
+      L[i].b_c = ws + pl.off_bc;
+    }
+    L[i].dy = io[i].dy;
+    L[i].dys = p.dy_stride;
+    L[i].dx = io[i].dx;
+    L[i].part_da = reinterpret_cast<float*>(ws + pl.off_pda);
+    L[i].part_db = reinterpret_cast<float*>(ws + pl.off_pdb);
+    L[i].D = p.D;
+    const int grad = route_grad(p.routing);
+    s2.l[i] = Stage2Layer{L[i].part_da,
+                          static_cast<int64_t>(pl.bg.gx),
+                          static_cast<int64_t>(pl.bg.gy),
+                          (grad != ROUTE_ALPHA && !dir) ? reinterpret_cast<const float*>(ws + pl.off_ar)
+                                                        : nullptr,
+                          static_cast<const uint16_t*>(io[i].alpha),
+                          io[i].dalpha,
+                          p.a_dt,
+                          grad,
+                          io[i].dbasis,
+                          p.b_dt,
+                          L[i].part_db,
+                          p.D,
+                          blk};
+    blk += da_blocks + cdiv(p.K * p.S * p.D, 256);
+    ws += pl.total;
+  }
+  prof_begin(ps[0], st);
+  switch (ps[0].S) {
+    case 2: launch_bwd_layers<2>(ps[0], L, n, st); break;
+    case 3: launch_bwd_layers<3>(ps[0], L, n, st); break;
+    case 4: launch_bwd_layers<4>(ps[0], L, n, st); break;
+    case 8: launch_bwd_layers<8>(ps[0], L, n, st); break;
+    default: break;
+  }
+  prof_end(ps[0], st);
+  const int K = static_cast<int>(ps[0].K), S = static_cast<int>(ps[0].S);
+  if (K <= 16)
+    hipLaunchKernelGGL(stage2_layers_kernel<1>, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st,
+                       s2, N, K, S, da_blocks);
+  else
+    hipLaunchKernelGGL(stage2_layers_kernel<2>, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st,
+                       s2, N, K, S, da_blocks);
 }
 
 }  // namespace mfma

@@ -43,8 +43,11 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // longer ones (measured: D 4096, 32768 tokens, 161 -> 141 us).
 constexpr int64_t kFwdMaxSb = 4;
 
-inline Grid2 fwd_grid(int64_t N, int64_t D) {
-  const int64_t gx = cdiv(D, 4 * 16 * kFwdNC);
+// Channels of one forward / backward workgroup (grid x counts these groups).
+constexpr int64_t kFwdCW = 4 * 16 * kFwdNC, kBwdCW = kBwdWPG * 16 * kBwdNC;
+
+// Forward grid over gx channel groups (the sum over the layers of a grouped launch).
+inline Grid2 fwd_grid_gx(int64_t N, int64_t gx) {
   const int64_t n_super = cdiv(N, 16 * kFwdNB);
   int64_t gy_target = kFwdTargetWG / gx;
   if (gy_target < 1) gy_target = 1;
@@ -56,8 +59,12 @@ inline Grid2 fwd_grid(int64_t N, int64_t D) {
                static_cast<int>(n_sb)};
 }
 
-inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S, int64_t target_wg = kBwdTargetWG) {
-  const int64_t gx = cdiv(D, kBwdWPG * 16 * kBwdNC);
+inline Grid2 fwd_grid(int64_t N, int64_t D) { return fwd_grid_gx(N, cdiv(D, kFwdCW)); }
+
+// Backward grid over gx channel groups; D is the widest layer's channel count
+// (it bounds the token range of a workgroup's buffers).
+inline Grid2 bwd_grid_gx(int64_t N, int64_t gx, int64_t D, int64_t S,
+                         int64_t target_wg = kBwdTargetWG) {
   const int64_t eown = 16 * kBwdNB - (S - 1);
   const int64_t n_super = cdiv(N, eown);
   int64_t gy_target = target_wg / gx;
@@ -73,6 +80,10 @@ inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S, int64_t target_wg = kBwdT
   g.n_old = static_cast<int>(n_sb * static_cast<int64_t>(g.gy));
   g.n_total = g.n_old;
   return g;
+}
+
+inline Grid2 bwd_grid(int64_t N, int64_t D, int64_t S, int64_t target_wg = kBwdTargetWG) {
+  return bwd_grid_gx(N, cdiv(D, kBwdCW), D, S, target_wg);
 }
 
 // Number of compute units of the current device (cached per device).
@@ -104,8 +115,8 @@ inline int device_cu_count() {
 #endif
 constexpr int64_t kBwdOldShare = MOC_BWD_OLD_SHARE;
 
-inline Grid2 bwd_grid_tiered(int64_t N, int64_t D, int64_t S, int n_cu) {
-  Grid2 g = bwd_grid(N, D, S);
+inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_cu) {
+  Grid2 g = bwd_grid_gx(N, gx, D, S);
   if (n_cu <= 0 || n_cu % static_cast<int64_t>(g.gx) != 0) return g;
   const int64_t gy1 = n_cu / static_cast<int64_t>(g.gx);
   const int64_t gy = g.gy;
@@ -138,15 +149,34 @@ inline bool bwd_two_pass(const Problem& p) {
 // of n_cu workgroups, with ranges twice as long as the default grid's.  Two
 // rounds measured slower: each round pays a prologue of about 6 us, and the
 // second round's workgroups started 15-20 us after the first round's ended.
-inline Grid2 bwd_taps_grid(int64_t N, int64_t D, int64_t S, int n_cu) {
-  return bwd_grid(N, D, S, n_cu > 0 ? n_cu : kBwdTargetWG / 2);
+inline Grid2 bwd_taps_grid(int64_t N, int64_t gx, int64_t D, int64_t S, int n_cu) {
+  return bwd_grid_gx(N, gx, D, S, n_cu > 0 ? n_cu : kBwdTargetWG / 2);
 }
 
-// The grid whose ranges own the dalpha / dbasis partials (workspace, stage 2).
-inline Grid2 bwd_partials_grid(const Problem& p) {
-  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, p.D, p.S, device_cu_count())
-                         : bwd_grid(p.n_tokens, p.D, p.S);
+// The grid whose ranges own the dalpha / dbasis partials (workspace, stage 2),
+// over gx channel groups of layers at most D channels wide.
+inline Grid2 bwd_partials_grid(const Problem& p, int64_t gx, int64_t D) {
+  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, gx, D, p.S, device_cu_count())
+                         : bwd_grid_gx(p.n_tokens, gx, D, p.S);
 }
+inline Grid2 bwd_partials_grid(const Problem& p) {
+  return bwd_partials_grid(p, cdiv(p.D, kBwdCW), p.D);
+}
+
+// Operands of one layer of a grouped launch (after operand preparation); the
+// layers share Problem's token axis, K, S, activation and dtypes.
+struct LayerOps {
+  const void* x;
+  const void* a_c;
+  const void* b_c;
+  void* y;           // forward output
+  const void* dy;    // backward
+  int64_t dys;
+  void* dx;
+  float* part_da;
+  float* part_db;
+  int64_t D;
+};
 
 template <int S, int KC, bool ACT, bool BF>
 void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
@@ -168,7 +198,9 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   constexpr bool kSplit = BF && KC == 2;
   // tiers for the fused pass at two resident workgroups per CU (not split in halves)
   constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
-  const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, p.D, S, device_cu_count()) : bwd_grid(p.n_tokens, p.D, S);
+  const int64_t gx_all = cdiv(p.D, kBwdCW);
+  const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, gx_all, p.D, S, device_cu_count())
+                         : bwd_grid(p.n_tokens, p.D, S);
   const auto* a = static_cast<const E*>(a_c);
   const auto* b = static_cast<const E*>(b_c);
   const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
@@ -183,7 +215,7 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
     // (one round of n_cu workgroups: bwd_taps_grid)
-    const Grid2 gt = bwd_taps_grid(p.n_tokens, p.D, S, device_cu_count());
+    const Grid2 gt = bwd_taps_grid(p.n_tokens, gx_all, p.D, S, device_cu_count());
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
                        dim3(gt.gx, gt.gy), dim3(128 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
@@ -192,6 +224,95 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a,
                        b, dx, part_da, part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
+  }
+}
+
+// Grouped launches (bf16): one kernel over the layers' own grids, one after
+// another on a 1-D grid (see FwdLayers / BwdLayers).
+template <int S, int KC, bool ACT>
+void fwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
+  FwdLayers ly{};
+  ly.n = n;
+  int64_t blk = 0;
+  for (int i = 0; i < n; ++i) {
+    const Grid2 g = fwd_grid(p.n_tokens, L[i].D);
+    ly.l[i] = FwdLayer{L[i].x, L[i].a_c, L[i].b_c, L[i].y, L[i].D, static_cast<int>(g.gx),
+                       g.n_sb, static_cast<int>(blk)};
+    blk += static_cast<int64_t>(g.gx) * g.gy;
+  }
+  hipLaunchKernelGGL((fwd_layers_kernel<S, KC, kFwdNB, kFwdNC, ACT, true>),
+                     dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, ly, p.seq);
+}
+
+template <int S, int KC, bool ACT>
+void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
+  constexpr bool kSplit = KC == 2;
+  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, true);
+  constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, true> == 2;
+  const int n_cu = device_cu_count();
+  // each layer's grid as bwd_one forms it (the taps pass has its own)
+  BwdLayers ly{}, lt{};
+  ly.n = lt.n = n;
+  int64_t blk = 0, blkt = 0;
+  bool any_dx = false;
+  for (int i = 0; i < n; ++i) {
+    const int64_t gx_l = cdiv(L[i].D, kBwdCW);
+    const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, gx_l, L[i].D, S, n_cu)
+                           : bwd_grid(p.n_tokens, L[i].D, S);
+    ly.l[i] = BwdLayer{L[i].x, L[i].dy, L[i].dys, L[i].a_c, L[i].b_c, L[i].dx, L[i].part_da,
+                       L[i].part_db, L[i].D, static_cast<int>(g.gx), static_cast<int>(g.gy),
+                       g.gy1, g.n_old, g.n_total, static_cast<int>(blk)};
+    const int64_t tiles = static_cast<int64_t>(g.gx) * g.gy;
+    // the dx pass of the two-pass form skips layers without dx (no blocks:
+    // layer_index then never selects them)
+    blk += kSplit ? 16 * cdiv(tiles, 8) : (kTwo && L[i].dx == nullptr ? 0 : tiles);
+    any_dx = any_dx || L[i].dx != nullptr;
+    if constexpr (kTwo) {
+      const Grid2 gt = bwd_taps_grid(p.n_tokens, gx_l, L[i].D, S, n_cu);
+      lt.l[i] = ly.l[i];
+      lt.l[i].dx = nullptr;
+      lt.l[i].gx = static_cast<int>(gt.gx);
+      lt.l[i].gy = static_cast<int>(gt.gy);
+      lt.l[i].gy1 = gt.gy1;
+      lt.l[i].n_old = gt.n_old;
+      lt.l[i].n_total = gt.n_total;
+      lt.l[i].blk0 = static_cast<int>(blkt);
+      blkt += static_cast<int64_t>(gt.gx) * gt.gy;
+    }
+  }
+  if constexpr (kTwo) {
+    if (any_dx)
+      hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, false, kBwdDx>),
+                         dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
+    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, true, false, kBwdTaps>),
+                       dim3(static_cast<unsigned>(blkt)), dim3(128 * kBwdWPG), 0, st, lt, p.seq);
+  } else {
+    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, kSplit, kBwdFused>),
+                       dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
+  }
+}
+
+template <int S>
+void launch_fwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
+  const bool act = p.activation != 0;
+  if (p.K <= 16) {
+    if (act) fwd_layers_one<S, 1, true>(p, L, n, st);
+    else fwd_layers_one<S, 1, false>(p, L, n, st);
+  } else {
+    if (act) fwd_layers_one<S, 2, true>(p, L, n, st);
+    else fwd_layers_one<S, 2, false>(p, L, n, st);
+  }
+}
+
+template <int S>
+void launch_bwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
+  const bool act = p.activation != 0;
+  if (p.K <= 16) {
+    if (act) bwd_layers_one<S, 1, true>(p, L, n, st);
+    else bwd_layers_one<S, 1, false>(p, L, n, st);
+  } else {
+    if (act) bwd_layers_one<S, 2, true>(p, L, n, st);
+    else bwd_layers_one<S, 2, false>(p, L, n, st);
   }
 }
 
@@ -242,7 +363,9 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
   extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
                                       void*, hipStream_t);                                    \
   extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
-                                      const void*, void*, float*, float*, hipStream_t);
+                                      const void*, void*, float*, float*, hipStream_t);       \
+  extern template void launch_fwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t); \
+  extern template void launch_bwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t);
 MOC_DECLARE_S(2)
 MOC_DECLARE_S(3)
 MOC_DECLARE_S(4)

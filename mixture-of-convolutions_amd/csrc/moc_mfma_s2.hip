@@ -8,6 +8,8 @@ template void launch_fwd<2>(const Problem&, const void*, const void*, const void
                              hipStream_t);
 template void launch_bwd<2>(const Problem&, const void*, const void*, const void*, const void*,
                              void*, float*, float*, hipStream_t);
+template void launch_fwd_layers<2>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_bwd_layers<2>(const Problem&, const LayerOps*, int, hipStream_t);
 
 }  // namespace mfma
 }  // namespace moc

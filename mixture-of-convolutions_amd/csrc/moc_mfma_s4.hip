@@ -8,6 +8,8 @@ template void launch_fwd<4>(const Problem&, const void*, const void*, const void
                              hipStream_t);
 template void launch_bwd<4>(const Problem&, const void*, const void*, const void*, const void*,
                              void*, float*, float*, hipStream_t);
+template void launch_fwd_layers<4>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_bwd_layers<4>(const Problem&, const LayerOps*, int, hipStream_t);
 
 }  // namespace mfma
 }  // namespace moc

@@ -35,6 +35,10 @@ EXPORTED_SYMBOLS = (
     "moc_backward_workspace_bytes",
     "moc_backward",
     "moc_backward_noalloc",
+    "moc_forward_layers_workspace_bytes",
+    "moc_forward_layers",
+    "moc_backward_layers_workspace_bytes",
+    "moc_backward_layers",
     "moc_update",
     "moc_profile_events",
     "moc_decode_step_supported",
@@ -46,6 +50,20 @@ EXPORTED_SYMBOLS = (
     "moc_router_backward_workspace_bytes",
     "moc_router_backward",
 )
+
+MAX_LAYERS = 4
+
+
+class MocLayer(ctypes.Structure):
+    """struct MocLayer of include/moc_hip.h: one layer of a grouped launch."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("alpha", ctypes.c_void_p), ("basis", ctypes.c_void_p),
+        ("y", ctypes.c_void_p), ("dy", ctypes.c_void_p), ("dy_row_stride", ctypes.c_int64),
+        ("dx", ctypes.c_void_p), ("dalpha", ctypes.c_void_p), ("dbasis", ctypes.c_void_p),
+        ("dim", ctypes.c_int64), ("routing", ctypes.c_int), ("alpha_dtype", ctypes.c_int),
+        ("basis_dtype", ctypes.c_int),
+    ]
+
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -90,6 +108,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_backward_noalloc.restype = _i
     lib.moc_set_kernel_path.argtypes = [_i]
     lib.moc_set_kernel_path.restype = _i
+    for name in ("moc_forward_layers", "moc_backward_layers"):
+        fn = getattr(lib, name)
+        fn.argtypes = [_p, _i, _p, _i, _l, _l, _l, _l, _l, _i, _i, _p, _z, _p]
+        fn.restype = _i
+        q = getattr(lib, name + "_workspace_bytes")
+        q.argtypes = [_p, _i, _l, _l, _l, _i, _i]
+        q.restype = _z
     lib.moc_update.argtypes = [
         _p, _p, _p, _p,            # x, alpha, basis, cache
         _l, _l, _l,                # cache strides (elements)

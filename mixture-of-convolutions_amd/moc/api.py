@@ -288,39 +288,49 @@ class _MoCGroupFunction(torch.autograd.Function):
         router_cat = torch.cat([r.contiguous() for r in routers], 0)
         weights = ops.router_forward_grouped(z, router_cat, ks,
                                              [_ROUTING_CODES[r] for r in routes])
-        ys, saved_x, saved_b = [], [], []
+        saved_x, saved_b = [], []
         cu = None
         for g in range(n):
             x, w, b, cu = _prepare(None, xs[g], weights[g], bases[g], cu_seqlens, max_seqlen,
                                    cu_seqlens_cpu, chunk_indices)
-            ys.append(ops.launch_forward(x, w, b, activation_flag=activation_flag(acts[g]),
-                                         cu_seqlens=cu, routing=_WEIGHTS_CODES[routes[g]]))
             saved_x.append(x)
             saved_b.append(b)
+        flags = [activation_flag(a) for a in acts]
+        codes = [_WEIGHTS_CODES[r] for r in routes]
+        # one launch over all layers when they share K, S and the activation
+        together = (len({tuple(b.shape[:2]) for b in saved_b}) == 1 and len(set(flags)) == 1
+                    and len({x.dtype for x in saved_x}) == 1)
+        if together:
+            ys = ops.launch_forward_layers(saved_x, weights, saved_b, activation_flag=flags[0],
+                                           routings=codes, cu_seqlens=cu)
+        else:
+            ys = [ops.launch_forward(x, w, b, activation_flag=f, cu_seqlens=cu, routing=c)
+                  for x, w, b, f, c in zip(saved_x, weights, saved_b, flags, codes)]
         tail = () if cu is None else (cu,)
         ctx.save_for_backward(z, router_cat, *saved_x, *weights, *saved_b, *tail)
-        ctx.spec = (n, [activation_flag(a) for a in acts], [_WEIGHTS_CODES[r] for r in routes],
-                    ks, cu is not None)
+        ctx.spec = (n, flags, codes, ks, cu is not None, together)
         return tuple(ys)
 
     @staticmethod
     @once_differentiable
     def backward(ctx, *dys):
-        n, acts, codes, ks, varlen = ctx.spec
+        n, acts, codes, ks, varlen, together = ctx.spec
         saved = ctx.saved_tensors
         z, router_cat = saved[0], saved[1]
         xs, weights, bases = saved[2:2 + n], saved[2 + n:2 + 2 * n], saved[2 + 2 * n:2 + 3 * n]
         cu = saved[2 + 3 * n] if varlen else None
-        dxs, dls, dbs = [], [], []
-        for g in range(n):
-            dy = dys[g] if dys[g] is not None else torch.zeros_like(xs[g])
-            dx, dl, db = ops.launch_backward(xs[g], weights[g], bases[g], dy,
-                                             activation_flag=acts[g],
-                                             need_x=ctx.needs_input_grad[2 + n + g],
-                                             cu_seqlens=cu, routing=codes[g])
-            dxs.append(dx)
-            dls.append(dl)
-            dbs.append(db)
+        dys = [dy if dy is not None else torch.zeros_like(x) for dy, x in zip(dys, xs)]
+        need = [ctx.needs_input_grad[2 + n + g] for g in range(n)]
+        if together:
+            res = ops.launch_backward_layers(xs, weights, bases, dys, activation_flag=acts[0],
+                                             routings=codes, need_xs=need, cu_seqlens=cu)
+        else:
+            res = [ops.launch_backward(x, w, b, dy, activation_flag=f, need_x=nx, cu_seqlens=cu,
+                                       routing=c)
+                   for x, w, b, dy, f, nx, c in zip(xs, weights, bases, dys, acts, need, codes)]
+        dxs = [r[0] for r in res]
+        dls = [r[1] for r in res]
+        dbs = [r[2] for r in res]
         need_z = ctx.needs_input_grad[0]
         need_r = any(ctx.needs_input_grad[2:2 + n])
         dz, dr = None, None

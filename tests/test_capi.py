@@ -163,3 +163,42 @@ def test_backward_noalloc_rejects_before_touching_the_device():
     assert rc == -3 and b"moc_backward_noalloc holds" in L.moc_last_error()
     small = L.moc_backward_workspace_bytes(16384, 2048, 16, 4, _lib.DT_BF16, 3)
     assert small <= _lib.NOALLOC_SCRATCH_BYTES    # the headline shape fits
+
+
+def _layers(dims, **kw):
+    arr = (_lib.MocLayer * max(len(dims), 1))()
+    for i, d in enumerate(dims):
+        arr[i].x = arr[i].alpha = arr[i].basis = arr[i].y = FAKE
+        arr[i].dy = arr[i].dx = arr[i].dalpha = arr[i].dbasis = FAKE
+        arr[i].dy_row_stride = d
+        arr[i].dim = d
+        arr[i].routing = 3
+        arr[i].alpha_dtype = arr[i].basis_dtype = _lib.DT_BF16
+        for k, v in kw.items():
+            setattr(arr[i], k, v)
+    return arr
+
+
+def test_layer_entries_validate_and_size():
+    """moc_*_layers: argument checks before any launch; grouped bf16 layers need
+    the per-layer workspaces side by side."""
+    L = _lib.lib()
+    dims = [4096, 1024, 1024]
+    arr = _layers(dims)
+    N, K, S = 16384, 32, 8
+    for which in ("forward", "backward"):
+        q = getattr(L, f"moc_{which}_layers_workspace_bytes")
+        single = getattr(L, f"moc_{which}_workspace_bytes")
+        assert q(arr, 3, N, K, S, _lib.DT_BF16, 0) == sum(single(N, d, K, S, _lib.DT_BF16, 3)
+                                                            for d in dims)
+        assert q(arr, 0, N, K, S, _lib.DT_BF16, 0) == 0
+        fn = getattr(L, f"moc_{which}_layers")
+        assert fn(arr, 5, None, 0, 0, N, N, K, S, 1, 0, FAKE, 1 << 40, None) == -1
+        assert b"n_layers" in L.moc_last_error()
+        assert fn(arr, 3, None, 0, 0, N, N, K, S, 1, 0, FAKE, 16, None) == -3
+    bad = _layers([64, 64], dy_row_stride=7)
+    assert L.moc_backward_layers(bad, 2, None, 0, 0, 8, 8, 16, 4, 1, 0, FAKE, 1 << 30, None) == -1
+    assert b"dy_row_stride" in L.moc_last_error()
+    nul = _layers([64], dalpha=None)
+    assert L.moc_backward_layers(nul, 1, None, 0, 0, 8, 8, 16, 4, 1, 0, FAKE, 1 << 30, None) == -1
+    assert b"null" in L.moc_last_error()

@@ -207,6 +207,8 @@ def _run_layers(layers, xs, z, dys, grouped, **kw):
 
 QKV_SPECS = [
     [(256, 32, 8, None, "exp"), (64, 32, 8, None, "exp"), (64, 32, 8, None, "softmax")],
+    [(192, 16, 4, "silu", "softmax"), (128, 16, 4, "silu", "exp"), (64, 16, 4, "silu", "softmax")],
+    [(256, 32, 4, "silu", "exp"), (96, 32, 4, "silu", "softmax")],
     [(192, 16, 4, "silu", "softmax"), (128, 20, 3, None, "exp")],
     [(128, 8, 2, "silu", "softmax"), (64, 4, 4, None, "exp"), (64, 12, 4, None, "softmax"),
      (32, 32, 8, "silu", "exp")],
@@ -216,11 +218,13 @@ QKV_SPECS = [
 @pytest.mark.parametrize("specs", QKV_SPECS)
 @pytest.mark.parametrize("varlen", [False, True])
 def test_group_matches_separate_layers(specs, varlen):
-    """MoCGroup (one router pass over the concatenated routers, one router
-    backward) against the same layers called one by one: y, dx, drouter and
-    dbasis bit for bit (same kernels, same reduction order); dz, which the
-    group sums over all routes in fp32 while autograd adds the layers' bf16
-    dz, within the bf16 rule."""
+    """MoCGroup (one router pass over the concatenated routers, one forward and
+    one backward launch over all layers when they share K, S and activation,
+    one router backward) against the same layers called one by one: y, dx,
+    drouter and dbasis bit for bit (every workgroup does the work of its own
+    layer's launch, same reduction order); dz, which the group sums over all
+    routes in fp32 while autograd adds the layers' bf16 dz, within the bf16
+    rule."""
     Z, B, T = 128, 2, 61
     layers, g = _qkv_layers(specs, Z, len(specs) * 10 + varlen)
     if varlen:
