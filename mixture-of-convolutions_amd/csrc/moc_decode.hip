@@ -105,8 +105,42 @@ __global__ void __launch_bounds__(256) decode_kernel(
   const int64_t dl = d0 + kNC * i;        // first channel of this lane
   const bool ch_ok = wave_on && dl < D;   // D is even: both channels are in or out
 
-  // Every load of the step is issued first, without branches (out-of-range
-  // offsets load zeros): logits, basis rows, x and cache rows.
+  // FUSED: the router GEMV's loads go first, all of a wave's z chunks in one
+  // round (UBW chunks; more rounds only past 256 UBW z columns), so that the
+  // GEMV waits for them alone: the memory counter retires loads in issue
+  // order, and loads issued before them would hold it up.  Wave w takes the
+  // 64-wide z chunks c = w, w + 4, ...; lane (i, qq) loads columns 64 c + 8 qq
+  // + [0, 8) and 64 c + 32 + 8 qq + [0, 8) of token tb + i and route 16 kc + i.
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int UBW = KC == 1 ? 8 : 4;
+  u32x4 za[UBW][2], ra[UBW][KC][2];
+  const int nchunk = Z / 64;
+  const uint32_t zrow = static_cast<uint32_t>(i * Z * 2);
+  const int64_t zrows = (B - tb < 16) ? B - tb : 16;
+  const Buf zb(z + tb * Z, FUSED ? zrows * Z * 2 : 0);
+  const Buf rbuf(router, FUSED ? static_cast<int64_t>(K) * Z * 2 : 0);
+  auto gemv_load = [&](int c0) {
+#pragma unroll
+    for (int u = 0; u < UBW; ++u) {
+      const int c = c0 + 4 * u;
+      const bool on = c < nchunk;
+      const uint32_t col0 = static_cast<uint32_t>((64 * c + 8 * qq) * 2), col1 = col0 + 64;
+      za[u][0] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col0 : kOffNone), 0, 0);
+      za[u][1] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col1 : kOffNone), 0, 0);
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
+        ra[u][kc][0] = __builtin_amdgcn_raw_buffer_load_b128(rbuf.r, static_cast<int>(on ? rrow + col0 : kOffNone), 0, 0);
+        ra[u][kc][1] = __builtin_amdgcn_raw_buffer_load_b128(rbuf.r, static_cast<int>(on ? rrow + col1 : kOffNone), 0, 0);
+      }
+    }
+  };
+  if constexpr (FUSED) gemv_load(wave);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // The other loads of the step, without branches (out-of-range offsets load
+  // zeros): logits (not FUSED), basis rows, x and cache rows.
   // logits of token ta, routes 16 kc + 4 qq + {0..3} (K % 4 == 0: whole words)
   uint32_t lw[KC][2];
   if constexpr (!FUSED) {
@@ -148,6 +182,9 @@ __global__ void __launch_bounds__(256) decode_kernel(
     cr[v].load(cb, ch_ok ? static_cast<uint32_t>((r * D + dl) * S * 2) : kOffNone);
   }
 
+  // every load above is issued before the GEMV's products consume its loads
+  __builtin_amdgcn_sched_barrier(0);
+
   // routing weights in the A-operand layout, rounded as the forward path rounds
   // them (softmax / exp in fp32, then to bf16)
   float l[KC][4];
@@ -158,34 +195,12 @@ __global__ void __launch_bounds__(256) decode_kernel(
     // + [0, 8) of token tb + i and route 16 kc + i); the 4 partial tiles are
     // summed in LDS in wave order
     __shared__ float red[4][16 * KC][17];
-    const int64_t rows = (B - tb < 16) ? B - tb : 16;
-    const Buf zb(z + tb * Z, rows * Z * 2);
-    const Buf rb(router, static_cast<int64_t>(K) * Z * 2);
-    typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     f32x4 acc[KC];
 #pragma unroll
     for (int kc = 0; kc < KC; ++kc) acc[kc] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int nchunk = Z / 64;
-    const uint32_t zrow = static_cast<uint32_t>(i * Z * 2);
-    for (int c0 = wave; c0 < nchunk; c0 += 16) {
-      u32x4 za[4][2], ra[4][KC][2];
+    auto gemv_mma = [&]() {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int c = c0 + 4 * u;
-        const bool on = c < nchunk;
-        const uint32_t col0 = static_cast<uint32_t>((64 * c + 8 * qq) * 2), col1 = col0 + 64;
-        za[u][0] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col0 : kOffNone), 0, 0);
-        za[u][1] = __builtin_amdgcn_raw_buffer_load_b128(zb.r, static_cast<int>(on ? zrow + col1 : kOffNone), 0, 0);
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
-          const uint32_t rrow = static_cast<uint32_t>((16 * kc + i) * Z * 2);
-          ra[u][kc][0] = __builtin_amdgcn_raw_buffer_load_b128(rb.r, static_cast<int>(on ? rrow + col0 : kOffNone), 0, 0);
-          ra[u][kc][1] = __builtin_amdgcn_raw_buffer_load_b128(rb.r, static_cast<int>(on ? rrow + col1 : kOffNone), 0, 0);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < UBW; ++u)
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc)
 #pragma unroll
@@ -193,6 +208,14 @@ __global__ void __launch_bounds__(256) decode_kernel(
             acc[kc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, za[u][h]),
                                                               __builtin_bit_cast(bf16x8, ra[u][kc][h]),
                                                               acc[kc], 0, 0, 0);
+    };
+    // the first round in straight-line code, so that each product waits for
+    // its own loads only (not for the step's later-issued loads); further
+    // rounds (z_dim above 256 UBW) in a loop
+    gemv_mma();
+    for (int c0 = wave + 4 * UBW; c0 < nchunk; c0 += 4 * UBW) {
+      gemv_load(c0);
+      gemv_mma();
     }
     // result lane (j, q): route 16 kc + j, tokens 4 q + v
 #pragma unroll
