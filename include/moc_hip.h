@@ -111,7 +111,8 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
                 int activation, int routing,
                 void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes moc_backward needs for this problem. */
+/* Workspace bytes moc_backward needs for this problem, with or without the
+ * activation (it is not an argument here). */
 size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                     int64_t kernel_size, int x_dtype, int routing);
 
@@ -162,6 +163,54 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
                          int64_t dim, int64_t k, int64_t kernel_size,
                          int x_dtype, int alpha_dtype, int basis_dtype,
                          int activation, int routing, void* stream);
+
+/*
+ * Prefill from a cache: n_seqs fixed-length sequences of seq_len tokens that
+ * continue the inputs a cache holds.  Replaces the reference's cache path of
+ * moc_triton (moc/api.py:299-309: cat the cache before x with zero routing,
+ * run the op, drop the first kernel_size outputs) and its final state
+ * (moc/api.py:218-227, _final_state) with one launch per pass:
+ *   cache       : [n_seqs, dim, kernel_size] in x_dtype, contiguous, slot
+ *                 kernel_size-1 the newest input; NULL for a zero history
+ *                 (the plain op); read by the taps that reach before a
+ *                 sequence's first token
+ *   final_state : [n_seqs, dim, kernel_size] in x_dtype, or NULL: each
+ *                 sequence's last kernel_size inputs (with seq_len <
+ *                 kernel_size, the cache's newest slots first, or zeros)
+ * y equals the reference's prefill output; the other arguments are those of
+ * moc_forward with n_tokens = n_seqs * seq_len.  With a cache, seq_len must be
+ * at least kernel_size - 1.  Runs on the matrix-core kernels only:
+ * moc_prefill_supported tells whether a problem does (with_cache: a cache is
+ * given), otherwise the calls fail with MOC_ERR_ARG.  Workspaces are those of
+ * moc_forward_workspace_bytes / moc_backward_workspace_bytes for n_tokens.
+ */
+int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,
+                          int64_t kernel_size, int x_dtype, int with_cache);
+
+int moc_forward_prefill(const void* x, const void* alpha, const void* basis, void* y,
+                        const void* cache, void* final_state,
+                        int64_t n_seqs, int64_t seq_len,
+                        int64_t dim, int64_t k, int64_t kernel_size,
+                        int x_dtype, int alpha_dtype, int basis_dtype,
+                        int activation, int routing,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Gradients of moc_forward_prefill (cache required): moc_backward's dx,
+ * dalpha and dbasis (arguments as there), plus
+ *   dcache : [n_seqs, dim, kernel_size] in x_dtype, or NULL to skip it: the
+ *            gradient of the cache (slot 0 is read by no output and gets 0).
+ * A gradient of the final state is not an input: its dx / dcache part is a
+ * copy the caller adds (the state is a slice of x and the cache).
+ */
+int moc_backward_prefill(const void* x, const void* alpha, const void* basis, const void* dy,
+                         int64_t dy_row_stride, const void* cache,
+                         void* dx, void* dalpha, void* dbasis, void* dcache,
+                         int64_t n_seqs, int64_t seq_len,
+                         int64_t dim, int64_t k, int64_t kernel_size,
+                         int x_dtype, int alpha_dtype, int basis_dtype,
+                         int activation, int routing,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Several MoC layers on one token axis in one launch per pass: the q / k / v

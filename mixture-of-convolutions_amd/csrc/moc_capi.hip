@@ -140,7 +140,7 @@ int hip_status(const char* what) {
 
 extern "C" {
 
-int moc_abi_version(void) { return 2; }
+int moc_abi_version(void) { return 3; }
 
 const char* moc_last_error(void) { return g_err; }
 
@@ -200,9 +200,16 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
 size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                     int64_t kernel_size, int x_dtype, int routing) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
-  moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
-                                MOC_DT_F32, MOC_DT_F32, 0, routing);
-  return backward_bytes(p);
+  // the activation is not an argument, and the kernel plan can depend on it
+  // (8 taps, 32 routes, bf16: two passes without it, the fused pass with it)
+  size_t need = 0;
+  for (int act = 0; act <= 1; ++act) {
+    const moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size,
+                                        x_dtype, MOC_DT_F32, MOC_DT_F32, act, routing);
+    const size_t b = backward_bytes(p);
+    if (b > need) need = b;
+  }
+  return need;
 }
 
 }  // extern "C"
@@ -331,6 +338,100 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
                          static_cast<hipStream_t>(stream));
 }
 
+
+// ---------------------------------------------------------------------------
+// Prefill from a cache (fixed-length sequences, MFMA kernels).
+
+int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,
+                          int64_t kernel_size, int x_dtype, int with_cache) {
+  if (n_seqs <= 0 || seq_len <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
+  if (n_seqs > kMaxTokens / seq_len) return 0;
+  moc::Problem p = make_problem(nullptr, 0, n_seqs, n_seqs * seq_len, seq_len, dim, k,
+                                kernel_size, x_dtype, MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
+  return use_mfma(p) && moc::mfma::prefill_supported(p, with_cache != 0) ? 1 : 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the prefill entries; fills p (fixed-length, n_seqs x seq_len tokens).
+int prefill_problem(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k, int64_t kernel_size,
+                    int x_dtype, int alpha_dtype, int basis_dtype, int activation, int routing,
+                    bool has_cache, moc::Problem& p) {
+  int rc;
+  if (n_seqs <= 0 || seq_len <= 0)
+    return fail(MOC_ERR_ARG, "n_seqs and seq_len must be positive (got %lld, %lld)",
+                (long long)n_seqs, (long long)seq_len);
+  if (n_seqs > kMaxTokens / seq_len)
+    return fail(MOC_ERR_ARG, "n_seqs * seq_len too large: %lld x %lld", (long long)n_seqs,
+                (long long)seq_len);
+  const int64_t n_tokens = n_seqs * seq_len;
+  if ((rc = check_dims(n_tokens, dim, k, kernel_size)) != MOC_OK) return rc;
+  if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
+  p = make_problem(nullptr, 0, n_seqs, n_tokens, seq_len, dim, k, kernel_size, x_dtype,
+                   alpha_dtype, basis_dtype, activation, routing);
+  if (!use_mfma(p) || !moc::mfma::prefill_supported(p, has_cache))
+    return fail(MOC_ERR_ARG,
+                "prefill not supported for this problem (seq_len %lld, dim %lld, k %lld, "
+                "kernel_size %lld%s); see moc_prefill_supported",
+                (long long)seq_len, (long long)dim, (long long)k, (long long)kernel_size,
+                has_cache && seq_len < kernel_size - 1 ? ", seq_len < kernel_size - 1 with a cache" : "");
+  return MOC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moc_forward_prefill(const void* x, const void* alpha, const void* basis, void* y,
+                        const void* cache, void* final_state, int64_t n_seqs, int64_t seq_len,
+                        int64_t dim, int64_t k, int64_t kernel_size, int x_dtype,
+                        int alpha_dtype, int basis_dtype, int activation, int routing,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem p;
+  int rc = prefill_problem(n_seqs, seq_len, dim, k, kernel_size, x_dtype, alpha_dtype, basis_dtype,
+                           activation, routing, cache != nullptr, p);
+  if (rc != MOC_OK) return rc;
+  if (!x || !alpha || !basis || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
+  const size_t need = forward_bytes(p);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  moc::mfma::forward_prefill(p, x, alpha, basis, y, cache, final_state, workspace,
+                             static_cast<hipStream_t>(stream));
+  return hip_status("moc_forward_prefill launch");
+}
+
+int moc_backward_prefill(const void* x, const void* alpha, const void* basis, const void* dy,
+                         int64_t dy_row_stride, const void* cache, void* dx, void* dalpha,
+                         void* dbasis, void* dcache, int64_t n_seqs, int64_t seq_len, int64_t dim,
+                         int64_t k, int64_t kernel_size, int x_dtype, int alpha_dtype,
+                         int basis_dtype, int activation, int routing, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  moc::Problem p;
+  int rc = prefill_problem(n_seqs, seq_len, dim, k, kernel_size, x_dtype, alpha_dtype, basis_dtype,
+                           activation, routing, true, p);
+  if (rc != MOC_OK) return rc;
+  if (!x || !alpha || !basis || !dy || !cache || !dalpha || !dbasis)
+    return fail(MOC_ERR_ARG, "null tensor pointer");
+  if (dy_row_stride != 0 && dy_row_stride != dim)
+    return fail(MOC_ERR_ARG, "dy_row_stride must be dim (%lld) or 0, got %lld", (long long)dim,
+                (long long)dy_row_stride);
+  if ((p.n_tokens + 255) / 256 > 65535)
+    return fail(MOC_ERR_ARG, "n_tokens too large for the backward grid: %lld",
+                (long long)p.n_tokens);
+  p.dy_stride = dy_row_stride;
+  const size_t need = backward_bytes(p);
+  if (workspace_bytes < need || !workspace)
+    return fail(MOC_ERR_WORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                workspace_bytes);
+  moc::mfma::backward_prefill(p, x, alpha, basis, dy, cache, dx, dalpha, dbasis, dcache, workspace,
+                              static_cast<hipStream_t>(stream));
+  return hip_status("moc_backward_prefill launch");
+}
 
 }  // extern "C"
 

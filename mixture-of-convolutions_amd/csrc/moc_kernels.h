@@ -59,6 +59,18 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
               const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
               hipStream_t st);
 
+// Prefill from a cache (moc/api.py:299-309): fixed-length sequences
+// (p.seq.seq_len tokens each; at least S-1 with a cache).  cache [n_seqs, D, S]
+// in the x dtype (or null: zero history); fin (or null) receives the final
+// state [n_seqs, D, S]; dcache (or null) the cache gradient.  The workspaces
+// are those of forward / backward.
+bool prefill_supported(const Problem& p, bool has_cache);
+void forward_prefill(const Problem& p, const void* x, const void* alpha, const void* basis,
+                     void* y, const void* cache, void* fin, void* workspace, hipStream_t st);
+void backward_prefill(const Problem& p, const void* x, const void* alpha, const void* basis,
+                      const void* dy, const void* cache, void* dx, void* dalpha, void* dbasis,
+                      void* dcache, void* workspace, hipStream_t st);
+
 // Grouped layers: layer i is problem ps[i] (one token axis; K, S, activation
 // shared) on tensors io[i]; layers_grouped tells whether they can run as one
 // launch per pass (bf16, at most 4 layers).

@@ -138,7 +138,11 @@ struct Buf {
   }
   template <int BYTES>
   __device__ __forceinline__ void store(uint32_t off, const void* src) const {
-    if constexpr (BYTES == 4) {
+    if constexpr (BYTES == 2) {
+      uint16_t v;
+      __builtin_memcpy(&v, src, 2);
+      __builtin_amdgcn_raw_buffer_store_b16(v, r, static_cast<int>(off), 0, 0);
+    } else if constexpr (BYTES == 4) {
       uint32_t v;
       __builtin_memcpy(&v, src, 4);
       __builtin_amdgcn_raw_buffer_store_b32(v, r, static_cast<int>(off), 0, 0);
@@ -209,6 +213,99 @@ __device__ __forceinline__ void tap_bits_rows(const SeqLayout& seq, int64_t row0
 }
 
 // ---------------------------------------------------------------------------
+// Prefill from a cache (moc/api.py:299-309, 218-227): fixed-length sequences of
+// T = seq.seq_len tokens, T >= S-1, each continuing the S inputs its cache
+// holds.  The reference prepends the cache to x with zero routing and drops
+// those outputs; here the taps that reach before a sequence's first token read
+// the cache where the plain kernels read nothing:
+//   hist [n_seqs, D, S] (contiguous, slot S-1 the newest input), or null for a
+//     zero history; tap s of the sequence's token pos < S-1-s reads slot
+//     s + 1 + pos;
+//   fin [n_seqs, D, S] (or null) receives each sequence's last S inputs (the
+//     state a later call continues from), slot S-1 the last token; with T < S
+//     its oldest S-T slots are the cache's newest ones (zeros without a cache).
+struct Pre {
+  const void* hist;
+  void* fin;
+};
+
+// History value of window rows u0 + w (w < NW) for this lane's channels: with
+// T >= S-1 the taps that reach row u from a later sequence all belong to the
+// first sequence starting after u (at st, u >= st - (S-1)), and read its cache
+// slot S - (st - u).  Rows that no masked tap reads get zero.
+template <int S, int NW, int NC, typename E>
+__device__ __forceinline__ void hist_window(const Buf& hb, int64_t u0, int64_t T, int64_t N,
+                                            int64_t D, int64_t dl, bool ch_ok,
+                                            float (&hx)[NW][NC]) {
+  // sequence b starting at st = b T: the first start after u0 (token indices
+  // stay below 2^31)
+  int64_t b = 0;
+  if (u0 >= 0) b = static_cast<int64_t>(static_cast<uint32_t>(u0) / static_cast<uint32_t>(T)) + 1;
+  int64_t st = b * T;
+  constexpr uint32_t ESZ = sizeof(E);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int64_t u = u0 + w;
+    const int64_t m = st - u;  // >= 1
+    const bool on = ch_ok && m <= S - 1 && st < N;
+    const uint32_t off = static_cast<uint32_t>(((b * D + dl) * S + (S - m)) * ESZ);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      E v;
+      hb.load<ESZ>(on ? off + c * S * ESZ : kOffNone, &v);
+      if constexpr (sizeof(E) == 2) hx[w][c] = bf16_to_f32(v);
+      else hx[w][c] = v;
+    }
+    if (u + 1 == st) {
+      st += T;
+      ++b;
+    }
+  }
+}
+
+// Final-state rows of a super-block [t0, t0 + TB): this lane's run trun + r
+// (r < R) with x values xw[r + S - 1]; writes fin for the rows within S of
+// their sequence's end, and the cache part of the state for T < S.
+template <int S, int R, int NC, typename E>
+__device__ __forceinline__ void fin_rows(const Pre& pre, const Buf& hb, int64_t trun, int64_t T,
+                                         int64_t N, int64_t D, int64_t dl, bool ch_ok,
+                                         const float (&xw)[R + S - 1][NC]) {
+  constexpr uint32_t ESZ = sizeof(E);
+  const Buf fb(pre.fin, N / T * D * S * ESZ);
+  // sequence b and position pos of row trun (token indices stay below 2^31)
+  int64_t b = static_cast<int64_t>(static_cast<uint32_t>(trun) / static_cast<uint32_t>(T));
+  int64_t pos = trun - b * T;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t t = trun + r;
+    const bool live = ch_ok && t < N;
+    const int64_t slot = S - (T - pos);
+    const uint32_t base = static_cast<uint32_t>((b * D + dl) * S * ESZ);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      E v;
+      if constexpr (sizeof(E) == 2) v = f32_to_bf16(xw[r + S - 1][c]);
+      else v = xw[r + S - 1][c];
+      fb.store<ESZ>(live && slot >= 0 ? base + static_cast<uint32_t>((c * S + slot) * ESZ) : kOffNone, &v);
+    }
+    if (T < S && pos == 0) {
+      // the oldest S - T slots: the cache's slots T.. (zero without a cache)
+      for (int jj = 0; jj < S - T; ++jj)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          E v;
+          hb.load<ESZ>(live && pre.hist ? base + static_cast<uint32_t>((c * S + jj + T) * ESZ) : kOffNone, &v);
+          fb.store<ESZ>(live ? base + static_cast<uint32_t>((c * S + jj) * ESZ) : kOffNone, &v);
+        }
+    }
+    if (++pos == T) {
+      pos = 0;
+      ++b;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Layer tables of a grouped launch.  The MoC layers of one launch share the
 // token axis (sequence layout), K, S, activation and compute dtype; each has its
 // own tensors, channel count and the grid its own launch would use, and the
@@ -267,13 +364,14 @@ __device__ __forceinline__ int layer_index(const LT& ly, int blk) {
 // ranges of n_sb super-blocks.  No LDS, no barriers: every wave walks its
 // super-blocks on its own, loading the rows of super-block i+1 (x window and
 // routing weights, raw) before it computes super-block i.  fwd_tile is the
-// work of workgroup (bx, by) of one layer.
-template <int S, int KC, int NB, int NC, bool ACT, bool BF>
+// work of workgroup (bx, by) of one layer.  PRE: prefill from a cache (Pre;
+// fixed-length sequences).
+template <int S, int KC, int NB, int NC, bool ACT, bool BF, bool PRE = false>
 __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
                                          const typename CT<BF>::elem* __restrict__ a_c,
                                          const typename CT<BF>::elem* __restrict__ b_c,
                                          void* __restrict__ yv, SeqLayout seq, int64_t D, int n_sb,
-                                         int bx, int by) {
+                                         int bx, int by, Pre pre = Pre{nullptr, nullptr}) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -299,6 +397,9 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
   const Buf yb(y + row_lo * D, (row_hi - row_lo) * D * ESZ);
   const Buf ab(a_c + tbase * KP, (row_hi - tbase) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
+  // PRE: the cache (n_seqs = N / T sequences)
+  const int64_t T = seq.seq_len;
+  const Buf hb(PRE ? pre.hist : nullptr, PRE && pre.hist ? N / T * D * S * ESZ : 0);
 
   // basis B operands: bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c], v = 0..3
   Op bop[NC][S][KC];
@@ -368,6 +469,13 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
 #pragma unroll
         for (int r = 0; r < R; ++r) ok[r] = (1u << S) - 1u;
       }
+      // PRE: masked taps read the cache (uniform: is there one?)
+      float hx[PRE && MASK ? W : 1][NC];
+      bool use_h = false;
+      if constexpr (PRE && MASK) {
+        use_h = pre.hist != nullptr;
+        if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
+      }
       float acc[R][NC];
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -390,6 +498,7 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
             for (int v = 0; v < 4; ++v) {
               const int r = 4 * b + v;
               if (!MASK || ((ok[r] >> s) & 1u)) acc[r][c] = fmaf(xw[r + s][c], w[v], acc[r][c]);
+              else if (PRE && MASK && use_h) acc[r][c] = fmaf(hx[PRE && MASK ? r + s : 0][c], w[v], acc[r][c]);
             }
           }
       }
@@ -403,6 +512,13 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
     };
     if (interior) body(std::false_type{});
     else body(std::true_type{});
+    if constexpr (PRE) {
+      // final state: does a sequence end within S rows after this super-block's rows?
+      if (pre.fin != nullptr) {
+        const int64_t e1 = (t0 / T + 1) * T;  // first sequence end after t0 (uniform)
+        if (e1 - S <= t0 + TB - 1) fin_rows<S, R, NC, E>(pre, hb, trun, T, N, D, dl, ch_ok, xw);
+      }
+    }
   }
 }
 
@@ -413,6 +529,16 @@ fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict_
            int64_t D, int n_sb) {
   fwd_tile<S, KC, NB, NC, ACT, BF>(xv, a_c, b_c, yv, seq, D, n_sb, static_cast<int>(blockIdx.x),
                                    static_cast<int>(blockIdx.y));
+}
+
+// Prefill from a cache (Pre), same grid as fwd_kernel.
+template <int S, int KC, int NB, int NC, bool ACT, bool BF>
+__global__ void __launch_bounds__(256)
+fwd_pre_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict__ a_c,
+               const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ yv, SeqLayout seq,
+               int64_t D, int n_sb, Pre pre) {
+  fwd_tile<S, KC, NB, NC, ACT, BF, true>(xv, a_c, b_c, yv, seq, D, n_sb, static_cast<int>(blockIdx.x),
+                                         static_cast<int>(blockIdx.y), pre);
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another).
@@ -583,14 +709,18 @@ constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2 && BF) ? 1
                              : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
 // bwd_tile is the work of workgroup (bx, by) (route half zh with SPLIT) of
-// one layer; the __global__ wrappers below map the grid onto it.
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
+// one layer; the __global__ wrappers below map the grid onto it.  PRE (fused
+// pass only): prefill from a cache, whose values the masked taps read in P and
+// in the m products (the cache gradient is not formed here).
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE,
+          bool PRE = false>
 __device__ __forceinline__ void
 bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
          const typename CT<BF>::elem* __restrict__ a_c,
          const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
          float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
-         int bx, int by, int zh, int gy, int gy1, int n_old, int n_total) {
+         int bx, int by, int zh, int gy, int gy1, int n_old, int n_total,
+         Pre pre = Pre{nullptr, nullptr}) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -614,6 +744,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(MODE == kBwdFused || (BF && !ACT && S % 2 == 0),
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
+  static_assert(!PRE || (MODE == kBwdFused && !SPLIT), "prefill runs the fused pass");
   constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
   // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, S/2) and
   // [S/2, S): x and dy rows are read once per workgroup and the dalpha sum over
@@ -691,6 +822,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   const Buf dyb(dy + row_lo * dys, ((row_hi - row_lo - 1) * dys + D) * ESZ);
   const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
+  // PRE: the cache (n_seqs = N / T sequences)
+  const int64_t T = seq.seq_len;
+  const Buf hb(PRE ? pre.hist : nullptr, PRE && pre.hist ? N / T * D * S * ESZ : 0);
 
   // W operands (P, dx): bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
   Op bop[NC][S][KC];
@@ -860,6 +994,14 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
         for (int r = 0; r < NOK; ++r) ok[r] = (1u << S) - 1u;
       }
+      // PRE: masked taps read the cache (uniform: is there one?)
+      constexpr bool HX = PRE && MASK;
+      float hx[HX ? W : 1][NC];
+      bool use_h = false;
+      if constexpr (HX) {
+        use_h = pre.hist != nullptr;
+        if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
+      }
 
       if (ACT) {
         float p[R][NC];
@@ -892,6 +1034,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
           for (int v = 0; v < 4; ++v) {
             const int r = 4 * b + v;
             if (!MASK || ((ok[r] >> s) & 1u)) p[r][c] = fmaf(xw[r + s][c], wq[jb][v], p[r][c]);
+            else if (HX && use_h) p[r][c] = fmaf(hx[HX ? r + s : 0][c], wq[jb][v], p[r][c]);
           }
         }
         // g *= silu'(P) = sg (1 + P (1 - sg)), sg = sigmoid(P) as sigmoid_f forms
@@ -1041,7 +1184,8 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                   for (int v = 0; v < 4; ++v) {
                     const int r = 4 * b + v;
                     const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
-                    const float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                    float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                    if (HX && use_h && !on) mval = g[r][c] * hx[HX ? r + s : 0][c];
                     hb[v] = __float_as_uint(mval) & 0xffff0000u;
                     lo[v] = mval - __uint_as_float(hb[v]);
                   }
@@ -1107,7 +1251,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 E parts[NP];
-                MS::split(on ? g[r][c] * xw[r + s][c] : 0.f, parts);
+                float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                if (HX && use_h && !on) mval = g[r][c] * hx[HX ? r + s : 0][c];
+                MS::split(mval, parts);
 #pragma unroll
                 for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
               }
@@ -1250,6 +1396,26 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(xv, dyv, dys, a_c, b_c, dxv, part_da, part_db,
                                                      seq, D, bx, by, zh, gy, gy1, n_old, n_total);
+}
+
+// Prefill from a cache (Pre): the fused pass on a 2-D grid (bf16 with 32
+// routes, which the plain backward splits, at one wave per SIMD: both route
+// chunks' accumulators and operands stay in registers; with 8 taps at two, as
+// LLVM's AGPR-copy rewrite crashes on the one-wave form).
+template <int S, int KC, bool BF>
+constexpr int kBwdPreWaves = (BF && KC >= 2 && S < 8) ? 1
+                             : (BF && KC >= 2) ? 2 : kBwdMinWaves<S, KC, kBwdFused, BF>;
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(kBwdPreWaves<S, KC, BF>)))
+bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
+               const typename CT<BF>::elem* __restrict__ a_c,
+               const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
+               float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
+               int gx, int gy, int gy1, int n_old, int n_total, Pre pre) {
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, false, kBwdFused, true>(
+      xv, dyv, dys, a_c, b_c, dxv, part_da, part_db, seq, D, static_cast<int>(blockIdx.x),
+      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre);
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another:

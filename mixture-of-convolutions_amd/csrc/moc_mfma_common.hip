@@ -213,6 +213,71 @@ stage2_layers_kernel(Stage2Layers ly, int64_t N, int K, int S, int64_t da_blocks
 }
 
 // ---------------------------------------------------------------------------
+// Cache gradient of a prefill (one thread per channel d of sequence b): the
+// outputs of the sequence's first S-1 tokens read the cache (slot s + 1 + pos
+// for tap s < S-1-pos of token pos), so
+//   dcache[b, d, j] = sum over pos < S-1, s = j - 1 - pos >= 0 of g[t, d] W[t, s, d]
+// (t = b T + pos; slot 0 is read by no kept output and gets zero), with W from the
+// kernels' operands and, with SiLU, g = dy silu'(P) recomputed in fp32.
+template <int S, bool BF>
+__global__ void __launch_bounds__(256)
+hist_grad_kernel(const typename CT<BF>::elem* __restrict__ x,
+                 const typename CT<BF>::elem* __restrict__ a_c,
+                 const typename CT<BF>::elem* __restrict__ b_c,
+                 const typename CT<BF>::elem* __restrict__ dy, int64_t dys,
+                 const typename CT<BF>::elem* __restrict__ hist,
+                 typename CT<BF>::elem* __restrict__ dcache, int64_t T, int64_t D, int KP, int act) {
+  using C = CT<BF>;
+  constexpr int NP = S - 1;  // tokens of a sequence whose taps reach the cache (T >= S-1)
+  const int64_t b = blockIdx.y;
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (d >= D) return;
+  const int64_t t0 = b * T;
+  float w[NP][S];
+#pragma unroll
+  for (int pos = 0; pos < NP; ++pos)
+#pragma unroll
+    for (int s = 0; s < S; ++s) w[pos][s] = 0.f;
+  for (int k = 0; k < KP; ++k) {
+    float bs[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) bs[s] = C::to_f(b_c[(static_cast<int64_t>(k) * S + s) * D + d]);
+#pragma unroll
+    for (int pos = 0; pos < NP; ++pos) {
+      const float a = C::to_f(a_c[(t0 + pos) * KP + k]);
+#pragma unroll
+      for (int s = 0; s < S; ++s) w[pos][s] = fmaf(a, bs[s], w[pos][s]);
+    }
+  }
+  float hv[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) hv[s] = C::to_f(hist[(b * D + d) * S + s]);
+  float dc[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) dc[s] = 0.f;
+#pragma unroll
+  for (int pos = 0; pos < NP; ++pos) {
+    const int64_t t = t0 + pos;
+    float g = C::to_f(dy[t * dys + d]);
+    if (act) {
+      float p = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int src = pos - (S - 1 - s);
+        const float xv = src >= 0 ? C::to_f(x[(t0 + src) * D + d]) : hv[src >= 0 ? 0 : s + 1 + pos];
+        p = fmaf(xv, w[pos][s], p);
+      }
+      const float sg = sigmoid_f(p);
+      g *= sg * (1.f + p * (1.f - sg));
+    }
+#pragma unroll
+    for (int s = 0; s < S - 1 - pos; ++s) dc[s + 1 + pos] = fmaf(g, w[pos][s], dc[s + 1 + pos]);
+  }
+#pragma unroll
+  for (int s = 0; s < S; ++s) dcache[(b * D + d) * S + s] = C::from_f(dc[s]);
+}
+
+// ---------------------------------------------------------------------------
 // workspace plans
 
 namespace {
@@ -293,6 +358,34 @@ void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void
   }
 }
 
+// Backward stage 2 of one problem on its plan's partials.
+void launch_stage2(const Problem& p, const Plan& pl, bool dir, char* ws, const void* alpha,
+                   void* dalpha, void* dbasis, hipStream_t st) {
+  float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
+  float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
+  const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
+  const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
+  const int grad = route_grad(p.routing);
+  // weights for the activation gradient: prep's fp32 copy, or the caller's
+  // bf16 weights read in place
+  const float* a_r = (grad != ROUTE_ALPHA && !dir)
+                         ? reinterpret_cast<const float*>(ws + pl.off_ar) : nullptr;
+  const auto* a_w = static_cast<const uint16_t*>(alpha);
+  const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
+  const int64_t n_da = pl.bg.gx;
+  if (pl.KP == 16) {
+    hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda, n_da, pdb,
+                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
+                       p.b_dt, p.n_tokens,
+                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
+  } else {
+    hipLaunchKernelGGL(stage2_kernel<2>, grid, dim3(256), 0, st, pda, n_da, pdb,
+                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
+                       p.b_dt, p.n_tokens,
+                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
+  }
+}
+
 }  // namespace
 
 bool supported(const Problem& p) {
@@ -354,26 +447,99 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     default: break;
   }
   prof_end(p, st);
-  const int64_t db_blocks = cdiv(p.K * p.S * p.D, 256);
-  const int64_t da_blocks = cdiv(p.n_tokens * 16, 256);
-  const int grad = route_grad(p.routing);
-  // weights for the activation gradient: prep's fp32 copy, or the caller's
-  // bf16 weights read in place
-  const float* a_r = (grad != ROUTE_ALPHA && !dir)
-                         ? reinterpret_cast<const float*>(ws + pl.off_ar) : nullptr;
-  const auto* a_w = static_cast<const uint16_t*>(alpha);
-  const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
-  const int64_t n_da = pl.bg.gx;
-  if (pl.KP == 16) {
-    hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda, n_da, pdb,
-                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
-                       p.b_dt, p.n_tokens,
-                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
-  } else {
-    hipLaunchKernelGGL(stage2_kernel<2>, grid, dim3(256), 0, st, pda, n_da, pdb,
-                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
-                       p.b_dt, p.n_tokens,
-                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
+  launch_stage2(p, pl, dir, ws, alpha, dalpha, dbasis, st);
+}
+
+bool prefill_supported(const Problem& p, bool has_cache) {
+  if (!supported(p) || p.seq.cu != nullptr || p.seq.seq_len <= 0 ||
+      p.n_tokens % p.seq.seq_len != 0)
+    return false;
+  if (has_cache && p.seq.seq_len < p.S - 1) return false;
+  // the cache gradient's grid has one y block per sequence
+  if (p.n_tokens / p.seq.seq_len > 65535) return false;
+  // the cache / final state are addressed with 32-bit byte offsets
+  const int64_t esz = p.x_dt == DT_BF16 ? 2 : 4;
+  return p.n_tokens / p.seq.seq_len * p.D * p.S * esz < (int64_t(1) << 31);
+}
+
+void forward_prefill(const Problem& p, const void* x, const void* alpha, const void* basis,
+                     void* y, const void* cache, void* fin, void* workspace, hipStream_t st) {
+  const Plan pl = plan(p, false);
+  char* ws = static_cast<char*>(workspace);
+  const bool dir = direct(p, alpha, basis, nullptr);
+  const void* a_c = alpha;
+  const void* b_c = basis;
+  if (!dir) {
+    launch_prep(p, pl, alpha, basis, ws, false, st);
+    a_c = ws + pl.off_ac;
+    b_c = ws + pl.off_bc;
+  }
+  const Pre pre{cache, fin};
+  prof_begin(p, st);
+  switch (p.S) {
+    case 2: launch_fwd_pre<2>(p, x, a_c, b_c, y, pre, st); break;
+    case 3: launch_fwd_pre<3>(p, x, a_c, b_c, y, pre, st); break;
+    case 4: launch_fwd_pre<4>(p, x, a_c, b_c, y, pre, st); break;
+    case 8: launch_fwd_pre<8>(p, x, a_c, b_c, y, pre, st); break;
+    default: break;
+  }
+  prof_end(p, st);
+}
+
+template <int S, bool BF>
+void hist_grad_one(const Problem& p, const void* x, const void* a_c, const void* b_c,
+                   const void* dy, const void* cache, void* dcache, int KP, hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const int64_t B = p.n_tokens / p.seq.seq_len;
+  hipLaunchKernelGGL((hist_grad_kernel<S, BF>),
+                     dim3(static_cast<unsigned>(cdiv(p.D, 256)), static_cast<unsigned>(B)),
+                     dim3(256), 0, st, static_cast<const E*>(x), static_cast<const E*>(a_c),
+                     static_cast<const E*>(b_c), static_cast<const E*>(dy), p.dy_stride,
+                     static_cast<const E*>(cache), static_cast<E*>(dcache), p.seq.seq_len, p.D, KP,
+                     p.activation);
+}
+
+void backward_prefill(const Problem& p, const void* x, const void* alpha, const void* basis,
+                      const void* dy, const void* cache, void* dx, void* dalpha, void* dbasis,
+                      void* dcache, void* workspace, hipStream_t st) {
+  const Plan pl = plan(p, true);
+  char* ws = static_cast<char*>(workspace);
+  const bool dir = direct(p, alpha, basis, dalpha);
+  const void* a_c = alpha;
+  const void* b_c = basis;
+  if (!dir) {
+    launch_prep(p, pl, alpha, basis, ws, true, st);
+    a_c = ws + pl.off_ac;
+    b_c = ws + pl.off_bc;
+  }
+  float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
+  float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
+  const Pre pre{cache, nullptr};
+  prof_begin(p, st);
+  switch (p.S) {
+    case 2: launch_bwd_pre<2>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 3: launch_bwd_pre<3>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 4: launch_bwd_pre<4>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 8: launch_bwd_pre<8>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    default: break;
+  }
+  prof_end(p, st);
+  launch_stage2(p, pl, dir, ws, alpha, dalpha, dbasis, st);
+  if (dcache != nullptr) {
+    const bool bf = p.x_dt == DT_BF16;
+#define MOC_HG(S_)                                                              \
+  case S_:                                                                      \
+    if (bf) hist_grad_one<S_, true>(p, x, a_c, b_c, dy, cache, dcache, pl.KP, st); \
+    else hist_grad_one<S_, false>(p, x, a_c, b_c, dy, cache, dcache, pl.KP, st);   \
+    break;
+    switch (p.S) {
+      MOC_HG(2)
+      MOC_HG(3)
+      MOC_HG(4)
+      MOC_HG(8)
+      default: break;
+    }
+#undef MOC_HG
   }
 }
 

@@ -359,13 +359,88 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
 #undef MOC_BWD
 }
 
+// Prefill from a cache (Pre, fixed-length sequences): the forward on
+// fwd_kernel's grid; the backward's fused pass (for every K, activation and
+// dtype) on the grid that owns the partials, so the workspace and stage 2 are
+// those of moc_backward.
+template <int S, int KC, bool ACT, bool BF>
+void fwd_pre_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
+                 const Pre& pre, hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const Grid2 g = fwd_grid(p.n_tokens, p.D);
+  hipLaunchKernelGGL((fwd_pre_kernel<S, KC, kFwdNB, kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256),
+                     0, st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq,
+                     p.D, g.n_sb, pre);
+}
+
+template <int S, int KC, bool ACT, bool BF>
+void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_c,
+                 const void* b_c, void* dx, float* part_da, float* part_db, const Pre& pre,
+                 hipStream_t st) {
+  using E = typename CT<BF>::elem;
+  const Grid2 g = bwd_partials_grid(p);
+  hipLaunchKernelGGL((bwd_pre_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF>), dim3(g.gx, g.gy),
+                     dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, static_cast<const E*>(a_c),
+                     static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D,
+                     static_cast<int>(g.gx), static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total,
+                     pre);
+}
+
+template <int S>
+void launch_fwd_pre(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
+                    const Pre& pre, hipStream_t st) {
+  const int kc = static_cast<int>((p.K + 15) / 16);
+  const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
+#define MOC_FWD(KC_)                                                        \
+  if (kc == KC_) {                                                          \
+    if (bf) {                                                               \
+      if (act) fwd_pre_one<S, KC_, true, true>(p, x, a_c, b_c, y, pre, st); \
+      else fwd_pre_one<S, KC_, false, true>(p, x, a_c, b_c, y, pre, st);    \
+    } else {                                                                \
+      if (act) fwd_pre_one<S, KC_, true, false>(p, x, a_c, b_c, y, pre, st); \
+      else fwd_pre_one<S, KC_, false, false>(p, x, a_c, b_c, y, pre, st);   \
+    }                                                                       \
+    return;                                                                 \
+  }
+  MOC_FWD(1)
+  MOC_FWD(2)
+#undef MOC_FWD
+}
+
+template <int S>
+void launch_bwd_pre(const Problem& p, const void* x, const void* dy, const void* a_c,
+                    const void* b_c, void* dx, float* part_da, float* part_db, const Pre& pre,
+                    hipStream_t st) {
+  const int kc = static_cast<int>((p.K + 15) / 16);
+  const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
+#define MOC_BWD(KC_)                                                                                \
+  if (kc == KC_) {                                                                                  \
+    if (bf) {                                                                                       \
+      if (act) bwd_pre_one<S, KC_, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, pre, st);  \
+      else bwd_pre_one<S, KC_, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, pre, st);     \
+    } else {                                                                                        \
+      if (act) bwd_pre_one<S, KC_, true, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, pre, st); \
+      else bwd_pre_one<S, KC_, false, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, pre, st);    \
+    }                                                                                               \
+    return;                                                                                         \
+  }
+  MOC_BWD(1)
+  MOC_BWD(2)
+#undef MOC_BWD
+}
+
 #define MOC_DECLARE_S(S_)                                                                     \
   extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
                                       void*, hipStream_t);                                    \
   extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
                                       const void*, void*, float*, float*, hipStream_t);       \
   extern template void launch_fwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t); \
-  extern template void launch_bwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t);
+  extern template void launch_bwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t); \
+  extern template void launch_fwd_pre<S_>(const Problem&, const void*, const void*, const void*, \
+                                          void*, const Pre&, hipStream_t);                    \
+  extern template void launch_bwd_pre<S_>(const Problem&, const void*, const void*, const void*, \
+                                          const void*, void*, float*, float*, const Pre&,     \
+                                          hipStream_t);
 MOC_DECLARE_S(2)
 MOC_DECLARE_S(3)
 MOC_DECLARE_S(4)

@@ -10,6 +10,10 @@ template void launch_bwd<2>(const Problem&, const void*, const void*, const void
                              void*, float*, float*, hipStream_t);
 template void launch_fwd_layers<2>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_bwd_layers<2>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_fwd_pre<2>(const Problem&, const void*, const void*, const void*, void*,
+                                 const Pre&, hipStream_t);
+template void launch_bwd_pre<2>(const Problem&, const void*, const void*, const void*, const void*,
+                                 void*, float*, float*, const Pre&, hipStream_t);
 
 }  // namespace mfma
 }  // namespace moc

@@ -10,6 +10,10 @@ template void launch_bwd<4>(const Problem&, const void*, const void*, const void
                              void*, float*, float*, hipStream_t);
 template void launch_fwd_layers<4>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_bwd_layers<4>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_fwd_pre<4>(const Problem&, const void*, const void*, const void*, void*,
+                                 const Pre&, hipStream_t);
+template void launch_bwd_pre<4>(const Problem&, const void*, const void*, const void*, const void*,
+                                 void*, float*, float*, const Pre&, hipStream_t);
 
 }  // namespace mfma
 }  // namespace moc

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
@@ -39,6 +39,9 @@ EXPORTED_SYMBOLS = (
     "moc_forward_layers",
     "moc_backward_layers_workspace_bytes",
     "moc_backward_layers",
+    "moc_prefill_supported",
+    "moc_forward_prefill",
+    "moc_backward_prefill",
     "moc_update",
     "moc_profile_events",
     "moc_decode_step_supported",
@@ -106,6 +109,29 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_backward.restype = _i
     lib.moc_backward_noalloc.argtypes = bwd + [_p]   # stream
     lib.moc_backward_noalloc.restype = _i
+    lib.moc_prefill_supported.argtypes = [_l, _l, _l, _l, _l, _i, _i]
+    lib.moc_prefill_supported.restype = _i
+    lib.moc_forward_prefill.argtypes = [
+        _p, _p, _p, _p,            # x, alpha, basis, y
+        _p, _p,                    # cache, final_state
+        _l, _l,                    # n_seqs, seq_len
+        _l, _l, _l,                # dim, k, kernel_size
+        _i, _i, _i,                # dtypes
+        _i, _i,                    # activation, routing
+        _p, _z, _p,                # workspace, bytes, stream
+    ]
+    lib.moc_forward_prefill.restype = _i
+    lib.moc_backward_prefill.argtypes = [
+        _p, _p, _p, _p, _l,        # x, alpha, basis, dy, dy_row_stride
+        _p,                        # cache
+        _p, _p, _p, _p,            # dx, dalpha, dbasis, dcache
+        _l, _l,                    # n_seqs, seq_len
+        _l, _l, _l,                # dim, k, kernel_size
+        _i, _i, _i,                # dtypes
+        _i, _i,                    # activation, routing
+        _p, _z, _p,                # workspace, bytes, stream
+    ]
+    lib.moc_backward_prefill.restype = _i
     lib.moc_set_kernel_path.argtypes = [_i]
     lib.moc_set_kernel_path.restype = _i
     for name in ("moc_forward_layers", "moc_backward_layers"):

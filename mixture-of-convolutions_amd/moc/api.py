@@ -372,15 +372,67 @@ def _step(x, a, basis, cache, activation, router_activation):
     return y[:, None]
 
 
-def _prefill(x, a, basis, cache, activation, router_activation):
-    """Prefill continuing from a cache (moc/api.py:299-307).  The reference
-    prepends the whole cache to x (and zero routing to a) and drops the first
-    S outputs.  Only the first S-1 tokens of each sequence have taps that reach
-    into the cache, so here the op runs on x as it is, and those tokens are
-    recomputed from a short window (the S-1 newest cached tokens, then the
-    tokens themselves) and written over the first result.  No copy of x; y is
-    the reference's bit for bit (each token's output depends only on its own
-    window), and gradients flow to x, a, basis and the cache as there."""
+class _MoCPrefillFunction(torch.autograd.Function):
+    """Prefill continuing from a cache (moc/api.py:299-309) with its final
+    state (moc/api.py:218-227) on the library's prefill entries: one forward
+    launch whose taps that reach before a sequence's first token read the
+    cache, and which writes the final state; one backward call that also forms
+    the cache gradient.  Returns (y, final state or None); a gradient of the
+    final state (a slice of x and the cache) is added to dx / dcache here."""
+
+    @staticmethod
+    def forward(ctx, x, a, basis, cache, activation, routing, want_state):
+        x, a, basis = x.contiguous(), a.contiguous(), basis.contiguous()
+        act = activation_flag(activation)
+        y, fin = ops.launch_forward_prefill(x, a, basis, cache, activation_flag=act,
+                                            final_state=want_state, routing=routing)
+        ctx.save_for_backward(x, a, basis, cache)
+        ctx.act = act
+        ctx.routing = routing
+        ctx.set_materialize_grads(False)
+        return y, fin
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy, dfin):
+        x, a, basis, cache = ctx.saved_tensors
+        B, T, _ = x.shape
+        S = basis.shape[1]
+        if dy is None:
+            dy = torch.zeros_like(x)
+        need_x = ctx.needs_input_grad[0] or dfin is not None
+        dx, da, db, dc = ops.launch_backward_prefill(
+            x, a, basis, cache, dy, activation_flag=ctx.act, need_x=need_x,
+            need_cache=ctx.needs_input_grad[3], routing=ctx.routing)
+        if dfin is not None:
+            n = min(S, T)
+            dx[:, T - n:] += dfin[:, :, S - n:].transpose(1, 2).to(dx.dtype)
+            if T < S and dc is not None:
+                dc[:, :, T:] += dfin[:, :, :S - T].to(dc.dtype)
+        return (dx if ctx.needs_input_grad[0] else None), da, db, dc, None, None, None
+
+
+def _prefill(x, a, basis, cache, activation, router_activation, output_final_state):
+    """Prefill continuing from a cache (moc/api.py:299-309): (y, final state or
+    None).  On the library's prefill entries where they take the shape
+    (_MoCPrefillFunction), else by _prefill_window."""
+    routing = ROUTE_ALPHA if router_activation is None else _ROUTING_CODES[router_activation]
+    if ops.prefill_supported(x, basis, with_cache=True):
+        return _MoCPrefillFunction.apply(x, a, basis, cache, activation, routing,
+                                         output_final_state)
+    y = _prefill_window(x, a, basis, cache, activation, router_activation)
+    return y, (_final_state(x, cache, basis.shape[1]) if output_final_state else None)
+
+
+def _prefill_window(x, a, basis, cache, activation, router_activation):
+    """Prefill without the prefill entries.  The reference prepends the whole
+    cache to x (and zero routing to a) and drops the first S outputs.  Only the
+    first S-1 tokens of each sequence have taps that reach into the cache, so
+    here the op runs on x as it is, and those tokens are recomputed from a
+    short window (the S-1 newest cached tokens, then the tokens themselves) and
+    written over the first result.  No copy of x; y is the reference's bit for
+    bit (each token's output depends only on its own window), and gradients
+    flow to x, a, basis and the cache as there."""
     B, T, _ = x.shape
     KS = basis.shape[1]
     y = _apply(x, a, basis, activation, router_activation)
@@ -409,7 +461,8 @@ def _dispatch(x, a, basis, cache, output_final_state, activation, router_activat
             if T == 1:
                 y = _step(x, a, basis, cache, activation, router_activation)
                 return y, (cache if output_final_state else None)
-            y = _prefill(x, a, basis, cache, activation, router_activation)
+            return _prefill(x, a, basis, cache, activation, router_activation,
+                            output_final_state)
         else:
             y = _apply(x, a, basis, activation, router_activation)
         return y, (_final_state(x, cache, KS) if output_final_state else None)

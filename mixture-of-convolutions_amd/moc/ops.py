@@ -232,6 +232,103 @@ def launch_backward(
     return dx, dalpha, dbasis
 
 
+def prefill_supported(x: torch.Tensor, basis: torch.Tensor, with_cache: bool) -> bool:
+    """Whether moc_forward_prefill / moc_backward_prefill take a [B, T, D] x
+    with this basis (matrix-core shapes; T >= kernel_size - 1 with a cache)."""
+    B, T, D = x.shape
+    K, S, _ = basis.shape
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        return False
+    return bool(_lib.lib().moc_prefill_supported(B, T, D, K, S, _lib.dtype_code(x.dtype),
+                                                 int(with_cache)))
+
+
+def launch_forward_prefill(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    cache: torch.Tensor | None,
+    *,
+    activation_flag: int,
+    final_state: bool,
+    routing: int = ROUTE_ALPHA,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """(y, final state or None) of a fixed-length [B, T, D] x continuing from
+    ``cache`` [B, D, S] (moc/api.py:299-309, 218-227) in one launch: the taps
+    that reach before a sequence's first token read the cache, and the kernel
+    writes the final state (the last S inputs, [B, D, S])."""
+    L = _lib.lib()
+    x = x.contiguous()
+    a = _operand(alpha)
+    b = _operand(basis)
+    K, S, _ = b.shape
+    B, T, D = x.shape
+    c = None if cache is None else cache.to(x.dtype).contiguous()
+    out = torch.empty_like(x)
+    fin = x.new_empty(B, D, S) if final_state else None
+    x_dt = _lib.dtype_code(x.dtype)
+    with _lib.device_guard(x.device):
+        nbytes = L.moc_forward_workspace_bytes(B * T, D, K, S, x_dt, routing)
+        ws = _workspace(nbytes, x.device)
+        rc = L.moc_forward_prefill(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), out.data_ptr(),
+            None if c is None else c.data_ptr(), None if fin is None else fin.data_ptr(),
+            B, T, D, K, S, x_dt, _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
+            int(activation_flag), int(routing),
+            ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device),
+        )
+    _lib.check(rc, "moc_forward_prefill")
+    return out, fin
+
+
+def launch_backward_prefill(
+    x: torch.Tensor,
+    alpha: torch.Tensor,
+    basis: torch.Tensor,
+    cache: torch.Tensor,
+    moc_dy: torch.Tensor,
+    *,
+    activation_flag: int,
+    need_x: bool,
+    need_cache: bool,
+    routing: int = ROUTE_ALPHA,
+) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """(dx or None, dalpha, dbasis, dcache or None) of launch_forward_prefill's
+    y in one moc_backward_prefill call."""
+    L = _lib.lib()
+    x = x.contiguous()
+    dy, dy_stride = dy_operand(moc_dy, x.dtype)
+    a = _operand(alpha)
+    b = _operand(basis)
+    K, S, _ = b.shape
+    B, T, D = x.shape
+    c = cache.to(x.dtype).contiguous()
+    dx = torch.empty_like(x) if need_x else None
+    dalpha = torch.empty_like(a)
+    dbasis = torch.empty_like(b)
+    dcache = torch.empty_like(c) if need_cache else None
+    x_dt = _lib.dtype_code(x.dtype)
+    with _lib.device_guard(x.device):
+        nbytes = L.moc_backward_workspace_bytes(B * T, D, K, S, x_dt, routing)
+        ws = _workspace(nbytes, x.device)
+        rc = L.moc_backward_prefill(
+            x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(), dy_stride, c.data_ptr(),
+            None if dx is None else dx.data_ptr(), dalpha.data_ptr(), dbasis.data_ptr(),
+            None if dcache is None else dcache.data_ptr(),
+            B, T, D, K, S, x_dt, _lib.dtype_code(a.dtype), _lib.dtype_code(b.dtype),
+            int(activation_flag), int(routing),
+            ws.data_ptr(), ws.numel(), _lib.stream_ptr(x.device),
+        )
+    _lib.check(rc, "moc_backward_prefill")
+    if dalpha.dtype != alpha.dtype:
+        dalpha = dalpha.to(alpha.dtype)
+    if dbasis.dtype != basis.dtype:
+        dbasis = dbasis.to(basis.dtype)
+    if dcache is not None and dcache.dtype != cache.dtype:
+        dcache = dcache.to(cache.dtype)
+    return dx, dalpha, dbasis, dcache
+
+
 def _layer_table(entries):
     """ctypes array of MocLayer from dicts of field values."""
     arr = (_lib.MocLayer * len(entries))()

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.EXPORTED_SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.moc_abi_version() == _lib.ABI_VERSION == 2
+    assert L.moc_abi_version() == _lib.ABI_VERSION == 3
 
 
 def test_header_constants_match_binding():
@@ -50,6 +50,7 @@ def test_workspace_queries():
 
 
 FAKE = 0x1000  # never dereferenced: every call below fails validation first
+ERR_ARG, ERR_DTYPE, ERR_WORKSPACE = -1, -2, -3  # MOC_ERR_* of include/moc_hip.h
 
 
 def _fwd(**kw):
@@ -189,8 +190,10 @@ def test_layer_entries_validate_and_size():
     for which in ("forward", "backward"):
         q = getattr(L, f"moc_{which}_layers_workspace_bytes")
         single = getattr(L, f"moc_{which}_workspace_bytes")
-        assert q(arr, 3, N, K, S, _lib.DT_BF16, 0) == sum(single(N, d, K, S, _lib.DT_BF16, 3)
-                                                            for d in dims)
+        # the single-layer queries cover either activation (no argument there)
+        total = sum(single(N, d, K, S, _lib.DT_BF16, 3) for d in dims)
+        assert q(arr, 3, N, K, S, _lib.DT_BF16, 1) == total
+        assert q(arr, 3, N, K, S, _lib.DT_BF16, 0) <= total
         assert q(arr, 0, N, K, S, _lib.DT_BF16, 0) == 0
         fn = getattr(L, f"moc_{which}_layers")
         assert fn(arr, 5, None, 0, 0, N, N, K, S, 1, 0, FAKE, 1 << 40, None) == -1
@@ -202,3 +205,62 @@ def test_layer_entries_validate_and_size():
     nul = _layers([64], dalpha=None)
     assert L.moc_backward_layers(nul, 1, None, 0, 0, 8, 8, 16, 4, 1, 0, FAKE, 1 << 30, None) == -1
     assert b"null" in L.moc_last_error()
+
+
+def _pre_fwd(**kw):
+    args = dict(x=FAKE, alpha=FAKE, basis=FAKE, y=FAKE, cache=FAKE, fin=None, n_seqs=2,
+                seq_len=8, dim=16, k=4, ks=4, x_dt=1, a_dt=1, b_dt=1, act=0, route=0,
+                ws=FAKE, ws_bytes=0, stream=None)
+    args.update(kw)
+    return _lib.lib().moc_forward_prefill(*args.values())
+
+
+def _pre_bwd(**kw):
+    args = dict(x=FAKE, alpha=FAKE, basis=FAKE, dy=FAKE, dys=16, cache=FAKE, dx=FAKE,
+                dalpha=FAKE, dbasis=FAKE, dcache=FAKE, n_seqs=2, seq_len=8, dim=16, k=4, ks=4,
+                x_dt=1, a_dt=1, b_dt=1, act=0, route=0, ws=FAKE, ws_bytes=0, stream=None)
+    args.update(kw)
+    return _lib.lib().moc_backward_prefill(*args.values())
+
+
+def test_prefill_entries_validate_before_touching_the_device():
+    """moc_prefill_supported's answer, and the prefill entries' status codes for
+    bad arguments (every call below fails before a launch: the valid-shape ones
+    with a zero-byte workspace)."""
+    L = _lib.lib()
+    assert L.moc_prefill_supported(2, 8, 16, 4, 4, _lib.DT_BF16, 1) == 1
+    assert L.moc_prefill_supported(2, 3, 16, 4, 4, _lib.DT_BF16, 1) == 1   # T = S-1
+    assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 1) == 0   # T < S-1 with a cache
+    assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 0) == 1   # no cache: any T
+    assert L.moc_prefill_supported(2, 8, 16, 4, 5, _lib.DT_BF16, 1) == 0   # no matrix-core S = 5
+    assert L.moc_prefill_supported(2, 8, 18, 4, 4, _lib.DT_BF16, 1) == 0   # D % 4 != 0
+    assert L.moc_prefill_supported(2, 8, 16, 33, 4, _lib.DT_F32, 1) == 0   # K > 32
+    assert L.moc_prefill_supported(0, 8, 16, 4, 4, _lib.DT_BF16, 1) == 0
+    fwd_need = L.moc_forward_workspace_bytes(16, 16, 4, 4, _lib.DT_BF16, 0)
+    assert fwd_need > 0
+    assert _pre_fwd() == ERR_WORKSPACE
+    assert _pre_fwd(n_seqs=0) == ERR_ARG
+    assert _pre_fwd(seq_len=2) == ERR_ARG
+    assert b"kernel_size - 1" in L.moc_last_error()
+    assert _pre_fwd(seq_len=2, cache=None) == ERR_WORKSPACE  # no cache: T = 2 is fine
+    assert _pre_fwd(x_dt=_lib.DT_F16) == ERR_DTYPE
+    assert _pre_fwd(ks=5) == ERR_ARG
+    assert _pre_fwd(x=None, ws_bytes=fwd_need) == ERR_ARG
+    assert _pre_fwd(act=2) == ERR_ARG
+    assert _pre_bwd() == ERR_WORKSPACE
+    assert _pre_bwd(cache=None) == ERR_ARG
+    assert _pre_bwd(dys=3) == ERR_ARG
+    assert _pre_bwd(dalpha=None) == ERR_ARG
+    assert _pre_bwd(seq_len=1) == ERR_ARG
+    assert _pre_bwd(route=7) == ERR_ARG
+
+
+def test_backward_workspace_query_covers_the_activation():
+    """moc_backward_workspace_bytes has no activation argument: at 8 taps,
+    32 routes, bf16 (two passes without SiLU, the fused pass with it) it gives
+    at least what either plan needs, so it is no smaller than the 4-tap figure
+    scaled by the taps (partials grow with S)."""
+    L = _lib.lib()
+    n = L.moc_backward_workspace_bytes(16384, 2048, 32, 8, _lib.DT_BF16, 0)
+    assert n > 0 and n % 256 == 0
+    assert n >= L.moc_backward_workspace_bytes(16384, 2048, 32, 4, _lib.DT_BF16, 0)
