@@ -10,6 +10,7 @@ inputs already resident in HBM.  Printed as one JSON line:
   value         tokens/s (millions) of the full layer step (router GEMMs + MoC)
   roofline      HBM roofline of the dominant entry (the fused backward)
   kernel_scope  forward / backward entry times alone (no router GEMMs)
+  prefill       a headline-shape chunk continuing from a cache (bench_prefill)
   decode        configs[3]: batch-256 single-token steps: us per MoC.step call
                 (host-synchronised each step, and back to back), per MoC.step
                 replayed from a HIP graph, and per launch of the one-launch
@@ -38,7 +39,6 @@ import torch  # noqa: E402
 
 METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/step"
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
-VALU_PEAK = 157.3e12       # flop/s, MI355X fp32 vector (packed)
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
 # FETCH_SIZE (68700 KiB) and WRITE_SIZE (98382 KiB) per dispatch of
@@ -209,6 +209,56 @@ def entry_calls(dev, rotate=ROTATE):
         return ops.launch_backward(xd, w, basis, dy, activation_flag=1, need_x=True,
                                    routing=ROUTE_SOFTMAX_WEIGHTS)
     return fwd, bwd
+
+
+def bench_prefill(dev, steps, warmup, rotate=ROTATE):
+    """A chunk of the headline layer shape continuing from a cache (chunked
+    prefill, moc/api.py:299-309): B=4 x T=4096 new tokens per sequence at D=2048,
+    K=16, S=4, SiLU, softmax routing.  Times (us, inputs rotated):
+      fwd_kernel_us / plain_fwd_kernel_us  the prefill forward kernel (cache
+          halo, final state written) and the plain forward kernel on the same
+          x and weights without a cache;
+      bwd_us  moc_backward_prefill (stage 1, stage 2, cache gradient);
+      module_fwd_us  MoC.forward(x, z, cache=..., output_final_state=True)
+          without autograd: router GEMM + the prefill forward launch."""
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX, ROUTE_SOFTMAX_WEIGHTS
+    m, sets = build_layer(dev, n_sets=rotate)
+    basis = m.conv_bases.detach()
+    B, D, S = CFG["B"], CFG["D"], CFG["S"]
+    g = torch.Generator(device=dev).manual_seed(7)
+    args = []
+    with torch.no_grad():
+        for x, z in sets:
+            w = ops.router_forward(z, m.router, routing=ROUTE_SOFTMAX)
+            c = torch.randn(B, D, S, generator=g, device=dev).to(torch.bfloat16)
+            args.append((x.detach(), z.detach(), w, c, torch.ones_like(x)))
+    cyc = _Cycle(args)
+
+    def pre_fwd():
+        x, _, w, c, _ = cyc.next()
+        return ops.launch_forward_prefill(x, w, basis, c, activation_flag=1, final_state=True,
+                                          routing=ROUTE_SOFTMAX_WEIGHTS)
+
+    def plain_fwd():
+        x, _, w, _, _ = cyc.next()
+        return ops.launch_forward(x, w, basis, activation_flag=1, routing=ROUTE_SOFTMAX_WEIGHTS)
+
+    def pre_bwd():
+        x, _, w, c, dy = cyc.next()
+        return ops.launch_backward_prefill(x, w, basis, c, dy, activation_flag=1, need_x=True,
+                                           need_cache=True, routing=ROUTE_SOFTMAX_WEIGHTS)
+
+    def module_fwd():
+        x, z, _, c, _ = cyc.next()
+        with torch.no_grad():
+            return m(x, z, cache=c, output_final_state=True)
+
+    return {"B": B, "T": CFG["T"], "D": D, "K": CFG["K"], "S": S,
+            "fwd_kernel_us": round(time_kernel(pre_fwd, steps, warmup) * 1e3, 2),
+            "plain_fwd_kernel_us": round(time_kernel(plain_fwd, steps, warmup) * 1e3, 2),
+            "bwd_us": round(time_region(pre_bwd, steps, warmup) * 1e3, 2),
+            "module_fwd_us": round(time_region(module_fwd, steps, warmup) * 1e3, 2)}
 
 
 def bench_entries(dev, steps, warmup, rotate=ROTATE):
@@ -495,6 +545,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
                     help="2: the headline line (default); 3 / 5: one JSON line for BASELINE "
                          "configs[2] (varlen) / configs[4] (QKV triple) instead")
@@ -532,11 +583,6 @@ def main():
     fb, bb = bytes_fwd(N, D, K, S), bytes_bwd(N, D, K, S)
     roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / 2.5e15)
                + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / 2.5e15)) * 1e6
-    # the same bytes with the algorithm's flops on the fp32 VALU (157.3 TF/s):
-    # the bound of an implementation that runs the K-contractions on VALU,
-    # which binds at this config (about 54 flop/B)
-    valu_roof_us = (max(fb / HBM_PEAK, flops_fwd(N, D, K, S) / VALU_PEAK)
-                    + max(bb / HBM_PEAK, flops_bwd(N, D, K, S) / VALU_PEAK)) * 1e6
     # dominant kernel: the fused backward stage 1; its algorithmic bytes are x, dy
     # and dx, the routing weights and the basis (dalpha / dbasis leave it as
     # partial sums that the stage-2 reduction turns into the outputs)
@@ -571,10 +617,10 @@ def main():
                          "fwd_GBps": round(fb / (t_fwd * 1e-3) / 1e9, 1),
                          "bwd_GBps": round(bb / (t_bwd * 1e-3) / 1e9, 1),
                          "hbm_roofline_us": round(roof_us, 2),
-                         "roofline_frac": round(roof_us / ((t_fwd + t_bwd) * 1e3), 4),
-                         "valu_roofline_us": round(valu_roof_us, 2),
-                         "valu_roofline_frac": round(valu_roof_us / ((t_fwd + t_bwd) * 1e3), 4)},
+                         "roofline_frac": round(roof_us / ((t_fwd + t_bwd) * 1e3), 4)},
     }
+    if not args.no_prefill:
+        out["prefill"] = bench_prefill(dev, min(args.steps, 20), min(args.warmup, 5), args.rotate)
     if not args.no_decode:
         out["decode"] = bench_decode(dev)
     if not args.no_cpu:
