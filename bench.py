@@ -221,6 +221,18 @@ def bench_prefill(dev, steps, warmup, rotate=ROTATE):
       bwd_us  moc_backward_prefill (stage 1, stage 2, cache gradient);
       module_fwd_us  MoC.forward(x, z, cache=..., output_final_state=True)
           without autograd: router GEMM + the prefill forward launch."""
+    pre_fwd, plain_fwd, pre_bwd, module_fwd = prefill_calls(dev, rotate, parts=True)
+    return {"B": CFG["B"], "T": CFG["T"], "D": CFG["D"], "K": CFG["K"], "S": CFG["S"],
+            "fwd_kernel_us": round(time_kernel(pre_fwd, steps, warmup) * 1e3, 2),
+            "plain_fwd_kernel_us": round(time_kernel(plain_fwd, steps, warmup) * 1e3, 2),
+            "bwd_us": round(time_region(pre_bwd, steps, warmup) * 1e3, 2),
+            "module_fwd_us": round(time_region(module_fwd, steps, warmup) * 1e3, 2)}
+
+
+def prefill_calls(dev, rotate=ROTATE, parts=False):
+    """The calls bench_prefill times, on ``rotate`` input sets: (prefill forward
+    entry, plain forward entry, prefill backward entry, module forward) with
+    parts, else one callable running the module forward and the backward entry."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX, ROUTE_SOFTMAX_WEIGHTS
     m, sets = build_layer(dev, n_sets=rotate)
@@ -254,11 +266,13 @@ def bench_prefill(dev, steps, warmup, rotate=ROTATE):
         with torch.no_grad():
             return m(x, z, cache=c, output_final_state=True)
 
-    return {"B": B, "T": CFG["T"], "D": D, "K": CFG["K"], "S": S,
-            "fwd_kernel_us": round(time_kernel(pre_fwd, steps, warmup) * 1e3, 2),
-            "plain_fwd_kernel_us": round(time_kernel(plain_fwd, steps, warmup) * 1e3, 2),
-            "bwd_us": round(time_region(pre_bwd, steps, warmup) * 1e3, 2),
-            "module_fwd_us": round(time_region(module_fwd, steps, warmup) * 1e3, 2)}
+    if parts:
+        return pre_fwd, plain_fwd, pre_bwd, module_fwd
+
+    def both():
+        module_fwd()
+        pre_bwd()
+    return both
 
 
 def bench_entries(dev, steps, warmup, rotate=ROTATE):
@@ -276,6 +290,9 @@ def counter_run(dev, which, reps=3):
       step       the headline layer step (bench_layer's step, inputs rotated);
       decode     the one-launch decode step of configs[3] (batch 256);
       c5         the configs[4] QKV triple step through MoCGroup;
+      prefill    a headline-shape chunk continuing from a cache: the module
+                 forward (router + prefill launch), then the prefill backward
+                 entry (bench_prefill's workload);
       copy       a bf16 copy of 128 MiB, the kernel of known traffic that
                  calibrates FETCH_SIZE and WRITE_SIZE."""
     if which == "copy":
@@ -298,6 +315,8 @@ def counter_run(dev, which, reps=3):
             y.sum().backward()
     elif which == "decode":
         fn = decode_step_call(dev)
+    elif which == "prefill":
+        fn = prefill_calls(dev, 1)
     else:
         fn = config5_step(dev)[0](True)
     for _ in range(2):
@@ -552,7 +571,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE,
                     help="input sets the timed loops cycle through (1: one set reused, "
                          "which the last-level cache partly holds across steps)")
-    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c5", "copy"),
+    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c5", "prefill", "copy"),
                     default=None,
                     help="only run --reps calls of one workload (see counter_run) for a "
                          "rocprofv3 --pmc or --kernel-trace pass; prints no JSON")

@@ -218,19 +218,23 @@ stage2_layers_kernel(Stage2Layers ly, int64_t N, int K, int S, int64_t da_blocks
 // for tap s < S-1-pos of token pos), so
 //   dcache[b, d, j] = sum over pos < S-1, s = j - 1 - pos >= 0 of g[t, d] W[t, s, d]
 // (t = b T + pos; slot 0 is read by no kept output and gets zero), with W from the
-// kernels' operands and, with SiLU, g = dy silu'(P) recomputed in fp32.
-template <int S, bool BF>
-__global__ void __launch_bounds__(256)
+// kernels' operands and, with SiLU, g = dy silu'(P) recomputed in fp32.  The
+// route loop is unrolled (KP = 16 KC), so all of a thread's loads are issued
+// before the first product; 64-lane workgroups spread the few sequences' work
+// over the CUs.
+template <int S, int KC, bool BF>
+__global__ void __launch_bounds__(64)
 hist_grad_kernel(const typename CT<BF>::elem* __restrict__ x,
                  const typename CT<BF>::elem* __restrict__ a_c,
                  const typename CT<BF>::elem* __restrict__ b_c,
                  const typename CT<BF>::elem* __restrict__ dy, int64_t dys,
                  const typename CT<BF>::elem* __restrict__ hist,
-                 typename CT<BF>::elem* __restrict__ dcache, int64_t T, int64_t D, int KP, int act) {
+                 typename CT<BF>::elem* __restrict__ dcache, int64_t T, int64_t D, int act) {
   using C = CT<BF>;
+  constexpr int KP = 16 * KC;
   constexpr int NP = S - 1;  // tokens of a sequence whose taps reach the cache (T >= S-1)
   const int64_t b = blockIdx.y;
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
   if (d >= D) return;
   const int64_t t0 = b * T;
   float w[NP][S];
@@ -238,6 +242,7 @@ hist_grad_kernel(const typename CT<BF>::elem* __restrict__ x,
   for (int pos = 0; pos < NP; ++pos)
 #pragma unroll
     for (int s = 0; s < S; ++s) w[pos][s] = 0.f;
+#pragma unroll
   for (int k = 0; k < KP; ++k) {
     float bs[S];
 #pragma unroll
@@ -491,11 +496,12 @@ void hist_grad_one(const Problem& p, const void* x, const void* a_c, const void*
                    const void* dy, const void* cache, void* dcache, int KP, hipStream_t st) {
   using E = typename CT<BF>::elem;
   const int64_t B = p.n_tokens / p.seq.seq_len;
-  hipLaunchKernelGGL((hist_grad_kernel<S, BF>),
-                     dim3(static_cast<unsigned>(cdiv(p.D, 256)), static_cast<unsigned>(B)),
-                     dim3(256), 0, st, static_cast<const E*>(x), static_cast<const E*>(a_c),
+  auto kern = KP == 16 ? hist_grad_kernel<S, 1, BF> : hist_grad_kernel<S, 2, BF>;
+  hipLaunchKernelGGL(kern,
+                     dim3(static_cast<unsigned>(cdiv(p.D, 64)), static_cast<unsigned>(B)),
+                     dim3(64), 0, st, static_cast<const E*>(x), static_cast<const E*>(a_c),
                      static_cast<const E*>(b_c), static_cast<const E*>(dy), p.dy_stride,
-                     static_cast<const E*>(cache), static_cast<E*>(dcache), p.seq.seq_len, p.D, KP,
+                     static_cast<const E*>(cache), static_cast<E*>(dcache), p.seq.seq_len, p.D,
                      p.activation);
 }
 
