@@ -371,6 +371,7 @@ int prefill_problem(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k, int
   if ((rc = check_common(x_dtype, alpha_dtype, basis_dtype, activation, routing)) != MOC_OK) return rc;
   p = make_problem(nullptr, 0, n_seqs, n_tokens, seq_len, dim, k, kernel_size, x_dtype,
                    alpha_dtype, basis_dtype, activation, routing);
+  p.pre = true;
   if (!use_mfma(p) || !moc::mfma::prefill_supported(p, has_cache))
     return fail(MOC_ERR_ARG,
                 "prefill not supported for this problem (seq_len %lld, dim %lld, k %lld, "

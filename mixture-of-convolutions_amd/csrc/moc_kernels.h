@@ -21,6 +21,7 @@ struct Problem {
   int routing;       // Route
   int64_t dy_stride = 0;  // backward: elements between token rows of dy (D, or 0 = one row for all)
   int path = PATH_AUTO;   // PATH_MFMA_PREP: MFMA kernels, operands always through prep
+  bool pre = false;       // prefill from a cache: the backward is the fused pass for every shape
   hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set
   hipEvent_t prof_stop = nullptr;
 };

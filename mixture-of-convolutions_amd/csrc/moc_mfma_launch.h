@@ -45,6 +45,15 @@ constexpr int64_t kFwdMaxSb = 4;
 
 // Channels of one forward / backward workgroup (grid x counts these groups).
 constexpr int64_t kFwdCW = 4 * 16 * kFwdNC, kBwdCW = kBwdWPG * 16 * kBwdNC;
+// Taps pass of the two-pass backward: kTapsWPG waves per workgroup, half of them
+// per tap half, so a workgroup covers kTapsCW channels; kTapsPerCU of its
+// workgroups fit a CU's LDS at once.
+#ifndef MOC_TAPS_WPG
+#define MOC_TAPS_WPG 8
+#endif
+constexpr int kTapsWPG = MOC_TAPS_WPG;
+constexpr int64_t kTapsCW = (kTapsWPG / 2) * 16 * kBwdNC;
+constexpr int kTapsPerCU = kTapsWPG >= 8 ? 1 : 2;
 
 // Forward grid over gx channel groups (the sum over the layers of a grouped launch).
 inline Grid2 fwd_grid_gx(int64_t N, int64_t gx) {
@@ -141,8 +150,8 @@ constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && KC == 2 && S == 8;
 }
 inline bool bwd_two_pass(const Problem& p) {
-  return bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16), p.activation != 0,
-                      p.x_dt == DT_BF16);
+  return !p.pre && bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16),
+                                p.activation != 0, p.x_dt == DT_BF16);
 }
 
 // The taps pass holds one workgroup per CU (its LDS), so it runs as one round
@@ -150,17 +159,14 @@ inline bool bwd_two_pass(const Problem& p) {
 // rounds measured slower: each round pays a prologue of about 6 us, and the
 // second round's workgroups started 15-20 us after the first round's ended.
 inline Grid2 bwd_taps_grid(int64_t N, int64_t gx, int64_t D, int64_t S, int n_cu) {
-  return bwd_grid_gx(N, gx, D, S, n_cu > 0 ? n_cu : kBwdTargetWG / 2);
+  return bwd_grid_gx(N, gx, D, S, n_cu > 0 ? int64_t(n_cu) * kTapsPerCU : kBwdTargetWG / 2);
 }
 
-// The grid whose ranges own the dalpha / dbasis partials (workspace, stage 2),
-// over gx channel groups of layers at most D channels wide.
-inline Grid2 bwd_partials_grid(const Problem& p, int64_t gx, int64_t D) {
-  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, gx, D, p.S, device_cu_count())
-                         : bwd_grid_gx(p.n_tokens, gx, D, p.S);
-}
+// The grid whose workgroups own the dalpha / dbasis partials (workspace,
+// stage 2): the taps pass's for the two-pass form, else the fused pass's.
 inline Grid2 bwd_partials_grid(const Problem& p) {
-  return bwd_partials_grid(p, cdiv(p.D, kBwdCW), p.D);
+  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, p.S, device_cu_count())
+                         : bwd_grid_gx(p.n_tokens, cdiv(p.D, kBwdCW), p.D, p.S);
 }
 
 // Operands of one layer of a grouped launch (after operand preparation); the
@@ -214,10 +220,10 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
-    // (one round of n_cu workgroups: bwd_taps_grid)
-    const Grid2 gt = bwd_taps_grid(p.n_tokens, gx_all, p.D, S, device_cu_count());
-    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, BF, false, kBwdTaps>),
-                       dim3(gt.gx, gt.gy), dim3(128 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
+    // (one round of workgroups: bwd_taps_grid)
+    const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, S, device_cu_count());
+    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF, false, kBwdTaps>),
+                       dim3(gt.gx, gt.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
                        gt.n_old, gt.n_total);
   } else {
@@ -268,7 +274,7 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
     blk += kSplit ? 16 * cdiv(tiles, 8) : (kTwo && L[i].dx == nullptr ? 0 : tiles);
     any_dx = any_dx || L[i].dx != nullptr;
     if constexpr (kTwo) {
-      const Grid2 gt = bwd_taps_grid(p.n_tokens, gx_l, L[i].D, S, n_cu);
+      const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(L[i].D, kTapsCW), L[i].D, S, n_cu);
       lt.l[i] = ly.l[i];
       lt.l[i].dx = nullptr;
       lt.l[i].gx = static_cast<int>(gt.gx);
@@ -284,8 +290,8 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
     if (any_dx)
       hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, false, kBwdDx>),
                          dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
-    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, 2 * kBwdWPG, ACT, true, false, kBwdTaps>),
-                       dim3(static_cast<unsigned>(blkt)), dim3(128 * kBwdWPG), 0, st, lt, p.seq);
+    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, true, false, kBwdTaps>),
+                       dim3(static_cast<unsigned>(blkt)), dim3(64 * kTapsWPG), 0, st, lt, p.seq);
   } else {
     hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, kSplit, kBwdFused>),
                        dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
