@@ -396,20 +396,64 @@ class _MoCPrefillFunction(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dy, dfin):
         x, a, basis, cache = ctx.saved_tensors
-        B, T, _ = x.shape
-        S = basis.shape[1]
-        if dy is None:
-            dy = torch.zeros_like(x)
-        need_x = ctx.needs_input_grad[0] or dfin is not None
-        dx, da, db, dc = ops.launch_backward_prefill(
-            x, a, basis, cache, dy, activation_flag=ctx.act, need_x=need_x,
-            need_cache=ctx.needs_input_grad[3], routing=ctx.routing)
-        if dfin is not None:
-            n = min(S, T)
-            dx[:, T - n:] += dfin[:, :, S - n:].transpose(1, 2).to(dx.dtype)
-            if T < S and dc is not None:
-                dc[:, :, T:] += dfin[:, :, :S - T].to(dc.dtype)
-        return (dx if ctx.needs_input_grad[0] else None), da, db, dc, None, None, None
+        dx, da, db, dc = _prefill_backward(ctx, dy, dfin, x, a, basis, cache,
+                                           ctx.needs_input_grad[0], ctx.needs_input_grad[3])
+        return dx, da, db, dc, None, None, None
+
+
+def _prefill_backward(ctx, dy, dfin, x, a, basis, cache, need_x, need_cache):
+    """(dx or None, dalpha, dbasis, dcache or None) of a prefill launch, with a
+    gradient of the final state (the last S inputs, a slice of x and for T < S
+    of the cache, moc/api.py:218-227) added to dx / dcache."""
+    B, T, _ = x.shape
+    S = basis.shape[1]
+    if dy is None:
+        dy = torch.zeros_like(x)
+    dx, da, db, dc = ops.launch_backward_prefill(
+        x, a, basis, cache, dy, activation_flag=ctx.act, need_x=need_x or dfin is not None,
+        need_cache=need_cache, routing=ctx.routing)
+    if dfin is not None:
+        n = min(S, T)
+        dx[:, T - n:] += dfin[:, :, S - n:].transpose(1, 2).to(dx.dtype)
+        if T < S and dc is not None:
+            dc[:, :, T:] += dfin[:, :, :S - T].to(dc.dtype)
+    return (dx if need_x else None), da, db, dc
+
+
+class _MoCLayerPrefillFunction(torch.autograd.Function):
+    """MoC.forward continuing from a cache (moc/api.py:299-309, 383-388) on the
+    library's kernels end to end: the router kernel forms the routing weights
+    softmax / exp(z . router^T), the prefill entries run on them (routing
+    *_WEIGHTS, so the backward returns the logits gradient), and the router
+    backward turns that into dz and drouter.  Returns (y, final state or None)."""
+
+    @staticmethod
+    def forward(ctx, x, z, router, basis, cache, activation, router_activation, want_state):
+        weights = ops.router_forward(z, router, routing=_ROUTING_CODES[router_activation])
+        x, basis = x.contiguous(), basis.contiguous()
+        check_fixed_inputs(x, weights, basis)
+        _check_cache(x, basis, cache)
+        act = activation_flag(activation)
+        routing = _WEIGHTS_CODES[router_activation]
+        y, fin = ops.launch_forward_prefill(x, weights, basis, cache, activation_flag=act,
+                                            final_state=want_state, routing=routing)
+        ctx.save_for_backward(x, weights, basis, cache, z, router)
+        ctx.act = act
+        ctx.routing = routing
+        ctx.set_materialize_grads(False)
+        return y, fin
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dy, dfin):
+        x, w, basis, cache, z, router = ctx.saved_tensors
+        dx, dlogits, db, dc = _prefill_backward(ctx, dy, dfin, x, w, basis, cache,
+                                                ctx.needs_input_grad[0], ctx.needs_input_grad[4])
+        dz = dr = None
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            dz, dr = ops.router_backward(z, router, dlogits, ctx.needs_input_grad[1],
+                                         ctx.needs_input_grad[2])
+        return dx, dz, dr, db, dc, None, None, None
 
 
 def _prefill(x, a, basis, cache, activation, router_activation, output_final_state):
@@ -545,10 +589,19 @@ class MoC(nn.Module):
                                            activation_flag=activation_flag(self.activation),
                                            routing=_ROUTING_CODES[self.router_activation])
                 return y, (cache if output_final_state else None)
-        if (cache is None and self.router.shape[0] <= ops.ROUTER_MAX_ROUTED_K
-                and ops.router_supported(z, self.router)):
+        routed = (self.router.shape[0] <= ops.ROUTER_MAX_ROUTED_K
+                  and ops.router_supported(z, self.router))
+        if cache is None and routed:
             return self._forward_kernels(x, z, output_final_state, cu_seqlens, max_seqlen,
                                          cu_seqlens_cpu, chunk_indices)
+        if (routed and cu_seqlens is None and x.dim() == 3 and x.shape[1] > 1
+                and ops.prefill_supported(x, self.conv_bases, with_cache=True)):
+            # prefill from the cache: router epilogue + prefill entries, one node
+            if cu_seqlens_cpu is not None or chunk_indices is not None:
+                raise ValueError("cu_seqlens_cpu and chunk_indices require cu_seqlens")
+            return _MoCLayerPrefillFunction.apply(x, z, self.router, self.conv_bases, cache,
+                                                  self.activation, self.router_activation,
+                                                  output_final_state)
         logits = router_linear(z, self.router)
         return _dispatch(x, logits, self.conv_bases, cache, output_final_state,
                          self.activation, self.router_activation, cu_seqlens, max_seqlen,

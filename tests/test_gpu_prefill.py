@@ -199,3 +199,44 @@ def test_backward_8_taps_32_routes_silu():
     assert_close("dx", xs.grad, rdx, dtype)
     assert_close("dalpha", as_.grad, rda, dtype)
     assert_close("dbasis", bs.grad, rdb, dtype)
+
+
+@pytest.mark.parametrize("route", ["softmax", "exp"])
+def test_module_prefill_gradients(route):
+    """MoC.forward continuing from a cache on its kernel path (router epilogue +
+    prefill entries, one autograd node): y, the final state and the gradients
+    of x, z, router, basis and the cache against the oracle chain on the
+    module's own bf16 logits."""
+    from moc import MoC, router_linear
+    from tests._parity import ulp_allowance
+    B, T, D, Z, K, S, bf = 2, 40, 128, 64, 16, 4, torch.bfloat16
+    g = gen(31)
+    m = MoC(D, Z, S, K, activation="silu", init_std=0.1, router_activation=route)
+    with torch.no_grad():
+        m.router.copy_(randn(g, K, Z, scale=0.1))
+    m = m.to(DEV, bf)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, bf).requires_grad_()
+    z = randn(g, B, T, Z).to(DEV, bf).requires_grad_()
+    c = randn(g, B, D, S, scale=0.5).to(DEV, bf).requires_grad_()
+    dy = randn(g, B, T, D, scale=0.1).to(DEV, bf)
+    y, st = m(x, z, cache=c, output_final_state=True)
+    y.backward(dy)
+    with torch.no_grad():
+        logits = router_linear(z, m.router).cpu()
+    lf = logits.float().requires_grad_()
+    rx = x.detach().float().cpu().requires_grad_()
+    rb = m.conv_bases.detach().float().cpu().requires_grad_()
+    rc = c.detach().float().cpu().requires_grad_()
+    ry = O.moc_prefill_ref(rx, O.route(lf, route, out_dtype=bf), rb, rc, "silu")
+    ry.backward(dy.float().cpu())
+    dl = lf.grad.to(bf).float().reshape(-1, K)
+    rz = (dl @ m.router.detach().float().cpu()).reshape(B, T, Z)
+    rr = dl.T @ z.detach().float().cpu().reshape(-1, Z)
+    assert_close("y", y, ry, bf)
+    assert torch.equal(st, O.final_state(torch.cat((c.detach().transpose(1, 2), x.detach()), 1),
+                                         None, S))
+    assert_close("dx", x.grad, rx.grad, bf)
+    assert_close("dz", z.grad, rz, bf, extra=ulp_allowance(lf.grad, m.router.cpu()))
+    assert_close("drouter", m.router.grad, rr, bf)
+    assert_close("dbasis", m.conv_bases.grad, rb.grad, bf)
+    assert_close("dcache", c.grad, rc.grad, bf)
