@@ -399,7 +399,7 @@ bool supported(const Problem& p) {
   // super-block's rows within a buffer's 32-bit range
   return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
          (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
-         bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D).gy <= 65535;
+         bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D, p.S).gy <= 65535;
 }
 
 size_t forward_workspace(const Problem& p) { return plan(p, false).total; }

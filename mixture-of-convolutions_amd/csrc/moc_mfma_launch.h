@@ -16,7 +16,14 @@ namespace mfma {
 #ifndef MOC_FWD_NC
 #define MOC_FWD_NC 2
 #endif
+// 8 taps with one token block per super-block (11 window rows instead of 15,
+// 135 VGPRs, three waves per SIMD) measured slower at configs[4]: 1237 -> 1251 us
+#ifndef MOC_FWD_NB8
+#define MOC_FWD_NB8 2
+#endif
 constexpr int kFwdNB = 2, kFwdNC = MOC_FWD_NC;
+// token blocks per forward super-block for kernel size S
+constexpr int fwd_nb(int S) { return S == 8 ? MOC_FWD_NB8 : kFwdNB; }
 constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
 // Resident workgroups the grids are sized for (256 CUs).
 #ifndef MOC_FWD_TARGET_WG
@@ -56,8 +63,8 @@ constexpr int64_t kTapsCW = (kTapsWPG / 2) * 16 * kBwdNC;
 constexpr int kTapsPerCU = kTapsWPG >= 8 ? 1 : 2;
 
 // Forward grid over gx channel groups (the sum over the layers of a grouped launch).
-inline Grid2 fwd_grid_gx(int64_t N, int64_t gx) {
-  const int64_t n_super = cdiv(N, 16 * kFwdNB);
+inline Grid2 fwd_grid_gx(int64_t N, int64_t gx, int64_t S) {
+  const int64_t n_super = cdiv(N, 16 * fwd_nb(static_cast<int>(S)));
   int64_t gy_target = kFwdTargetWG / gx;
   if (gy_target < 1) gy_target = 1;
   int64_t n_sb = cdiv(n_super, gy_target);
@@ -68,7 +75,7 @@ inline Grid2 fwd_grid_gx(int64_t N, int64_t gx) {
                static_cast<int>(n_sb)};
 }
 
-inline Grid2 fwd_grid(int64_t N, int64_t D) { return fwd_grid_gx(N, cdiv(D, kFwdCW)); }
+inline Grid2 fwd_grid(int64_t N, int64_t D, int64_t S) { return fwd_grid_gx(N, cdiv(D, kFwdCW), S); }
 
 // Backward grid over gx channel groups; D is the widest layer's channel count
 // (it bounds the token range of a workgroup's buffers).
@@ -188,8 +195,8 @@ template <int S, int KC, bool ACT, bool BF>
 void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
              hipStream_t st) {
   using E = typename CT<BF>::elem;
-  const Grid2 g = fwd_grid(p.n_tokens, p.D);
-  hipLaunchKernelGGL((fwd_kernel<S, KC, kFwdNB, kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256), 0,
+  const Grid2 g = fwd_grid(p.n_tokens, p.D, S);
+  hipLaunchKernelGGL((fwd_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256), 0,
                      st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq, p.D,
                      g.n_sb);
 }
@@ -241,12 +248,12 @@ void fwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
   ly.n = n;
   int64_t blk = 0;
   for (int i = 0; i < n; ++i) {
-    const Grid2 g = fwd_grid(p.n_tokens, L[i].D);
+    const Grid2 g = fwd_grid(p.n_tokens, L[i].D, S);
     ly.l[i] = FwdLayer{L[i].x, L[i].a_c, L[i].b_c, L[i].y, L[i].D, static_cast<int>(g.gx),
                        g.n_sb, static_cast<int>(blk)};
     blk += static_cast<int64_t>(g.gx) * g.gy;
   }
-  hipLaunchKernelGGL((fwd_layers_kernel<S, KC, kFwdNB, kFwdNC, ACT, true>),
+  hipLaunchKernelGGL((fwd_layers_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, true>),
                      dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, ly, p.seq);
 }
 
@@ -373,8 +380,8 @@ template <int S, int KC, bool ACT, bool BF>
 void fwd_pre_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
                  const Pre& pre, hipStream_t st) {
   using E = typename CT<BF>::elem;
-  const Grid2 g = fwd_grid(p.n_tokens, p.D);
-  hipLaunchKernelGGL((fwd_pre_kernel<S, KC, kFwdNB, kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256),
+  const Grid2 g = fwd_grid(p.n_tokens, p.D, S);
+  hipLaunchKernelGGL((fwd_pre_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256),
                      0, st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq,
                      p.D, g.n_sb, pre);
 }
