@@ -11,6 +11,8 @@ inputs already resident in HBM.  Printed as one JSON line:
   roofline      HBM roofline of the dominant entry (the fused backward)
   kernel_scope  forward / backward entry times alone (no router GEMMs)
   prefill       a headline-shape chunk continuing from a cache (bench_prefill)
+  config3_varlen, config5_qkv  BASELINE configs[2] and configs[4] (the
+                `--config 3` / `--config 5` measurements)
   decode        configs[3]: batch-256 single-token steps: us per MoC.step call
                 (host-synchronised each step, and back to back), per MoC.step
                 replayed from a HIP graph, and per launch of the one-launch
@@ -565,6 +567,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the configs[2] / configs[4] objects of the default line")
     ap.add_argument("--config", type=int, choices=(2, 3, 5), default=2,
                     help="2: the headline line (default); 3 / 5: one JSON line for BASELINE "
                          "configs[2] (varlen) / configs[4] (QKV triple) instead")
@@ -642,6 +646,13 @@ def main():
         out["prefill"] = bench_prefill(dev, min(args.steps, 20), min(args.warmup, 5), args.rotate)
     if not args.no_decode:
         out["decode"] = bench_decode(dev)
+    if not args.no_configs:
+        # BASELINE configs[2] (varlen) and configs[4] (QKV triple), as the
+        # `--config 3` / `--config 5` lines report them
+        for key, fn in (("config3_varlen", bench_config3), ("config5_qkv", bench_config5)):
+            r = fn(dev, min(args.steps, 20), min(args.warmup, 5))
+            out[key] = {k: r[k] for k in r if k not in ("metric",)}
+            torch.cuda.empty_cache()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
