@@ -291,7 +291,8 @@ def test_config4_decode():
     """configs[3] at its stated size: a batch-256 layer (D 2048, z_dim 2048, K16,
     S4, softmax, SiLU) prefilled from a 1024-token prompt, then 512 single-token
     steps; every step's y on every batch row against the fp32 oracle forward
-    over all 1536 tokens, the final cache bit-exact (the last S inputs)."""
+    over all 1536 tokens, the final cache bit-exact (the last S inputs); the
+    same steps as one MoC.forward call from the prompt's cache likewise."""
     B, D, Z, K, S, P, steps = 256, 2048, 2048, 16, 4, 1024, 512
     m, _ = _layer(D, Z, K, S, "silu", "softmax", None, torch.bfloat16)
     gd = torch.Generator(device=DEV).manual_seed(4)
@@ -305,6 +306,13 @@ def test_config4_decode():
             assert c2 is cache
             y_steps[:, i:i + 1] = y
     assert torch.equal(cache, x[:, -S:].transpose(1, 2))
+    # the same 512 steps as one call (their inputs known up front): MoC.forward
+    # continuing from the prompt's cache, i.e. one router launch and one prefill
+    # launch; y against the same oracle, the final cache bit-exact
+    with torch.no_grad():
+        _, cache_p = m(x[:, :P], z[:, :P], output_final_state=True)
+        y_call, cache_call = m(x[:, P:], z[:, P:], cache=cache_p, output_final_state=True)
+    assert torch.equal(cache_call, cache)
     basis = m.conv_bases.detach().float()
     for r0 in range(0, B, 64):   # the oracle in row blocks (its W is [rows, T, D, S] fp32)
         rows = slice(r0, r0 + 64)
@@ -313,6 +321,7 @@ def test_config4_decode():
             alpha = O.route(logits.float(), "softmax", out_dtype=logits.dtype)
             full = O.moc_ref(x[rows].float(), alpha, basis, "silu")
         assert_close(f"decode y rows {r0}..{r0 + 63}", y_steps[rows], full[:, P:], torch.bfloat16)
+        assert_close(f"one-call y rows {r0}..{r0 + 63}", y_call[rows], full[:, P:], torch.bfloat16)
         del full, alpha, logits
 
 
