@@ -394,7 +394,7 @@ void launch_stage2(const Problem& p, const Plan& pl, bool dir, char* ws, const v
 }  // namespace
 
 bool supported(const Problem& p) {
-  const bool s_ok = p.S == 2 || p.S == 3 || p.S == 4 || p.S == 8;
+  const bool s_ok = p.S >= 2 && p.S <= 8;
   // the grids' y dimensions stay within the 65535 launch limit and one
   // super-block's rows within a buffer's 32-bit range
   return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
@@ -422,6 +422,9 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
     case 2: launch_fwd<2>(p, x, a_c, b_c, y, st); break;
     case 3: launch_fwd<3>(p, x, a_c, b_c, y, st); break;
     case 4: launch_fwd<4>(p, x, a_c, b_c, y, st); break;
+    case 5: launch_fwd<5>(p, x, a_c, b_c, y, st); break;
+    case 6: launch_fwd<6>(p, x, a_c, b_c, y, st); break;
+    case 7: launch_fwd<7>(p, x, a_c, b_c, y, st); break;
     case 8: launch_fwd<8>(p, x, a_c, b_c, y, st); break;
     default: break;
   }
@@ -448,6 +451,9 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     case 2: launch_bwd<2>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     case 3: launch_bwd<3>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     case 4: launch_bwd<4>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 5: launch_bwd<5>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 6: launch_bwd<6>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 7: launch_bwd<7>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
     default: break;
   }
@@ -485,6 +491,9 @@ void forward_prefill(const Problem& p, const void* x, const void* alpha, const v
     case 2: launch_fwd_pre<2>(p, x, a_c, b_c, y, pre, st); break;
     case 3: launch_fwd_pre<3>(p, x, a_c, b_c, y, pre, st); break;
     case 4: launch_fwd_pre<4>(p, x, a_c, b_c, y, pre, st); break;
+    case 5: launch_fwd_pre<5>(p, x, a_c, b_c, y, pre, st); break;
+    case 6: launch_fwd_pre<6>(p, x, a_c, b_c, y, pre, st); break;
+    case 7: launch_fwd_pre<7>(p, x, a_c, b_c, y, pre, st); break;
     case 8: launch_fwd_pre<8>(p, x, a_c, b_c, y, pre, st); break;
     default: break;
   }
@@ -526,6 +535,9 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
     case 2: launch_bwd_pre<2>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
     case 3: launch_bwd_pre<3>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
     case 4: launch_bwd_pre<4>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 5: launch_bwd_pre<5>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 6: launch_bwd_pre<6>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
+    case 7: launch_bwd_pre<7>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
     case 8: launch_bwd_pre<8>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;
     default: break;
   }
@@ -542,6 +554,9 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
       MOC_HG(2)
       MOC_HG(3)
       MOC_HG(4)
+      MOC_HG(5)
+      MOC_HG(6)
+      MOC_HG(7)
       MOC_HG(8)
       default: break;
     }
@@ -602,6 +617,9 @@ void forward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace
     case 2: launch_fwd_layers<2>(ps[0], L, n, st); break;
     case 3: launch_fwd_layers<3>(ps[0], L, n, st); break;
     case 4: launch_fwd_layers<4>(ps[0], L, n, st); break;
+    case 5: launch_fwd_layers<5>(ps[0], L, n, st); break;
+    case 6: launch_fwd_layers<6>(ps[0], L, n, st); break;
+    case 7: launch_fwd_layers<7>(ps[0], L, n, st); break;
     case 8: launch_fwd_layers<8>(ps[0], L, n, st); break;
     default: break;
   }
@@ -658,6 +676,9 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
     case 2: launch_bwd_layers<2>(ps[0], L, n, st); break;
     case 3: launch_bwd_layers<3>(ps[0], L, n, st); break;
     case 4: launch_bwd_layers<4>(ps[0], L, n, st); break;
+    case 5: launch_bwd_layers<5>(ps[0], L, n, st); break;
+    case 6: launch_bwd_layers<6>(ps[0], L, n, st); break;
+    case 7: launch_bwd_layers<7>(ps[0], L, n, st); break;
     case 8: launch_bwd_layers<8>(ps[0], L, n, st); break;
     default: break;
   }

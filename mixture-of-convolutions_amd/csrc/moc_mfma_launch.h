@@ -457,6 +457,9 @@ void launch_bwd_pre(const Problem& p, const void* x, const void* dy, const void*
 MOC_DECLARE_S(2)
 MOC_DECLARE_S(3)
 MOC_DECLARE_S(4)
+MOC_DECLARE_S(5)
+MOC_DECLARE_S(6)
+MOC_DECLARE_S(7)
 MOC_DECLARE_S(8)
 #undef MOC_DECLARE_S
 

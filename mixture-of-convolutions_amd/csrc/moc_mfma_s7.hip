@@ -1,0 +1,19 @@
+// MFMA forward / backward kernels instantiated for kernel size S = 7.
+#include "moc_mfma_launch.h"
+
+namespace moc {
+namespace mfma {
+
+template void launch_fwd<7>(const Problem&, const void*, const void*, const void*, void*,
+                             hipStream_t);
+template void launch_bwd<7>(const Problem&, const void*, const void*, const void*, const void*,
+                             void*, float*, float*, hipStream_t);
+template void launch_fwd_layers<7>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_bwd_layers<7>(const Problem&, const LayerOps*, int, hipStream_t);
+template void launch_fwd_pre<7>(const Problem&, const void*, const void*, const void*, void*,
+                                 const Pre&, hipStream_t);
+template void launch_bwd_pre<7>(const Problem&, const void*, const void*, const void*, const void*,
+                                 void*, float*, float*, const Pre&, hipStream_t);
+
+}  // namespace mfma
+}  // namespace moc

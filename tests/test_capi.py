@@ -232,7 +232,8 @@ def test_prefill_entries_validate_before_touching_the_device():
     assert L.moc_prefill_supported(2, 3, 16, 4, 4, _lib.DT_BF16, 1) == 1   # T = S-1
     assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 1) == 0   # T < S-1 with a cache
     assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 0) == 1   # no cache: any T
-    assert L.moc_prefill_supported(2, 8, 16, 4, 5, _lib.DT_BF16, 1) == 0   # no matrix-core S = 5
+    assert L.moc_prefill_supported(2, 8, 16, 4, 5, _lib.DT_BF16, 1) == 1   # S = 5
+    assert L.moc_prefill_supported(2, 8, 16, 4, 9, _lib.DT_BF16, 1) == 0   # no matrix-core S = 9
     assert L.moc_prefill_supported(2, 8, 18, 4, 4, _lib.DT_BF16, 1) == 0   # D % 4 != 0
     assert L.moc_prefill_supported(2, 8, 16, 33, 4, _lib.DT_F32, 1) == 0   # K > 32
     assert L.moc_prefill_supported(0, 8, 16, 4, 4, _lib.DT_BF16, 1) == 0
@@ -244,7 +245,7 @@ def test_prefill_entries_validate_before_touching_the_device():
     assert b"kernel_size - 1" in L.moc_last_error()
     assert _pre_fwd(seq_len=2, cache=None) == ERR_WORKSPACE  # no cache: T = 2 is fine
     assert _pre_fwd(x_dt=_lib.DT_F16) == ERR_DTYPE
-    assert _pre_fwd(ks=5) == ERR_ARG
+    assert _pre_fwd(ks=9, seq_len=9) == ERR_ARG
     assert _pre_fwd(x=None, ws_bytes=fwd_need) == ERR_ARG
     assert _pre_fwd(act=2) == ERR_ARG
     assert _pre_bwd() == ERR_WORKSPACE

@@ -24,6 +24,8 @@ CASES = [
     ([256, 192], 32, 4, 1, [0, 3], [True, True], torch.bfloat16),                 # route halves
     ([128, 64, 96, 32], 8, 2, 0, [0, 0, 4, 3], [False, True, True, True], torch.bfloat16),
     ([96, 64], 8, 2, 1, [0, 0], [True, True], torch.float32),                     # one by one
+    ([256, 128], 16, 6, 1, [3, 3], [True, True], torch.bfloat16),                 # 6 taps
+    ([128, 192, 64], 32, 7, 0, [4, 0, 3], [True, True, False], torch.bfloat16),  # 7 taps, halves
 ]
 
 

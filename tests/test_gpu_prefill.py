@@ -57,6 +57,9 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (8, 16, None, BF, 64),
     (4, 32, "silu", BF, 33),
     (4, 12, None, F32, 8),
+    (5, 16, "silu", BF, 9),
+    (6, 32, None, BF, 5),
+    (7, 16, "silu", F32, 6),
 ]
 
 
