@@ -49,7 +49,7 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st);
 
-// MFMA path (moc_mfma_common.hip): 2 <= S <= 8, K <= 32, D % 4 == 0
+// MFMA path (moc_mfma_common.hip): 2 <= S <= 8, K <= 64, D % 4 == 0
 namespace mfma {
 bool supported(const Problem& p);
 size_t forward_workspace(const Problem& p);

@@ -488,8 +488,10 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
             f32x4 w = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (BF && KC == 2) {
-              w = C::mma2(aop[b][0], aop[b][1], bop[c][s][0], bop[c][s][1], w);
+            if constexpr (BF && KC % 2 == 0) {
+#pragma unroll
+              for (int kp = 0; kp < KC; kp += 2)
+                w = C::mma2(aop[b][kp], aop[b][kp + 1], bop[c][s][kp], bop[c][s][kp + 1], w);
             } else {
 #pragma unroll
               for (int kc = 0; kc < KC; ++kc) w = C::mma(aop[b][kc], bop[c][s][kc], w);
@@ -705,10 +707,10 @@ constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 #define MOC_BWD_TAPS_WAVES MOC_BWD_MIN_WAVES
 #endif
 template <int S, int KC, int MODE, bool BF>
-constexpr int kBwdMinWaves = (MODE == kBwdFused && S >= 8 && KC >= 2 && BF) ? 1
+constexpr int kBwdMinWaves = (MODE == kBwdFused && ((S >= 8 && KC >= 2) || KC >= 4) && BF) ? 1
                              : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
-// bwd_tile is the work of workgroup (bx, by) (route half zh with SPLIT) of
+// bwd_tile is the work of workgroup (bx, by) (route chunk zh with SPLIT) of
 // one layer; the __global__ wrappers below map the grid onto it.  PRE (fused
 // pass only): prefill from a cache, whose values the masked taps read in P and
 // in the m products (the cache gradient is not formed here).
@@ -731,7 +733,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   // SPLIT the single chunk kc0 = zh (W still uses every route)
   constexpr int KX = SPLIT ? 1 : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
-  static_assert(!SPLIT || KC == 2, "the route split halves two route chunks");
+  static_assert(!SPLIT || KC % 2 == 0, "the route split takes an even number of route chunks");
   static_assert(!(SPLIT && MODE == kBwdTaps), "one split at a time");
   const int kc0 = SPLIT ? zh : 0;
   constexpr int EOWN = TB - (S - 1);
@@ -744,7 +746,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(MODE == kBwdFused || (BF && !ACT && S % 2 == 0),
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
-  static_assert(!PRE || (MODE == kBwdFused && !SPLIT), "prefill runs the fused pass");
+  static_assert(!PRE || MODE == kBwdFused, "prefill runs the fused pass");
   constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
   // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, S/2) and
   // [S/2, S): x and dy rows are read once per workgroup and the dalpha sum over
@@ -1016,8 +1018,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         auto issue = [&](int jb) {
           const int s = jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (BF && KC == 2) {
-            w4 = C::mma2(aop(0, b, 0), aop(0, b, 1), bop[c][s][0], bop[c][s][1], w4);
+          if constexpr (BF && KC % 2 == 0) {
+#pragma unroll
+            for (int kp = 0; kp < KC; kp += 2)
+              w4 = C::mma2(aop(0, b, kp), aop(0, b, kp + 1), bop[c][s][kp], bop[c][s][kp + 1], w4);
           } else {
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(0, b, kc), bop[c][s][kc], w4);
@@ -1080,8 +1084,11 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         auto issue = [&](int jb) {
           const int s = S - 1 - jb / (NB * NC), b = (jb / NC) % NB, c = jb % NC;
           f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (BF && KC == 2) {
-            w4 = C::mma2(aop(S - 1 - s, b, 0), aop(S - 1 - s, b, 1), bop[c][s][0], bop[c][s][1], w4);
+          if constexpr (BF && KC % 2 == 0) {
+#pragma unroll
+            for (int kp = 0; kp < KC; kp += 2)
+              w4 = C::mma2(aop(S - 1 - s, b, kp), aop(S - 1 - s, b, kp + 1), bop[c][s][kp],
+                           bop[c][s][kp + 1], w4);
           } else {
 #pragma unroll
             for (int kc = 0; kc < KC; ++kc) w4 = C::mma(aop(S - 1 - s, b, kc), bop[c][s][kc], w4);
@@ -1358,24 +1365,24 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   }
 }
 
-// Workgroup -> (channel group bx, token range by, route half zh) over a grid of
-// gx channel groups.  Split in route halves (SPLIT), the grid is 1-D and the two
-// halves of a tile are 8 workgroup ids apart: ids go round-robin over the 8
-// XCDs, so both halves run on one XCD at about the same time and the second
-// finds the tile's x / dy rows in that XCD's L2.  Returns false for the ids of
+// Workgroup -> (channel group bx, token range by, route chunk zh) over a grid of
+// gx channel groups.  Split in NZ route chunks, the grid is 1-D and the NZ
+// parts of a tile are 8 workgroup ids apart: ids go round-robin over the 8
+// XCDs, so the parts run on one XCD at about the same time and the later ones
+// find the tile's x / dy rows in that XCD's L2.  Returns false for the ids of
 // the 1-D grid past the last tile.
-// Block (x id, y id) of a 2-D grid, or id L of the 1-D grid of a split one.
-template <bool SPLIT>
+// Block (x id, y id) of a 2-D grid (NZ = 1), or id L of the 1-D grid of a split one.
+template <int NZ>
 __device__ __forceinline__ bool bwd_block(int gx, int gy, int idx, int idy, int& bx, int& by,
                                           int& zh) {
   bx = idx;
   by = idy;
   zh = 0;
-  if constexpr (SPLIT) {
+  if constexpr (NZ > 1) {
     const int L = idx;
-    const int t = (L >> 4) * 8 + (L & 7);
+    const int t = (L / (8 * NZ)) * 8 + (L & 7);
     if (t >= gx * gy) return false;
-    zh = (L >> 3) & 1;
+    zh = (L >> 3) % NZ;
     bx = t % gx;
     by = t / gx;
   }
@@ -1391,7 +1398,7 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
            int gx, int gy, int gy1, int n_old, int n_total) {
   int bx, by, zh;
-  if (!bwd_block<SPLIT>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), bx,
+  if (!bwd_block<SPLIT ? KC : 1>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), bx,
                         by, zh))
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(xv, dyv, dys, a_c, b_c, dxv, part_da, part_db,
@@ -1400,22 +1407,28 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
 
 // Prefill from a cache (Pre): the fused pass on a 2-D grid (bf16 with 32
 // routes, which the plain backward splits, at one wave per SIMD: both route
-// chunks' accumulators and operands stay in registers; with 8 taps at two, as
-// LLVM's AGPR-copy rewrite crashes on the one-wave form).
+// chunks' accumulators and operands stay in registers; with 8 taps or 64
+// routes at two, as LLVM's AGPR-copy rewrite crashes on those one-wave forms).
 template <int S, int KC, bool BF>
-constexpr int kBwdPreWaves = (BF && KC >= 2 && S < 8) ? 1
+constexpr int kBwdPreWaves = (BF && KC == 2 && S < 8) ? 1
                              : (BF && KC >= 2) ? 2 : kBwdMinWaves<S, KC, kBwdFused, BF>;
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
+// With 64 routes (SPLIT) it is split in route chunks like the plain pass.
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdPreWaves<S, KC, BF>)))
+__attribute__((amdgpu_waves_per_eu(SPLIT ? kBwdMinWaves<S, KC, kBwdFused, BF>
+                                         : kBwdPreWaves<S, KC, BF>)))
 bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                const typename CT<BF>::elem* __restrict__ a_c,
                const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
                float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
                int gx, int gy, int gy1, int n_old, int n_total, Pre pre) {
-  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, false, kBwdFused, true>(
-      xv, dyv, dys, a_c, b_c, dxv, part_da, part_db, seq, D, static_cast<int>(blockIdx.x),
-      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre);
+  int bx, by, zh;
+  if (!bwd_block<SPLIT ? KC : 1>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y),
+                                 bx, by, zh))
+    return;  // whole workgroup, before any barrier
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, kBwdFused, true>(
+      xv, dyv, dys, a_c, b_c, dxv, part_da, part_db, seq, D, bx, by, zh, gy, gy1, n_old, n_total,
+      pre);
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another:
@@ -1437,7 +1450,7 @@ bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
     }
   }
   int bx, by, zh;
-  if (!bwd_block<SPLIT>(Lp->gx, Lp->gy, local, row, bx, by, zh))
+  if (!bwd_block<SPLIT ? KC : 1>(Lp->gx, Lp->gy, local, row, bx, by, zh))
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(
       Lp->x, Lp->dy, Lp->dys, static_cast<const E*>(Lp->a), static_cast<const E*>(Lp->b), Lp->dx,

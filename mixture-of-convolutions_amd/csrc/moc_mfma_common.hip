@@ -305,17 +305,17 @@ struct Plan {
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 bool direct(const Problem& p, const void* alpha, const void* basis, const void* dalpha) {
-  // K = 16 or 32: the caller's [N, K] weights and [K, S, D] basis are then the
+  // K = 16, 32 or 64: the caller's [N, K] weights and [K, S, D] basis are then the
   // kernels' padded operand layouts (KP = K) as they are; PATH_MFMA_PREP forces
   // the prep launch (an A/B switch)
   return p.path != PATH_MFMA_PREP && route_form(p.routing) == ROUTE_ALPHA && p.x_dt == DT_BF16 &&
-         p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && (p.K == 16 || p.K == 32) &&
+         p.a_dt == DT_BF16 && p.b_dt == DT_BF16 && (p.K == 16 || p.K == 32 || p.K == 64) &&
          aligned16(alpha) && aligned16(basis) && aligned16(dalpha);
 }
 
 Plan plan(const Problem& p, bool backward) {
   Plan pl{};
-  pl.KP = static_cast<int>(16 * ((p.K + 15) / 16));
+  pl.KP = 16 * route_chunks(p.K);
   pl.esz = (p.x_dt == DT_BF16) ? 2 : 4;
   size_t off = 0;
   pl.off_ac = off;
@@ -357,9 +357,12 @@ void launch_prep(const Problem& p, const Plan& pl, const void* alpha, const void
   if (pl.KP == 16) {
     if (bf) prep_one<true, 1>(p, pl, alpha, basis, ws, keep_ar, st);
     else prep_one<false, 1>(p, pl, alpha, basis, ws, keep_ar, st);
-  } else {
+  } else if (pl.KP == 32) {
     if (bf) prep_one<true, 2>(p, pl, alpha, basis, ws, keep_ar, st);
     else prep_one<false, 2>(p, pl, alpha, basis, ws, keep_ar, st);
+  } else {
+    if (bf) prep_one<true, 4>(p, pl, alpha, basis, ws, keep_ar, st);
+    else prep_one<false, 4>(p, pl, alpha, basis, ws, keep_ar, st);
   }
 }
 
@@ -378,17 +381,10 @@ void launch_stage2(const Problem& p, const Plan& pl, bool dir, char* ws, const v
   const auto* a_w = static_cast<const uint16_t*>(alpha);
   const dim3 grid(static_cast<unsigned>(da_blocks + db_blocks));
   const int64_t n_da = pl.bg.gx;
-  if (pl.KP == 16) {
-    hipLaunchKernelGGL(stage2_kernel<1>, grid, dim3(256), 0, st, pda, n_da, pdb,
-                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
-                       p.b_dt, p.n_tokens,
-                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
-  } else {
-    hipLaunchKernelGGL(stage2_kernel<2>, grid, dim3(256), 0, st, pda, n_da, pdb,
-                       static_cast<int64_t>(pl.bg.gy), a_r, a_w, dalpha, p.a_dt, grad, dbasis,
-                       p.b_dt, p.n_tokens,
-                       static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
-  }
+  auto kern = pl.KP == 16 ? stage2_kernel<1> : (pl.KP == 32 ? stage2_kernel<2> : stage2_kernel<4>);
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, st, pda, n_da, pdb, static_cast<int64_t>(pl.bg.gy),
+                     a_r, a_w, dalpha, p.a_dt, grad, dbasis, p.b_dt, p.n_tokens,
+                     static_cast<int>(p.K), static_cast<int>(p.S), p.D, da_blocks);
 }
 
 }  // namespace
@@ -397,7 +393,7 @@ bool supported(const Problem& p) {
   const bool s_ok = p.S >= 2 && p.S <= 8;
   // the grids' y dimensions stay within the 65535 launch limit and one
   // super-block's rows within a buffer's 32-bit range
-  return s_ok && p.K >= 1 && p.K <= 32 && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
+  return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && p.x_dt == DT_BF16)) && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
          (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
          bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D, p.S).gy <= 65535;
 }
@@ -505,7 +501,8 @@ void hist_grad_one(const Problem& p, const void* x, const void* a_c, const void*
                    const void* dy, const void* cache, void* dcache, int KP, hipStream_t st) {
   using E = typename CT<BF>::elem;
   const int64_t B = p.n_tokens / p.seq.seq_len;
-  auto kern = KP == 16 ? hist_grad_kernel<S, 1, BF> : hist_grad_kernel<S, 2, BF>;
+  auto kern = KP == 16 ? hist_grad_kernel<S, 1, BF>
+                       : (KP == 32 ? hist_grad_kernel<S, 2, BF> : hist_grad_kernel<S, 4, BF>);
   hipLaunchKernelGGL(kern,
                      dim3(static_cast<unsigned>(cdiv(p.D, 64)), static_cast<unsigned>(B)),
                      dim3(64), 0, st, static_cast<const E*>(x), static_cast<const E*>(a_c),
@@ -684,12 +681,10 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
   }
   prof_end(ps[0], st);
   const int K = static_cast<int>(ps[0].K), S = static_cast<int>(ps[0].S);
-  if (K <= 16)
-    hipLaunchKernelGGL(stage2_layers_kernel<1>, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st,
-                       s2, N, K, S, da_blocks);
-  else
-    hipLaunchKernelGGL(stage2_layers_kernel<2>, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st,
-                       s2, N, K, S, da_blocks);
+  auto kern = K <= 16 ? stage2_layers_kernel<1>
+                      : (K <= 32 ? stage2_layers_kernel<2> : stage2_layers_kernel<4>);
+  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, s2, N, K, S,
+                     da_blocks);
 }
 
 }  // namespace mfma

@@ -45,6 +45,14 @@ struct Grid2 {
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Route chunks of 16 the kernels are built for: 1, 2 or 4 (K <= 64; K in
+// (32, 64] is padded to 64 routes).  Four chunks with bf16 data only: the fp32
+// fused backward at four chunks crashes LLVM's AGPR-copy rewrite, so fp32 x
+// with K > 32 stays on the generic kernels.
+inline int route_chunks(int64_t K) { return K <= 16 ? 1 : (K <= 32 ? 2 : 4); }
+template <int KC, bool BF>
+constexpr bool kcOK = KC <= 2 || BF;
+
 // Forward: about kFwdTargetWG workgroups, each wave walking at most
 // kFwdMaxSb super-blocks; larger problems get more workgroups rather than
 // longer ones (measured: D 4096, 32768 tokens, 161 -> 141 us).
@@ -157,8 +165,8 @@ constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && KC == 2 && S == 8;
 }
 inline bool bwd_two_pass(const Problem& p) {
-  return !p.pre && bwd_two_pass(static_cast<int>(p.S), static_cast<int>((p.K + 15) / 16),
-                                p.activation != 0, p.x_dt == DT_BF16);
+  return !p.pre && bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,
+                                p.x_dt == DT_BF16);
 }
 
 // The taps pass holds one workgroup per CU (its LDS), so it runs as one round
@@ -194,22 +202,27 @@ struct LayerOps {
 template <int S, int KC, bool ACT, bool BF>
 void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
              hipStream_t st) {
+  if constexpr (!kcOK<KC, BF>) return;
+  else {
   using E = typename CT<BF>::elem;
   const Grid2 g = fwd_grid(p.n_tokens, p.D, S);
   hipLaunchKernelGGL((fwd_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256), 0,
                      st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq, p.D,
                      g.n_sb);
+  }
 }
 
-// Fused pass with 32 routes (bf16): each workgroup accumulates dbasis / dalpha
-// for one of the two 16-route chunks, as the accumulators and dalpha operands
-// of both would not fit in registers beside the W operands.
+// Fused pass with 32 or 64 routes (bf16): each workgroup accumulates dbasis /
+// dalpha for one of the 16-route chunks, as the accumulators and dalpha
+// operands of all would not fit in registers beside the W operands.
 template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
              void* dx, float* part_da, float* part_db, hipStream_t st) {
+  if constexpr (!kcOK<KC, BF>) return;
+  else {
   using E = typename CT<BF>::elem;
-  constexpr bool kSplit = BF && KC == 2;
-  // tiers for the fused pass at two resident workgroups per CU (not split in halves)
+  constexpr bool kSplit = BF && KC >= 2;
+  // tiers for the fused pass at two resident workgroups per CU (not split in route chunks)
   constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
   const int64_t gx_all = cdiv(p.D, kBwdCW);
   const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, gx_all, p.D, S, device_cu_count())
@@ -217,8 +230,8 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   const auto* a = static_cast<const E*>(a_c);
   const auto* b = static_cast<const E*>(b_c);
   const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
-  // a grid split in halves is 1-D: 16 workgroups per 8 tiles (see bwd_kernel)
-  const dim3 halves(static_cast<unsigned>(16 * cdiv(static_cast<int64_t>(gx) * gy, 8)));
+  // a grid split in route chunks is 1-D: 8 KC workgroups per 8 tiles (see bwd_block)
+  const dim3 halves(static_cast<unsigned>(8 * KC * cdiv(static_cast<int64_t>(gx) * gy, 8)));
   if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
     if (dx != nullptr)
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
@@ -237,6 +250,7 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a,
                        b, dx, part_da, part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
+  }
   }
 }
 
@@ -259,7 +273,7 @@ void fwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
 
 template <int S, int KC, bool ACT>
 void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
-  constexpr bool kSplit = KC == 2;
+  constexpr bool kSplit = KC >= 2;
   constexpr bool kTwo = bwd_two_pass(S, KC, ACT, true);
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, true> == 2;
   const int n_cu = device_cu_count();
@@ -278,7 +292,7 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
     const int64_t tiles = static_cast<int64_t>(g.gx) * g.gy;
     // the dx pass of the two-pass form skips layers without dx (no blocks:
     // layer_index then never selects them)
-    blk += kSplit ? 16 * cdiv(tiles, 8) : (kTwo && L[i].dx == nullptr ? 0 : tiles);
+    blk += kSplit ? 8 * KC * cdiv(tiles, 8) : (kTwo && L[i].dx == nullptr ? 0 : tiles);
     any_dx = any_dx || L[i].dx != nullptr;
     if constexpr (kTwo) {
       const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(L[i].D, kTapsCW), L[i].D, S, n_cu);
@@ -311,9 +325,12 @@ void launch_fwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t s
   if (p.K <= 16) {
     if (act) fwd_layers_one<S, 1, true>(p, L, n, st);
     else fwd_layers_one<S, 1, false>(p, L, n, st);
-  } else {
+  } else if (p.K <= 32) {
     if (act) fwd_layers_one<S, 2, true>(p, L, n, st);
     else fwd_layers_one<S, 2, false>(p, L, n, st);
+  } else {
+    if (act) fwd_layers_one<S, 4, true>(p, L, n, st);
+    else fwd_layers_one<S, 4, false>(p, L, n, st);
   }
 }
 
@@ -323,9 +340,12 @@ void launch_bwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t s
   if (p.K <= 16) {
     if (act) bwd_layers_one<S, 1, true>(p, L, n, st);
     else bwd_layers_one<S, 1, false>(p, L, n, st);
-  } else {
+  } else if (p.K <= 32) {
     if (act) bwd_layers_one<S, 2, true>(p, L, n, st);
     else bwd_layers_one<S, 2, false>(p, L, n, st);
+  } else {
+    if (act) bwd_layers_one<S, 4, true>(p, L, n, st);
+    else bwd_layers_one<S, 4, false>(p, L, n, st);
   }
 }
 
@@ -333,7 +353,7 @@ void launch_bwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t s
 template <int S>
 void launch_fwd(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
                 hipStream_t st) {
-  const int kc = static_cast<int>((p.K + 15) / 16);
+  const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
 #define MOC_FWD(KC_)                                              \
   if (kc == KC_) {                                                \
@@ -348,13 +368,14 @@ void launch_fwd(const Problem& p, const void* x, const void* a_c, const void* b_
   }
   MOC_FWD(1)
   MOC_FWD(2)
+  MOC_FWD(4)
 #undef MOC_FWD
 }
 
 template <int S>
 void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
                 void* dx, float* part_da, float* part_db, hipStream_t st) {
-  const int kc = static_cast<int>((p.K + 15) / 16);
+  const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
 #define MOC_BWD(KC_)                                                                          \
   if (kc == KC_) {                                                                            \
@@ -369,6 +390,7 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
   }
   MOC_BWD(1)
   MOC_BWD(2)
+  MOC_BWD(4)
 #undef MOC_BWD
 }
 
@@ -379,30 +401,40 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
 template <int S, int KC, bool ACT, bool BF>
 void fwd_pre_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
                  const Pre& pre, hipStream_t st) {
+  if constexpr (!kcOK<KC, BF>) return;
+  else {
   using E = typename CT<BF>::elem;
   const Grid2 g = fwd_grid(p.n_tokens, p.D, S);
   hipLaunchKernelGGL((fwd_pre_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, BF>), dim3(g.gx, g.gy), dim3(256),
                      0, st, x, static_cast<const E*>(a_c), static_cast<const E*>(b_c), y, p.seq,
                      p.D, g.n_sb, pre);
+  }
 }
 
 template <int S, int KC, bool ACT, bool BF>
 void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_c,
                  const void* b_c, void* dx, float* part_da, float* part_db, const Pre& pre,
                  hipStream_t st) {
+  if constexpr (!kcOK<KC, BF>) return;
+  else {
   using E = typename CT<BF>::elem;
   const Grid2 g = bwd_partials_grid(p);
-  hipLaunchKernelGGL((bwd_pre_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF>), dim3(g.gx, g.gy),
+  // 64 routes: split in route chunks on a 1-D grid, as bwd_one does
+  constexpr bool kSplit = BF && KC >= 4;
+  const dim3 grid = kSplit ? dim3(static_cast<unsigned>(8 * KC * cdiv(int64_t(g.gx) * g.gy, 8)))
+                           : dim3(g.gx, g.gy);
+  hipLaunchKernelGGL((bwd_pre_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit>), grid,
                      dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, static_cast<const E*>(a_c),
                      static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D,
                      static_cast<int>(g.gx), static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total,
                      pre);
+  }
 }
 
 template <int S>
 void launch_fwd_pre(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
                     const Pre& pre, hipStream_t st) {
-  const int kc = static_cast<int>((p.K + 15) / 16);
+  const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
 #define MOC_FWD(KC_)                                                        \
   if (kc == KC_) {                                                          \
@@ -417,6 +449,7 @@ void launch_fwd_pre(const Problem& p, const void* x, const void* a_c, const void
   }
   MOC_FWD(1)
   MOC_FWD(2)
+  MOC_FWD(4)
 #undef MOC_FWD
 }
 
@@ -424,7 +457,7 @@ template <int S>
 void launch_bwd_pre(const Problem& p, const void* x, const void* dy, const void* a_c,
                     const void* b_c, void* dx, float* part_da, float* part_db, const Pre& pre,
                     hipStream_t st) {
-  const int kc = static_cast<int>((p.K + 15) / 16);
+  const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
 #define MOC_BWD(KC_)                                                                                \
   if (kc == KC_) {                                                                                  \
@@ -439,6 +472,7 @@ void launch_bwd_pre(const Problem& p, const void* x, const void* dy, const void*
   }
   MOC_BWD(1)
   MOC_BWD(2)
+  MOC_BWD(4)
 #undef MOC_BWD
 }
 

@@ -8,7 +8,8 @@
 // run the products on the matrix cores (v_mfma_f32_16x16x32_bf16, 16x16x16 for
 // dz with K = 16); accumulation is fp32, results are rounded to bf16 once.
 // drouter is reduced in a fixed order (per-range partials, then one sum), so it
-// is bitwise reproducible.  bf16 data only; K % 4 == 0, K <= 32, Z % 64 == 0.
+// is bitwise reproducible.  bf16 data only; K % 4 == 0, K <= 96 (the fused
+// activation K <= 32), Z % 64 == 0.
 
 #include "moc_kernels.h"
 #include "moc_mfma.h"

@@ -179,7 +179,8 @@ def test_config5_qkv_triple():
 @pytest.mark.parametrize("S,K,act", [(2, 8, "silu"), (3, 16, "silu"), (4, 16, "silu"), (4, 32, "silu"),
                                      (5, 16, "silu"), (5, 32, None), (6, 16, None), (6, 32, "silu"),
                                      (7, 12, None), (7, 32, "silu"),
-                                     (8, 32, "silu"), (8, 32, None), (8, 5, "silu")])
+                                     (8, 32, "silu"), (8, 32, None), (8, 5, "silu"),
+                                     (4, 64, "silu"), (2, 48, None), (8, 64, None)])
 def test_mfma_matches_generic(dtype, S, K, act):
     """Mid-size problems through both kernel families, fixed and packed, for
     every kernel size the matrix-core kernels are built for (2-8; bf16, 8 taps,

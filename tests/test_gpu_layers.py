@@ -26,6 +26,7 @@ CASES = [
     ([96, 64], 8, 2, 1, [0, 0], [True, True], torch.float32),                     # one by one
     ([256, 128], 16, 6, 1, [3, 3], [True, True], torch.bfloat16),                 # 6 taps
     ([128, 192, 64], 32, 7, 0, [4, 0, 3], [True, True, False], torch.bfloat16),  # 7 taps, halves
+    ([256, 128], 64, 4, 1, [3, 0], [True, True], torch.bfloat16),                 # 64 routes
 ]
 
 

@@ -480,6 +480,41 @@ def test_routed_function_dlogits(route, dtype):
     assert_close("dbasis", bb.grad, rb.grad, dtype)
 
 
+@pytest.mark.parametrize("Kr,S,route", [(48, 4, "softmax"), (64, 4, "exp"), (64, 8, "softmax"),
+                                        (40, 2, "softmax")])
+def test_routed_function_64_routes(Kr, S, route):
+    """More than 32 routes (bf16; K in (32, 64] padded to 64 in the kernels):
+    the logits-input function's y, dx, d(logits) and dbasis against the oracle,
+    and the same through the generic kernels."""
+    from moc import _lib, api
+    dtype = torch.bfloat16
+    g = gen(Kr + S)
+    Bn, Tn, Dn = 2, 150, 192
+    x = randn(g, Bn, Tn, Dn, scale=0.5).to(DEV, dtype)
+    lg = randn(g, Bn, Tn, Kr).to(DEV, dtype)
+    b = randn(g, Kr, S, Dn, scale=0.1).to(DEV, dtype)
+    dy = randn(g, Bn, Tn, Dn).to(DEV, dtype)
+
+    def run():
+        xx, ll, bb = (t.clone().requires_grad_() for t in (x, lg, b))
+        y = api._MoCRoutedFunction.apply(xx, ll, bb, "silu", route, None, None, None, None)
+        y.backward(dy)
+        return y.detach(), xx.grad, ll.grad, bb.grad
+
+    rx = x.float().cpu().requires_grad_()
+    rl = lg.float().cpu().requires_grad_()
+    rb = b.float().cpu().requires_grad_()
+    ry = O.moc_ref(rx, O.route(rl, route, out_dtype=dtype), rb, "silu")
+    ry.backward(dy.float().cpu())
+    got = run()
+    with _lib.kernel_path(_lib.PATH_GENERIC):
+        other = run()
+    for n, u, v, r in zip(("y", "dx", "dlogits", "dbasis"), got, other,
+                          (ry, rx.grad, rl.grad, rb.grad)):
+        assert_close(n, u, r, dtype)
+        assert_close(n + " (generic)", v, r, dtype)
+
+
 @pytest.mark.parametrize("T2,S", [(10, 4), (2, 4), (3, 4), (7, 2), (5, 8), (40, 3), (4, 8)])
 def test_prefill_matches_concatenated_history(T2, S):
     """Prefill from a cache against the reference's formulation of it

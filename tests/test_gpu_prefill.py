@@ -60,6 +60,8 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (5, 16, "silu", BF, 9),
     (6, 32, None, BF, 5),
     (7, 16, "silu", F32, 6),
+    (4, 64, "silu", BF, 21),
+    (3, 48, None, BF, 7),
 ]
 
 
