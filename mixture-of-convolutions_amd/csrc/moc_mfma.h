@@ -171,6 +171,15 @@ __device__ __forceinline__ uint32_t row_off(int64_t t, int64_t lo, uint32_t row_
 
 __device__ __forceinline__ float silu_f(float p) { return p * sigmoid_f(p); }
 
+// Two fp32 rounded to bf16 (nearest even) in one dword, a in the low half: one
+// v_cvt_pk_bf16_f32 (two scalar conversions compile to two conversions, a
+// shift and an OR).
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
 // Sequence starts near a super-block.  A tap s of token t is valid when its
 // source t-(S-1-s) is not before t's segment start.  All starts that can
 // invalidate a tap of the rows [r0, r1] lie in [r0 - (S-2), r1]; `starts_in`
@@ -422,17 +431,21 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
   // alpha A operands (row i = j of block b is token t0 + R*(j/4) + 4b + j%4)
   E xr[W][NC];
   Op ar[NB][KC];
+  // Window row w sits at base + w rb: rows before row_lo wrap to offsets
+  // >= 2^31 and load zeros, and a lane past the channel axis starts at
+  // kOffNone (row_off); the alpha rows of block b and route chunk kc sit a
+  // constant (immediate) offset from the lane's first one.
   auto fetch = [&](int64_t t0) {
     const int64_t trun = t0 + R * q;
+    const uint32_t base = row_off(trun - (S - 1), row_lo, rb, col, ch_ok);
 #pragma unroll
-    for (int w = 0; w < W; ++w)
-      xb.load<NC * ESZ>(row_off(trun - (S - 1) + w, row_lo, rb, col, ch_ok), xr[w]);
+    for (int w = 0; w < W; ++w) xb.load<NC * ESZ>(base + w * rb, xr[w]);
+    const uint32_t abase = row_off(t0 + R * (j >> 2) + (j & 3), tbase, KP * ESZ, 4 * q * ESZ);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const int64_t tok = t0 + R * (j >> 2) + 4 * b + (j & 3);
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc)
-        ab.load<4 * ESZ>(row_off(tok, tbase, KP * ESZ, (16 * kc + 4 * q) * ESZ), &ar[b][kc]);
+        ab.load<4 * ESZ>(abase + static_cast<uint32_t>((4 * b * KP + 16 * kc) * ESZ), &ar[b][kc]);
     }
   };
 
@@ -447,14 +460,21 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
 #pragma unroll
     for (int w = 0; w < W; ++w)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
+      for (int c = 0; c < NC; ++c) {
+        xw[w][c] = C::to_f(xr[w][c]);
+        asm volatile("" : "+v"(xw[w][c]));  // converted here, not sunk below the loads
+      }
     Op aop[NB][KC];
 #pragma unroll
     for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int kc = 0; kc < KC; ++kc) aop[b][kc] = ar[b][kc];
-    // issue the next super-block's loads before computing this one
-    if (sb + 1 < n_sb && t0 + TB < N) fetch(t0 + TB);
+    // issue the next super-block's loads before computing this one; after the
+    // last super-block they fall past the buffers and load zeros.  Issued
+    // unconditionally and after the conversions above, they land in the
+    // registers the rows just left, and the loop carries them without copies.
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(t0 + TB);
 
     // uniform over the wave: does a sequence start fall where it masks a tap?
     const int64_t w_lo = t0 - (S - 2), w_hi = t0 + TB - 1;
@@ -504,12 +524,19 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
             }
           }
       }
+      const uint32_t ybase = row_off(trun, row_lo, rb, col, ch_ok);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         E o[NC];
+        if constexpr (BF && NC == 2) {
+          const uint32_t pk = ACT ? pack2_bf16(silu_f(acc[r][0]), silu_f(acc[r][1]))
+                                  : pack2_bf16(acc[r][0], acc[r][1]);
+          __builtin_memcpy(o, &pk, 4);
+        } else {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
-        yb.store<NC * ESZ>(row_off(trun + r, row_lo, rb, col, ch_ok), o);
+          for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
+        }
+        yb.store<NC * ESZ>(ybase + r * rb, o);
       }
     };
     if (interior) body(std::false_type{});
@@ -596,11 +623,6 @@ __device__ __forceinline__ s16x4 pack4_hi(uint32_t a, uint32_t b, uint32_t c, ui
 }
 
 // Four fp32 rounded to bf16 (nearest even) in MFMA operand order.
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  typedef float f32x2 __attribute__((ext_vector_type(2)));
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
 __device__ __forceinline__ s16x4 pack4_bf16(float a, float b, float c, float d) {
   typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
   const u32x2 w = {pack2_bf16(a, b), pack2_bf16(c, d)};
@@ -948,21 +970,39 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     const int64_t own_end = (t0 + EOWN < N) ? t0 + EOWN : N;
     const int64_t trun = t0 + R * q;
 
+    // without the activation, the fused and dx passes convert the rows here,
+    // before the next super-block's loads (not sunk below them), so that those
+    // loads land in the registers the rows just left and the loop carries them
+    // without copies: configs[2] and configs[4] steps -1%; the SiLU pass
+    // measured 1 us slower this way, and the prefill pass's one-wave forms
+    // crash LLVM's AGPR-copy rewrite with it
+    constexpr bool kPin = MODE != kBwdTaps && !PRE && !ACT;
     float xw[WX][NC];
     float g[R][NC];
     if constexpr (NEED_X)
 #pragma unroll
       for (int w = 0; w < WX; ++w)
 #pragma unroll
-        for (int c = 0; c < NC; ++c) xw[w][c] = C::to_f(xr[w][c]);
+        for (int c = 0; c < NC; ++c) {
+          xw[w][c] = C::to_f(xr[w][c]);
+          if constexpr (kPin) asm volatile("" : "+v"(xw[w][c]));
+        }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) g[r][c] = C::to_f(dr[r][c]);
+      for (int c = 0; c < NC; ++c) {
+        g[r][c] = C::to_f(dr[r][c]);
+        if constexpr (kPin) asm volatile("" : "+v"(g[r][c]));
+      }
     const bool more = (sb + 1 < nsb) && (t0 + EOWN < N);
     // the taps pass loads the next x / dy rows after its m products, where
-    // fewer registers are live (issued here, they were spilled in the body)
-    if (more) {
+    // fewer registers are live (issued here, they were spilled in the body);
+    // the others load them here (kPin: also after the last super-block of the
+    // range, whose next rows fall past the buffers or are never used)
+    if constexpr (kPin) {
+      __builtin_amdgcn_sched_barrier(0);
+      fetch(t0 + EOWN);
+    } else if (more) {
       if constexpr (MODE == kBwdTaps) fetch_a(t0 + EOWN);
       else fetch(t0 + EOWN);
     }

@@ -24,7 +24,10 @@ namespace mfma {
 constexpr int kFwdNB = 2, kFwdNC = MOC_FWD_NC;
 // token blocks per forward super-block for kernel size S
 constexpr int fwd_nb(int S) { return S == 8 ? MOC_FWD_NB8 : kFwdNB; }
-constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = 4;
+#ifndef MOC_BWD_WPG
+#define MOC_BWD_WPG 4
+#endif
+constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = MOC_BWD_WPG;
 // Resident workgroups the grids are sized for (256 CUs).
 #ifndef MOC_FWD_TARGET_WG
 #define MOC_FWD_TARGET_WG 2048
