@@ -58,7 +58,7 @@ extern "C" {
 #define MOC_ERR_WORKSPACE -3
 #define MOC_ERR_HIP       -4
 
-/* ABI version of this header. */
+/* ABI version of this header (4: dy_row_stride -1 accepted). */
 int moc_abi_version(void);
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -121,8 +121,9 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
  * launch_backward (moc/ops.py:216-338) and the preact recompute it needed
  * (moc/ops.py:197-213), i.e. _moc_bwd_dx_kernel (moc/kernels.py:156-279) and
  * _moc_bwd_dalpha_dbasis_dot_kernel (moc/kernels.py:282-439).
- *   dy     : token rows dy_row_stride elements apart: dim (contiguous), or 0
- *            when one row of dim elements is the gradient of every token (the
+ *   dy     : token rows dy_row_stride elements apart: dim (contiguous); 0
+ *            when one row of dim elements is the gradient of every token; -1
+ *            when one element is the gradient of every token and channel (the
  *            broadcast gradient of y.sum(), which the reference copied into a
  *            contiguous tensor with dy.contiguous(), moc/api.py:171)
  *   dx     : [n_tokens, dim] in x_dtype, or NULL to skip it (need_x = False)
@@ -197,7 +198,7 @@ int moc_forward_prefill(const void* x, const void* alpha, const void* basis, voi
 
 /*
  * Gradients of moc_forward_prefill (cache required): moc_backward's dx,
- * dalpha and dbasis (arguments as there), plus
+ * dalpha and dbasis (arguments as there; dy_row_stride dim or 0), plus
  *   dcache : [n_seqs, dim, kernel_size] in x_dtype, or NULL to skip it: the
  *            gradient of the cache (slot 0 is read by no output and gets 0).
  * A gradient of the final state is not an input: its dx / dcache part is a

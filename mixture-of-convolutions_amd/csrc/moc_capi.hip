@@ -140,7 +140,7 @@ int hip_status(const char* what) {
 
 extern "C" {
 
-int moc_abi_version(void) { return 3; }
+int moc_abi_version(void) { return 4; }
 
 const char* moc_last_error(void) { return g_err; }
 
@@ -228,9 +228,9 @@ int backward_problem(const void* x, const void* alpha, const void* basis, const 
   if ((rc = check_seq(cu_seqlens, n_seqs, seq_len)) != MOC_OK) return rc;
   if (!x || !alpha || !basis || !dy || !dalpha || !dbasis)
     return fail(MOC_ERR_ARG, "null tensor pointer");
-  if (dy_row_stride != 0 && dy_row_stride != dim)
-    return fail(MOC_ERR_ARG, "dy_row_stride must be dim (%lld) or 0, got %lld", (long long)dim,
-                (long long)dy_row_stride);
+  if (dy_row_stride != 0 && dy_row_stride != dim && dy_row_stride != -1)
+    return fail(MOC_ERR_ARG, "dy_row_stride must be dim (%lld), 0 or -1, got %lld",
+                (long long)dim, (long long)dy_row_stride);
   if ((n_tokens + 255) / 256 > 65535)
     return fail(MOC_ERR_ARG, "n_tokens too large for the backward grid: %lld", (long long)n_tokens);
   p = make_problem(cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len, dim, k, kernel_size,
@@ -455,9 +455,9 @@ int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu6
     ps[i] = make_problem(cu, cu64, n_seqs, n_tokens, seq_len, l.dim, k, ks, x_dt, l.alpha_dtype,
                          l.basis_dtype, activation, l.routing);
     if (backward) {
-      if (l.dy_row_stride != 0 && l.dy_row_stride != l.dim)
-        return fail(MOC_ERR_ARG, "layer %d: dy_row_stride must be dim (%lld) or 0, got %lld", i,
-                    (long long)l.dim, (long long)l.dy_row_stride);
+      if (l.dy_row_stride != 0 && l.dy_row_stride != l.dim && l.dy_row_stride != -1)
+        return fail(MOC_ERR_ARG, "layer %d: dy_row_stride must be dim (%lld), 0 or -1, got %lld",
+                    i, (long long)l.dim, (long long)l.dy_row_stride);
       ps[i].dy_stride = l.dy_row_stride;
     }
   }

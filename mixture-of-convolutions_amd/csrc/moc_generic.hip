@@ -90,7 +90,7 @@ __global__ void fwd_generic_kernel(const void* __restrict__ x, int x_dt,
 
 // ---------------------------------------------------------------------------
 // Backward.  g = dy * silu'(P) (or dy), kept in fp32 scratch; dy rows are
-// dys elements apart (0: one row for every token).
+// dys elements apart (0: one row for every token; -1: one element for all).
 __global__ void bwd_g_kernel(const void* __restrict__ x, const void* __restrict__ dy, int64_t dys,
                              int x_dt, const float* __restrict__ a_r,
                              const float* __restrict__ basis_c, float* __restrict__ g,
@@ -99,7 +99,7 @@ __global__ void bwd_g_kernel(const void* __restrict__ x, const void* __restrict_
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t t = i / D, d = i - t * D;
-    float gv = load_any(dy, x_dt, t * dys + d);
+    float gv = load_any(dy, x_dt, dys < 0 ? 0 : t * dys + d);
     if (activation) {
       int64_t lo, hi;
       seq.bounds(t, lo, hi);

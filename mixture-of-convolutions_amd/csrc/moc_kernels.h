@@ -19,7 +19,8 @@ struct Problem {
   int x_dt, a_dt, b_dt;
   int activation;    // 0 = none, 1 = SiLU
   int routing;       // Route
-  int64_t dy_stride = 0;  // backward: elements between token rows of dy (D, or 0 = one row for all)
+  int64_t dy_stride = 0;  // backward: elements between token rows of dy (D; 0: one row for all
+                          // tokens; -1: one element for every token and channel)
   int path = PATH_AUTO;   // PATH_MFMA_PREP: MFMA kernels, operands always through prep
   bool pre = false;       // prefill from a cache: the backward is the fused pass for every shape
   hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set

@@ -342,7 +342,7 @@ struct FwdLayers {
 struct BwdLayer {
   const void* x;
   const void* dy;
-  int64_t dys;     // dy row stride (elements): D, or 0 for one broadcast row
+  int64_t dys;     // dy row stride (elements): D, 0 for one broadcast row, -1 for one element
   const void* a;
   const void* b;
   void* dx;
@@ -705,7 +705,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 // double buffered; x / dy rows of the next super-block are loaded before the
 // current one is computed.
 // dy rows are dys elements apart: D, or 0 when one row serves every token (the
-// broadcast gradient of a sum).
+// broadcast gradient of a sum), or -1 when one element serves every token and
+// channel (the gradient of a sum to a scalar, expanded).
 // Outputs: dx (own rows), part_da[bx][t][KP], part_db[by][KP][S][D] for channel
 // group bx and token range by.
 //
@@ -841,9 +842,23 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   const uint32_t rb = static_cast<uint32_t>(D * ESZ);
   const uint32_t col = static_cast<uint32_t>(dl * ESZ);
   const Buf xb(x + row_lo * D, (row_hi - row_lo) * D * ESZ);
-  // dy rows [row_lo, row_hi): rows dys apart, the last one D elements long
-  const uint32_t drb = static_cast<uint32_t>(dys * ESZ);
-  const Buf dyb(dy + row_lo * dys, ((row_hi - row_lo - 1) * dys + D) * ESZ);
+  // dy rows [row_lo, row_hi): rows dys apart, the last one D elements long;
+  // dys < 0: one element for every token and channel (not in the prefill
+  // pass, whose entry takes rows only: the branch makes LLVM's AGPR-copy
+  // rewrite crash on its one-wave forms)
+  const bool dy_one = !PRE && dys < 0;
+  const uint32_t drb = static_cast<uint32_t>((dy_one ? 0 : dys) * ESZ);
+  const Buf dyb(dy_one ? dy : dy + row_lo * dys, dy_one ? ESZ : ((row_hi - row_lo - 1) * dys + D) * ESZ);
+  // dy_one: the element's fp32 bits, OR-ed into every converted dy value while
+  // the row loads read nothing (kOffNone gives zeros): the conversion stays one
+  // instruction (v_lshl_or / v_and_or) and the loop has no branch on the form
+  uint32_t dy_or = 0;
+  if (dy_one) {
+    E e;
+    dyb.load<ESZ>(0, &e);
+    dy_or = ch_ok ? __float_as_uint(C::to_f(e)) : 0u;
+  }
+  const bool dy_rows = ch_ok && !dy_one;
   const Buf ab(a_c + first * KP, (a_hi - first) * KP * ESZ);
   const Buf bb(b_c, static_cast<int64_t>(KP) * S * D * ESZ);
   // PRE: the cache (n_seqs = N / T sequences)
@@ -914,7 +929,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     if constexpr (NEED_X)
 #pragma unroll
       for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
-    const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, ch_ok);
+    const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, dy_rows);
 #pragma unroll
     for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
   };
@@ -991,7 +1006,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        g[r][c] = C::to_f(dr[r][c]);
+        g[r][c] = __uint_as_float(__float_as_uint(C::to_f(dr[r][c])) | dy_or);
         if constexpr (kPin) asm volatile("" : "+v"(g[r][c]));
       }
     const bool more = (sb + 1 < nsb) && (t0 + EOWN < N);

@@ -263,7 +263,7 @@ hist_grad_kernel(const typename CT<BF>::elem* __restrict__ x,
 #pragma unroll
   for (int pos = 0; pos < NP; ++pos) {
     const int64_t t = t0 + pos;
-    float g = C::to_f(dy[t * dys + d]);
+    float g = C::to_f(dy[dys < 0 ? 0 : t * dys + d]);
     if (act) {
       float p = 0.f;
 #pragma unroll

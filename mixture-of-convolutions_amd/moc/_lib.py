@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2

@@ -105,14 +105,21 @@ def _seq_args(x: torch.Tensor, cu_seqlens: torch.Tensor | None):
             cu_seqlens.numel() - 1, N, 0, D)
 
 
-def dy_operand(dy: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+def dy_operand(dy: torch.Tensor, dtype: torch.dtype, one: bool = True
+               ) -> tuple[torch.Tensor, int]:
     """(dy tensor, row stride in elements) for moc_backward.  A gradient that is
-    one row broadcast over every token (stride 0 over all token dimensions, as
-    autograd hands over the gradient of ``y.sum()``) is passed as that single
-    row with row stride 0, instead of the [n_tokens, D] copy that
-    ``dy.contiguous()`` would make (the reference's moc/api.py:171); anything
-    else is made contiguous, rows D apart."""
+    one element broadcast over every token and channel (all strides 0, as
+    autograd hands over the gradient of ``y.sum()``) is passed as that element
+    with row stride -1; one row broadcast over every token (stride 0 over the
+    token dimensions) as that row with row stride 0.  Either replaces the
+    [n_tokens, D] copy that ``dy.contiguous()`` would make (the reference's
+    moc/api.py:171) and the small copy of the row; anything else is made
+    contiguous, rows D apart.  ``one=False`` (the prefill entry, which takes
+    rows only) passes a broadcast element as one row."""
     D = dy.shape[-1]
+    if one and dy.numel() > 1 and all(st == 0 for st in dy.stride()):
+        one = dy.as_strided((1,), (1,), dy.storage_offset())
+        return (one if one.dtype == dtype else one.to(dtype)), -1
     if dy.ndim >= 2 and dy.numel() > D and all(st == 0 for st in dy.stride()[:-1]):
         row = dy[(0,) * (dy.ndim - 1)]
         return row.to(dtype).contiguous(), 0
@@ -297,7 +304,7 @@ def launch_backward_prefill(
     y in one moc_backward_prefill call."""
     L = _lib.lib()
     x = x.contiguous()
-    dy, dy_stride = dy_operand(moc_dy, x.dtype)
+    dy, dy_stride = dy_operand(moc_dy, x.dtype, one=False)
     a = _operand(alpha)
     b = _operand(basis)
     K, S, _ = b.shape

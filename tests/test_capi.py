@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.EXPORTED_SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.moc_abi_version() == _lib.ABI_VERSION == 3
+    assert L.moc_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_header_constants_match_binding():
@@ -94,10 +94,16 @@ def test_backward_and_update_reject_bad_arguments():
     rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, 16, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
                         1, 1, 1, 0, 0, FAKE, 8, None)
     assert rc == -3
-    # dy rows are dim (contiguous) or 0 (one broadcast row) elements apart
-    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, 7, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
-                        1, 1, 1, 0, 0, FAKE, 1 << 30, None)
-    assert rc == -1 and b"dy_row_stride" in L.moc_last_error()
+    # dy rows are dim (contiguous) or 0 (one broadcast row) elements apart, or
+    # -1 (one element for every token and channel)
+    for bad in (7, -2):
+        rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, bad, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4,
+                            4, 1, 1, 1, 0, 0, FAKE, 1 << 30, None)
+        assert rc == -1 and b"dy_row_stride" in L.moc_last_error()
+    # -1 passes the argument checks (the call then stops at the workspace size)
+    rc = L.moc_backward(FAKE, FAKE, FAKE, FAKE, -1, None, FAKE, FAKE, None, 0, 0, 8, 8, 16, 4, 4,
+                        1, 1, 1, 0, 0, FAKE, 8, None)
+    assert rc == -3
     rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 70000, 16, 4, 4, 1, 1, 1, 0, 0, None)
     assert rc == -1
     rc = L.moc_update(FAKE, FAKE, FAKE, FAKE, 64, 4, 1, FAKE, 2, 16, 4, 4, 1, 9, 1, 0, 0, None)

@@ -452,6 +452,38 @@ def test_broadcast_dy_matches_materialised(dtype, varlen):
         assert_close(n, u, r, dtype)
 
 
+@pytest.mark.parametrize("form", ["element", "row"])
+@pytest.mark.parametrize("shape", ["fused", "two_pass", "generic", "varlen"])
+def test_broadcast_dy_forms_match_materialised(form, shape):
+    """dy passed as one element for every token and channel (row stride -1, the
+    expanded gradient of y.sum()) or as one row for every token (row stride 0)
+    gives the results of the same dy as a contiguous tensor, bit for bit: on the
+    fused matrix-core pass (4 taps, 16 routes, SiLU), the two-pass form (8 taps,
+    32 routes, no activation), the generic kernels and a varlen call."""
+    from moc import _lib, ops
+    S, Kr, act, Dd = (8, 32, 0, 256) if shape == "two_pass" else (4, 16, 1, 192)
+    g = gen(77)
+    N = 300
+    x = randn(g, N, Dd, scale=0.5).to(DEV, torch.bfloat16)
+    a = torch.softmax(randn(g, N, Kr), -1).to(DEV, torch.bfloat16)
+    b = randn(g, Kr, S, Dd, scale=0.1).to(DEV, torch.bfloat16)
+    lead = (N,) if shape == "varlen" else (2, N // 2)   # packed [N, D] or fixed [B, T, D]
+    x = x.reshape(*lead, Dd)
+    if form == "element":
+        dy = (randn(g, 1, scale=0.5) + 1.0).to(DEV, torch.bfloat16).reshape(()).expand(*lead, Dd)
+    else:
+        dy = randn(g, Dd, scale=0.5).to(DEV, torch.bfloat16).expand(*lead, Dd)
+    assert dy.stride()[0] == 0
+    assert ops.dy_operand(dy, torch.bfloat16)[1] == (-1 if form == "element" else 0)
+    kw = dict(cu_seqlens=_cu([120, 7, 173]).to(DEV)) if shape == "varlen" else {}
+    path = _lib.PATH_GENERIC if shape == "generic" else _lib.PATH_AUTO
+    with _lib.kernel_path(path):
+        got = ops.launch_backward(x, a, b, dy, activation_flag=act, need_x=True, **kw)
+        ref = ops.launch_backward(x, a, b, dy.contiguous(), activation_flag=act, need_x=True, **kw)
+    for n, u, v in zip(("dx", "dalpha", "dbasis"), got, ref):
+        assert torch.equal(u, v), n
+
+
 def test_moc_triton_name_is_hip_path():
     assert moc.moc_triton is moc.moc_hip
 
