@@ -292,6 +292,7 @@ def counter_run(dev, which, reps=3):
       fwd / bwd  one C-ABI entry at the headline config (entry_calls);
       step       the headline layer step (bench_layer's step, inputs rotated);
       decode     the one-launch decode step of configs[3] (batch 256);
+      c3         the configs[2] varlen layer step (config3_step);
       c5         the configs[4] QKV triple step through MoCGroup;
       prefill    a headline-shape chunk continuing from a cache: the module
                  forward (router + prefill launch), then the prefill backward
@@ -320,6 +321,8 @@ def counter_run(dev, which, reps=3):
         fn = decode_step_call(dev)
     elif which == "prefill":
         fn = prefill_calls(dev, 1)
+    elif which == "c3":
+        fn = config3_step(dev)[0]
     else:
         fn = config5_step(dev)[0](True)
     for _ in range(2):
@@ -487,10 +490,11 @@ def cpu_baseline(seconds):
                       f"K={CFG['K']} S={CFG['S']} fp32, {reps} reps in {el:.1f}s"}
 
 
-def bench_config3(dev, steps, warmup):
-    """packed varlen layer fwd+bwd, 32768 tokens in sequences of
-    lengths uniform in [16, 4096] (seeded, cu_seqlens int32), D=4096,
-    z_dim=2048, K=16, S=4, bf16, exp routing, no SiLU, dy ~ N(0, 1)."""
+def config3_step(dev):
+    """(step, total tokens, number of sequences): the configs[2] layer step,
+    packed varlen fwd+bwd, 32768 tokens in sequences of lengths uniform in
+    [16, 4096] (seeded, cu_seqlens int32), D=4096, z_dim=2048, K=16, S=4, bf16,
+    exp routing, no SiLU, dy ~ N(0, 1)."""
     import moc
     g = torch.Generator().manual_seed(0)
     total, lengths = 32768, []
@@ -514,9 +518,16 @@ def bench_config3(dev, steps, warmup):
         y, _ = m(x, z, cu_seqlens=cu, max_seqlen=max(lengths))
         y.backward(dy)
 
+    return step, total, len(lengths)
+
+
+def bench_config3(dev, steps, warmup):
+    """the varlen layer step of config3_step."""
+    step, total, n_seqs = config3_step(dev)
+    D, Z, K, S = 4096, 2048, 16, 4
     ms = time_region(step, steps, warmup)
     return {"metric": "configs[2] varlen layer fwd+bwd Mtok/s", "value": round(total / (ms * 1e-3) / 1e6, 3),
-            "unit": "Mtok/s", "ms_per_step": round(ms, 4), "n_seqs": len(lengths),
+            "unit": "Mtok/s", "ms_per_step": round(ms, 4), "n_seqs": n_seqs,
             "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[2]", "tokens": total, "D": D,
                        "z_dim": Z, "K": K, "S": S, "routing": "exp", "activation": None}}
 
@@ -587,7 +598,7 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE,
                     help="input sets the timed loops cycle through (1: one set reused, "
                          "which the last-level cache partly holds across steps)")
-    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c5", "prefill", "copy"),
+    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c3", "c5", "prefill", "copy"),
                     default=None,
                     help="only run --reps calls of one workload (see counter_run) for a "
                          "rocprofv3 --pmc or --kernel-trace pass; prints no JSON")
