@@ -675,7 +675,10 @@ struct TrTile {
 };
 
 // MFMA jobs issued ahead of the FMAs that consume them.
-constexpr int kLead = 2;
+#ifndef MOC_BWD_LEAD
+#define MOC_BWD_LEAD 2
+#endif
+constexpr int kLead = MOC_BWD_LEAD;
 
 // Wave-local ordering of LDS traffic: LDS operations of one wave complete in
 // issue order; this keeps the compiler from moving them across the point.
