@@ -779,7 +779,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   // the workgroup's waves covers every tap (one partial per channel group)
   static_assert(MODE != kBwdTaps || WPG % 2 == 0, "tap halves pair the waves");
   constexpr int WCH = MODE == kBwdTaps ? WPG / 2 : WPG;  // waves across channels
-  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  // wave index as a scalar (uniform over the wave): the tap half and channel
+  // offsets derived from it, and the x / dy row offsets of a window, then stay
+  // in scalar registers (as vector values, hoisted out of the loop, they were
+  // spilled, and each reload waited for the row loads just issued).  Not in the
+  // prefill pass, whose one-wave forms then crash LLVM's AGPR-copy rewrite.
+  const int wave = PRE ? static_cast<int>(threadIdx.x) >> 6
+                       : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int th = MODE == kBwdTaps ? wave / WCH : 0;
   const int s0 = th * ST;
   // x window rows: every tap (P, or the fused m products), ST taps from s0, none
@@ -929,12 +935,26 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     // window of the taps from s0 starts s0 rows into the full one.  dy rows are
     // t0 + R q + r >= row_lo (never before the buffer, also with dys = 0)
     const uint32_t base = row_off(t0 + R * q - (S - 1), row_lo, rb, col, ch_ok);
-    if constexpr (NEED_X)
+    if constexpr (!PRE) {
+      // both bases first: a value reloaded between the two groups of loads
+      // would wait for the first group (the memory counter retires in issue
+      // order).  The prefill pass keeps the plain order: its one-wave forms
+      // crash LLVM's AGPR-copy rewrite with this one.
+      const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, dy_rows);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (NEED_X)
 #pragma unroll
-      for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
-    const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, dy_rows);
+        for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
 #pragma unroll
-    for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
+      for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
+    } else {
+      if constexpr (NEED_X)
+#pragma unroll
+        for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
+      const uint32_t dbase = row_off(t0 + R * q, row_lo, drb, col, dy_rows);
+#pragma unroll
+      for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
+    }
   };
   auto fetch_a = [&](int64_t t0) {
     // taps pass: the per-lane terms are formed here each time (an opaque copy
@@ -956,9 +976,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     fetch_a(t0);
   };
   auto stage_alpha = [&](int buf) {
+    // taps pass: the LDS addresses formed here each time, as in fetch_a (a
+    // hoisted copy was spilled, and its reload waited for the row loads)
+    int tid_s = tid;
+    if constexpr (MODE == kBwdTaps) asm volatile("" : "+v"(tid_s));
 #pragma unroll
     for (int i = 0; i < APER; ++i) {
-      const int chunk = tid + i * 64 * WPG;
+      const int chunk = tid_s + i * 64 * WPG;
       const int row = chunk / (KP / AVEC);
       if (chunk < ACHUNKS)
         Vec<E, AVEC>::store(&a_lds[buf][row][acol(row, (chunk % (KP / AVEC)) * AVEC)], arw[i]);
@@ -995,9 +1019,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     // measured 1 us slower this way, and the prefill pass's one-wave forms
     // crash LLVM's AGPR-copy rewrite with it
     constexpr bool kPin = MODE != kBwdTaps && !PRE && !ACT;
-    float xw[WX][NC];
+    // the taps pass converts each x value where an m product uses it instead of
+    // keeping an fp32 copy of the window (22 registers for about 40 more VALU:
+    // the pass waits far more than it issues, and its spills waited on memory)
+    constexpr bool kXOnUse = MODE == kBwdTaps;
+    float xw[kXOnUse ? 1 : WX][NC];
     float g[R][NC];
-    if constexpr (NEED_X)
+    if constexpr (NEED_X && !kXOnUse)
 #pragma unroll
       for (int w = 0; w < WX; ++w)
 #pragma unroll
@@ -1021,8 +1049,8 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       __builtin_amdgcn_sched_barrier(0);
       fetch(t0 + EOWN);
     } else if (more) {
-      if constexpr (MODE == kBwdTaps) fetch_a(t0 + EOWN);
-      else fetch(t0 + EOWN);
+      // (the taps pass loads the next routing weights inside its products)
+      if constexpr (MODE != kBwdTaps) fetch(t0 + EOWN);
     }
 
     // alpha operand of token-row block b shifted by e rows (row i = j)
@@ -1063,7 +1091,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
       }
 
-      if (ACT) {
+      if constexpr (ACT) {
         float p[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1249,7 +1277,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                   for (int v = 0; v < 4; ++v) {
                     const int r = 4 * b + v;
                     const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
-                    float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                    float xv;
+                    if constexpr (kXOnUse) xv = C::to_f(xr[r + s][c]);
+                    else xv = xw[r + s][c];
+                    float mval = on ? g[r][c] * xv : 0.f;
                     if (HX && use_h && !on) mval = g[r][c] * hx[HX ? r + s : 0][c];
                     hb[v] = __float_as_uint(mval) & 0xffff0000u;
                     lo[v] = mval - __uint_as_float(hb[v]);
@@ -1268,6 +1299,16 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
             }
           };
           stage_m(0);
+          // taps pass: the next super-block's routing weights are loaded here,
+          // after the first tap's products (where the fewest registers are
+          // live), and go to LDS after the last tap, the loads covered by three
+          // taps' work; loaded at the top of the super-block they were spilled
+          // at once, the spill waiting for the loads to land.  The other half of
+          // the double buffer has been free since the previous super-block's
+          // closing barrier.
+          if constexpr (MODE == kBwdTaps) {
+            if (more) fetch_a(t0 + EOWN);
+          }
 #pragma unroll
           for (int s = 0; s < ST; ++s) {
             wave_lds_sync();
@@ -1301,6 +1342,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
                 for (int kx = 0; kx < KX; ++kx)
                   dacc[rb][kx] = mma32(ra[rb][h][0], ra[rb][h][1], bs[kx][0], bs[kx][1], dacc[rb][kx]);
+          }
+          if constexpr (MODE == kBwdTaps) {
+            if (more) stage_alpha(buf ^ 1);
           }
           wave_lds_sync();
         } else {
@@ -1367,7 +1411,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
           for (int v = 0; v < 4; ++v) da_lds[buf % DAB][wave][rb][kx][4 * q + v][j] = dacc[rb][kx][v];
     }
-    if (more) stage_alpha(buf ^ 1);
+    if constexpr (MODE != kBwdTaps) {
+      if (more) stage_alpha(buf ^ 1);
+    }
     __syncthreads();
     // sum the WPG waves' dalpha tiles in wave order; own rows only
     if constexpr (DO_M && BF) {
@@ -1378,9 +1424,11 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       static_assert(NB * KX * 256 % (64 * WPG) == 0, "dalpha tile elements per thread");
       float* __restrict__ pd = part_da + (static_cast<int64_t>(bx) * N + t0) * KP + 16 * kc0;
       const int n_own = static_cast<int>(own_end - t0);
+      int tid_d = tid;  // taps pass: offsets formed here each time (see stage_alpha)
+      if constexpr (MODE == kBwdTaps) asm volatile("" : "+v"(tid_d));
 #pragma unroll
       for (int i = 0; i < NSUM; ++i) {
-        const int idx = tid + i * 64 * WPG;
+        const int idx = tid_d + i * 64 * WPG;
         const int rb = idx / (KX * 256);
         const int kx = (idx / 256) % KX;
         const int row = (idx >> 4) & 15, col = idx & 15;
