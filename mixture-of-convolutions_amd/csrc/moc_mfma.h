@@ -945,8 +945,17 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       if constexpr (NEED_X)
 #pragma unroll
         for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
+      if (MODE == kBwdTaps && dy_one) {
+        // one dy element: the taps pass issues no row loads for it (they would
+        // read nothing but take places in the memory queue behind the x rows)
 #pragma unroll
-      for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) dr[r][c] = E(0);
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
+      }
     } else {
       if constexpr (NEED_X)
 #pragma unroll
@@ -1426,6 +1435,18 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       const int n_own = static_cast<int>(own_end - t0);
       int tid_d = tid;  // taps pass: offsets formed here each time (see stage_alpha)
       if constexpr (MODE == kBwdTaps) asm volatile("" : "+v"(tid_d));
+      // every tile value read first (all reads in flight together), then the
+      // sums in wave order
+      float tv[NSUM][WPG];
+#pragma unroll
+      for (int i = 0; i < NSUM; ++i) {
+        const int idx = tid_d + i * 64 * WPG;
+        const int rb = idx / (KX * 256);
+        const int kx = (idx / 256) % KX;
+        const int row = (idx >> 4) & 15, col = idx & 15;
+#pragma unroll
+        for (int w = 0; w < WPG; ++w) tv[i][w] = da_lds[buf % DAB][w][rb][kx][row][col];
+      }
 #pragma unroll
       for (int i = 0; i < NSUM; ++i) {
         const int idx = tid_d + i * 64 * WPG;
@@ -1434,7 +1455,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         const int row = (idx >> 4) & 15, col = idx & 15;
         float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < WPG; ++w) sum += da_lds[buf % DAB][w][rb][kx][row][col];
+        for (int w = 0; w < WPG; ++w) sum += tv[i][w];
         if (16 * rb + row < n_own) pd[(16 * rb + row) * KP + 16 * kx + col] = sum;
       }
     } else if constexpr (DO_M) {
