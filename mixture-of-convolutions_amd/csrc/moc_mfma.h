@@ -551,8 +551,14 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
   }
 }
 
+// Waves per SIMD the 8-tap, 32-route forward is built for (1: the compiler's
+// choice, 169 VGPRs, two waves).
+#ifndef MOC_FWD8_WAVES
+#define MOC_FWD8_WAVES 1
+#endif
 template <int S, int KC, int NB, int NC, bool ACT, bool BF>
 __global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((S == 8 && KC == 2) ? MOC_FWD8_WAVES : 1)))
 fwd_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ yv, SeqLayout seq,
            int64_t D, int n_sb) {
@@ -573,6 +579,7 @@ fwd_pre_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restr
 // Several layers in one launch (1-D grid, the layers' grids one after another).
 template <int S, int KC, int NB, int NC, bool ACT, bool BF>
 __global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu((S == 8 && KC == 2) ? MOC_FWD8_WAVES : 1)))
 fwd_layers_kernel(FwdLayers ly, SeqLayout seq) {
   using E = typename CT<BF>::elem;
   const int blk = static_cast<int>(blockIdx.x);
@@ -945,9 +952,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       if constexpr (NEED_X)
 #pragma unroll
         for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
-      if (MODE == kBwdTaps && dy_one) {
-        // one dy element: the taps pass issues no row loads for it (they would
-        // read nothing but take places in the memory queue behind the x rows)
+      if (MODE != kBwdFused && dy_one) {
+        // one dy element: the partial passes issue no row loads for it (they
+        // would read nothing but take places in the memory queue behind the x
+        // rows); the fused pass keeps them, a branch there cost it 3 us
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
