@@ -272,6 +272,24 @@ __device__ __forceinline__ void hist_window(const Buf& hb, int64_t u0, int64_t T
   }
 }
 
+// One value of hist_window: the cache entry standing for token u of channel
+// dl + c (the tap of the first sequence starting after u), or 0.
+template <int S, typename E>
+__device__ __forceinline__ float hist_at(const Buf& hb, int64_t u, int64_t T, int64_t N, int64_t D,
+                                         int64_t dl, bool ch_ok, int c) {
+  int64_t b = 0;
+  if (u >= 0) b = static_cast<int64_t>(static_cast<uint32_t>(u) / static_cast<uint32_t>(T)) + 1;
+  const int64_t st = b * T;
+  const int64_t m = st - u;  // >= 1
+  const bool on = ch_ok && m <= S - 1 && st < N;
+  constexpr uint32_t ESZ = sizeof(E);
+  const uint32_t off = static_cast<uint32_t>(((b * D + dl) * S + (S - m) + c * S) * ESZ);
+  E v;
+  hb.load<ESZ>(on ? off : kOffNone, &v);
+  if constexpr (sizeof(E) == 2) return bf16_to_f32(v);
+  else return v;
+}
+
 // Final-state rows of a super-block [t0, t0 + TB): this lane's run trun + r
 // (r < R) with x values xw[r + S - 1]; writes fin for the rows within S of
 // their sequence's end, and the cache part of the state for T < S.
@@ -779,7 +797,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(MODE == kBwdFused || (BF && !ACT && S % 2 == 0),
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
-  static_assert(!PRE || MODE == kBwdFused, "prefill runs the fused pass");
+  static_assert(!PRE || MODE != kBwdDx, "the prefill dx pass is the plain one (it reads no cache)");
   constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
   // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, S/2) and
   // [S/2, S): x and dy rows are read once per workgroup and the dalpha sum over
@@ -791,8 +809,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   // in scalar registers (as vector values, hoisted out of the loop, they were
   // spilled, and each reload waited for the row loads just issued).  Not in the
   // prefill pass, whose one-wave forms then crash LLVM's AGPR-copy rewrite.
-  const int wave = PRE ? static_cast<int>(threadIdx.x) >> 6
-                       : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  constexpr bool kPreFused = PRE && MODE == kBwdFused;
+  const int wave = kPreFused ? static_cast<int>(threadIdx.x) >> 6
+                             : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int th = MODE == kBwdTaps ? wave / WCH : 0;
   const int s0 = th * ST;
   // x window rows: every tap (P, or the fused m products), ST taps from s0, none
@@ -942,7 +961,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     // window of the taps from s0 starts s0 rows into the full one.  dy rows are
     // t0 + R q + r >= row_lo (never before the buffer, also with dys = 0)
     const uint32_t base = row_off(t0 + R * q - (S - 1), row_lo, rb, col, ch_ok);
-    if constexpr (!PRE) {
+    if constexpr (!kPreFused) {
       // both bases first: a value reloaded between the two groups of loads
       // would wait for the first group (the memory counter retires in issue
       // order).  The prefill pass keeps the plain order: its one-wave forms
@@ -1100,12 +1119,16 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         for (int r = 0; r < NOK; ++r) ok[r] = (1u << S) - 1u;
       }
       // PRE: masked taps read the cache (uniform: is there one?)
+      // (the taps pass loads them where it forms an m product: a window held in
+      // registers through its tap loop spills)
       constexpr bool HX = PRE && MASK;
-      float hx[HX ? W : 1][NC];
+      constexpr bool HXW = HX && MODE != kBwdTaps;
+      float hx[HXW ? W : 1][NC];
       bool use_h = false;
       if constexpr (HX) {
         use_h = pre.hist != nullptr;
-        if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
+        if constexpr (HXW)
+          if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
       }
 
       if constexpr (ACT) {
@@ -1141,7 +1164,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
           for (int v = 0; v < 4; ++v) {
             const int r = 4 * b + v;
             if (!MASK || ((ok[r] >> s) & 1u)) p[r][c] = fmaf(xw[r + s][c], wq[jb][v], p[r][c]);
-            else if (HX && use_h) p[r][c] = fmaf(hx[HX ? r + s : 0][c], wq[jb][v], p[r][c]);
+            else if (HXW && use_h) p[r][c] = fmaf(hx[HXW ? r + s : 0][c], wq[jb][v], p[r][c]);
           }
         }
         // g *= silu'(P) = sg (1 + P (1 - sg)), sg = sigmoid(P) as sigmoid_f forms
@@ -1288,7 +1311,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                 for (int bb = 0; bb < 2; ++bb) {
                   const int b = b2 + bb;
                   // m of rows 4b..4b+3 of channel NC j + c, split into bf16 hi / lo
-                  uint32_t hb[4];
+                  uint32_t hbits[4];
                   float lo[4];
 #pragma unroll
                   for (int v = 0; v < 4; ++v) {
@@ -1298,11 +1321,17 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                     if constexpr (kXOnUse) xv = C::to_f(xr[r + s][c]);
                     else xv = xw[r + s][c];
                     float mval = on ? g[r][c] * xv : 0.f;
-                    if (HX && use_h && !on) mval = g[r][c] * hx[HX ? r + s : 0][c];
-                    hb[v] = __float_as_uint(mval) & 0xffff0000u;
-                    lo[v] = mval - __uint_as_float(hb[v]);
+                    if constexpr (HXW) {
+                      if (use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
+                    } else if constexpr (HX) {
+                      if (use_h && !on)
+                        mval = g[r][c] * hist_at<S, E>(hb, trun - (S - 1) + s0 + r + s, T, N, D, dl,
+                                                       ch_ok, c);
+                    }
+                    hbits[v] = __float_as_uint(mval) & 0xffff0000u;
+                    lo[v] = mval - __uint_as_float(hbits[v]);
                   }
-                  mh[bb] = pack4_hi(hb[0], hb[1], hb[2], hb[3]);
+                  mh[bb] = pack4_hi(hbits[0], hbits[1], hbits[2], hbits[3]);
                   ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
                   m_tr[wave][0][TT::wslot(j, q, b, c)] = mh[bb];
                   m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
@@ -1378,7 +1407,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
               for (int c = 0; c < NC; ++c) {
                 E parts[NP];
                 float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
-                if (HX && use_h && !on) mval = g[r][c] * hx[HX ? r + s : 0][c];
+                if (HXW && use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
                 MS::split(mval, parts);
 #pragma unroll
                 for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
@@ -1564,6 +1593,22 @@ bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, kBwdFused, true>(
       xv, dyv, dys, a_c, b_c, dxv, part_da, part_db, seq, D, bx, by, zh, gy, gy1, n_old, n_total,
       pre);
+}
+
+// Prefill from a cache in the two-pass form (bf16, 8 taps, 32 routes, no
+// activation): the m products of the taps pass, whose masked taps read the cache;
+// the dx pass is the plain one (dx reads no cache).
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, kBwdTaps, BF>)))
+bwd_pre_taps_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
+                    const typename CT<BF>::elem* __restrict__ a_c,
+                    const typename CT<BF>::elem* __restrict__ b_c, float* __restrict__ part_da,
+                    float* __restrict__ part_db, SeqLayout seq, int64_t D, int gx, int gy,
+                    int gy1, int n_old, int n_total, Pre pre) {
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, false, kBwdTaps, true>(
+      xv, dyv, dys, a_c, b_c, nullptr, part_da, part_db, seq, D, static_cast<int>(blockIdx.x),
+      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre);
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another:

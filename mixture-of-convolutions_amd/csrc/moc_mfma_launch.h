@@ -168,8 +168,8 @@ constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && KC == 2 && S == 8;
 }
 inline bool bwd_two_pass(const Problem& p) {
-  return !p.pre && bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,
-                                p.x_dt == DT_BF16);
+  return bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,
+                      p.x_dt == DT_BF16);
 }
 
 // The taps pass holds one workgroup per CU (its LDS), so it runs as one round
@@ -422,15 +422,33 @@ void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_
   else {
   using E = typename CT<BF>::elem;
   const Grid2 g = bwd_partials_grid(p);
-  // 64 routes: split in route chunks on a 1-D grid, as bwd_one does
-  constexpr bool kSplit = BF && KC >= 4;
-  const dim3 grid = kSplit ? dim3(static_cast<unsigned>(8 * KC * cdiv(int64_t(g.gx) * g.gy, 8)))
-                           : dim3(g.gx, g.gy);
-  hipLaunchKernelGGL((bwd_pre_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit>), grid,
-                     dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, static_cast<const E*>(a_c),
-                     static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D,
-                     static_cast<int>(g.gx), static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total,
-                     pre);
+  if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
+    // two passes as bwd_one runs them: the plain dx pass (dx reads no cache),
+    // then the taps pass with the cache (g is the taps grid here)
+    const auto* a = static_cast<const E*>(a_c);
+    const auto* b = static_cast<const E*>(b_c);
+    if (dx != nullptr) {
+      const Grid2 gd = bwd_grid(p.n_tokens, p.D, S);
+      hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
+                         dim3(gd.gx, gd.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx,
+                         part_da, part_db, p.seq, p.D, static_cast<int>(gd.gx),
+                         static_cast<int>(gd.gy), gd.gy1, gd.n_old, gd.n_total);
+    }
+    hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF>),
+                       dim3(g.gx, g.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b,
+                       part_da, part_db, p.seq, p.D, static_cast<int>(g.gx),
+                       static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total, pre);
+  } else {
+    // 64 routes: split in route chunks on a 1-D grid, as bwd_one does
+    constexpr bool kSplit = BF && KC >= 4;
+    const dim3 grid = kSplit ? dim3(static_cast<unsigned>(8 * KC * cdiv(int64_t(g.gx) * g.gy, 8)))
+                             : dim3(g.gx, g.gy);
+    hipLaunchKernelGGL((bwd_pre_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit>), grid,
+                       dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, static_cast<const E*>(a_c),
+                       static_cast<const E*>(b_c), dx, part_da, part_db, p.seq, p.D,
+                       static_cast<int>(g.gx), static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total,
+                       pre);
+  }
   }
 }
 

@@ -52,6 +52,7 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (3, 16, "silu", BF, 2),
     (3, 5, "silu", F32, 41),
     (8, 32, None, BF, 7),
+    (8, 32, None, BF, 70),
     (8, 32, "silu", BF, 40),
     (8, 16, "silu", F32, 9),
     (8, 16, None, BF, 64),
