@@ -794,14 +794,16 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
   // work of this MODE: dx rows, m products of ST taps from tap s0
   constexpr bool DO_DX = MODE != kBwdTaps, DO_M = MODE != kBwdDx;
-  static_assert(MODE == kBwdFused || (BF && !ACT && S % 2 == 0),
+  static_assert(MODE == kBwdFused || (BF && !ACT),
                 "the partial passes are built for bf16 without activation");
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
   static_assert(!PRE || MODE != kBwdDx, "the prefill dx pass is the plain one (it reads no cache)");
-  constexpr int ST = MODE == kBwdTaps ? S / 2 : S;
-  // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, S/2) and
-  // [S/2, S): x and dy rows are read once per workgroup and the dalpha sum over
-  // the workgroup's waves covers every tap (one partial per channel group)
+  constexpr int ST = MODE == kBwdTaps ? (S + 1) / 2 : S;
+  // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, ST) and
+  // [ST, S): x and dy rows are read once per workgroup and the dalpha sum over
+  // the workgroup's waves covers every tap (one partial per channel group).  With
+  // S odd the second half's last tap (s0 + ST - 1 = S) does not exist: its m
+  // values are zero, its dalpha operands zero rows, its dbasis never stored.
   static_assert(MODE != kBwdTaps || WPG % 2 == 0, "tap halves pair the waves");
   constexpr int WCH = MODE == kBwdTaps ? WPG / 2 : WPG;  // waves across channels
   // wave index as a scalar (uniform over the wave): the tap half and channel
@@ -814,6 +816,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                              : __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   const int th = MODE == kBwdTaps ? wave / WCH : 0;
   const int s0 = th * ST;
+  // whether tap s of this wave's half exists (uniform; false only for the last
+  // tap of the second half with S odd)
+  const bool last_tap_in = MODE != kBwdTaps || S % 2 == 0 || th == 0;
+  auto tap_in = [&](int s) { return s + 1 < ST || last_tap_in; };
   // x window rows: every tap (P, or the fused m products), ST taps from s0, none
   constexpr bool NEED_X = DO_M || ACT;
   constexpr int WX = MODE == kBwdTaps ? R + ST - 1 : (NEED_X ? W : 1);
@@ -929,7 +935,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
         bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s0 + s, 0, rb,
-                                 static_cast<uint32_t>(ch * ESZ), wave_on && ch < D),
+                                 static_cast<uint32_t>(ch * ESZ), wave_on && ch < D && tap_in(s)),
                          e4);
         if constexpr (kBdaLds)  // read back per tap in the dalpha loop (wave-private rows)
           Vec<E, 4>::store(&b_lds[wave][s * 16 * KX + 16 * kx + j][16 * cg + 4 * q], e4);
@@ -1316,7 +1322,8 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
                   for (int v = 0; v < 4; ++v) {
                     const int r = 4 * b + v;
-                    const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
+                    // (the mask has no bit for a tap past S)
+                    const bool on = !MASK ? tap_in(s) : static_cast<bool>((ok[r] >> (s0 + s)) & 1u);
                     float xv;
                     if constexpr (kXOnUse) xv = C::to_f(xr[r + s][c]);
                     else xv = xw[r + s][c];
@@ -1324,7 +1331,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                     if constexpr (HXW) {
                       if (use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
                     } else if constexpr (HX) {
-                      if (use_h && !on)
+                      if (use_h && !on && tap_in(s))
                         mval = g[r][c] * hist_at<S, E>(hb, trun - (S - 1) + s0 + r + s, T, N, D, dl,
                                                        ch_ok, c);
                     }
@@ -1402,12 +1409,12 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
               const int r = 4 * b + v;
-              const bool on = !MASK || ((ok[r] >> (s0 + s)) & 1u);
+              const bool on = !MASK ? tap_in(s) : static_cast<bool>((ok[r] >> (s0 + s)) & 1u);
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 E parts[NP];
                 float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
-                if (HXW && use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
+                if (HXW && use_h && !on && tap_in(s)) mval = g[r][c] * hx[HXW ? r + s : 0][c];
                 MS::split(mval, parts);
 #pragma unroll
                 for (int h = 0; h < NP; ++h) mv[h][v][c] = parts[h];
@@ -1523,7 +1530,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
             const int64_t ch = d0 + NC * (4 * q + v) + c;
-            if (ch < D)
+            if (ch < D && tap_in(s))
               part_db[((base + 16 * (kc0 + kx) + j) * S + s0 + s) * D + ch] = dbacc[c][s][kx][v];
           }
   }
