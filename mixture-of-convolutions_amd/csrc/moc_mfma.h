@@ -1602,7 +1602,7 @@ bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_
       pre);
 }
 
-// Prefill from a cache in the two-pass form (bf16, 8 taps, 32 routes, no
+// Prefill from a cache in the two-pass form (the shapes of bwd_two_pass: bf16, no
 // activation): the m products of the taps pass, whose masked taps read the cache;
 // the dx pass is the plain one (dx reads no cache).
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>

@@ -163,10 +163,11 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_
 
 // The backward in two passes (bwd_kernel modes kBwdDx, then kBwdTaps with the
 // taps split in halves) where the fused pass does not fit two waves per SIMD
-// and no activation needs P: bf16, 32 routes and 5 to 8 taps, 16 routes and 7
-// or 8 taps.
+// and no activation needs P: bf16, 32 routes and 4 to 8 taps, 16 routes and 7
+// or 8 taps (measured against the fused pass at every kernel size: below those
+// the fused pass is faster).
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
-  return bf && !act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 7));
+  return bf && !act && ((KC == 2 && S >= 4) || (KC == 1 && S >= 7));
 }
 inline bool bwd_two_pass(const Problem& p) {
   return bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,

@@ -28,6 +28,7 @@ CASES = [
     ([128, 192, 64], 32, 7, 0, [4, 0, 3], [True, True, False], torch.bfloat16),  # 7 taps, halves
     ([256, 128], 64, 4, 1, [3, 0], [True, True], torch.bfloat16),                 # 64 routes
     ([256, 128], 32, 6, 0, [4, 3], [True, False], torch.bfloat16),               # 6 taps, two passes
+    ([192, 64], 32, 4, 0, [0, 4], [True, True], torch.bfloat16),                  # 4 taps, two passes
     ([128, 64], 16, 8, 0, [0, 3], [True, True], torch.bfloat16),                  # 16 routes, two passes
 ]
 

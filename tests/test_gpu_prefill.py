@@ -56,6 +56,7 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (7, 32, None, BF, 9),
     (5, 32, None, BF, 12),
     (7, 16, None, BF, 33),
+    (4, 32, None, BF, 20),
     (8, 32, "silu", BF, 40),
     (8, 16, "silu", F32, 9),
     (8, 16, None, BF, 64),
