@@ -44,11 +44,11 @@ METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/st
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
-# FETCH_SIZE (68700 KiB) and WRITE_SIZE (98382 KiB) per dispatch of
+# FETCH_SIZE (68681 KiB) and WRITE_SIZE (98388 KiB) per dispatch of
 # `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
 # 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
 # 131072 KiB -> factor 1.0); profiles/traffic_fwd_bwd_config2.md
-TRAFFIC_BWD = 241_440_768
+TRAFFIC_BWD = 241_408_000
 # input sets the timed loops cycle through: 3 x (x, z) = 402 MB at CFG, more
 # than the 256 MB last-level cache, so each step reads its inputs from HBM
 ROTATE = 3
