@@ -222,6 +222,26 @@ def test_mfma_matches_generic(dtype, S, K, act):
         assert_close("varlen " + n, u.reshape(r.shape), r, dtype)
 
 
+@pytest.mark.parametrize("S,K", [(5, 32), (7, 32), (8, 16), (7, 16)])
+@pytest.mark.parametrize("B,T,D", [(1, 1, 64), (1, 2, 4), (2, 3, 132), (1, 17, 260), (3, 40, 68)])
+def test_two_pass_small_and_ragged(S, K, B, T, D):
+    """The two-pass backward (bf16, no activation) at token counts below one
+    super-block and channel counts that leave partial channel groups, against
+    the oracle."""
+    g = gen(S * 1000 + K * 10 + T)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, torch.bfloat16)
+    a = torch.softmax(randn(g, B, T, K), -1).to(DEV, torch.bfloat16)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, torch.bfloat16)
+    dy = randn(g, B, T, D).to(DEV, torch.bfloat16)
+    xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
+    y, _ = moc_triton(xx, aa, bb)
+    y.backward(dy)
+    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), None)
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), (y, xx.grad, aa.grad, bb.grad), ref):
+        assert_close(n, u, r, torch.bfloat16)
+
+
 @pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 20), (8, 32), (8, 5)])
 @pytest.mark.parametrize("route", [None, "softmax", "exp"])
 def test_decode_kernel_matches_oracle_and_generic(S, K, route):
