@@ -200,9 +200,8 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
 size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                     int64_t kernel_size, int x_dtype, int routing) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
-  // the activation is not an argument, and the kernel plan can depend on it
-  // (bf16 with 4-8 taps and 32 routes or 7-8 taps and 16: two passes without
-  // it, the fused pass with it)
+  // the activation is not an argument, and the kernel plan depends on it (bf16
+  // two-pass shapes: the taps pass's partials, and with SiLU the g buffer)
   size_t need = 0;
   for (int act = 0; act <= 1; ++act) {
     const moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size,

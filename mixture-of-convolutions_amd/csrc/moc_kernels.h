@@ -23,6 +23,7 @@ struct Problem {
                           // tokens; -1: one element for every token and channel)
   int path = PATH_AUTO;   // PATH_MFMA_PREP: MFMA kernels, operands always through prep
   bool pre = false;       // prefill from a cache: the backward is the fused pass for every shape
+  bool grouped = false;   // a layer of a grouped launch: with the activation, the fused pass
   hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set
   hipEvent_t prof_stop = nullptr;
 };

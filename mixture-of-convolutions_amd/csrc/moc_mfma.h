@@ -764,7 +764,9 @@ constexpr int kBwdMinWaves = (MODE == kBwdFused && ((S >= 8 && KC >= 2) || KC >=
 // bwd_tile is the work of workgroup (bx, by) (route chunk zh with SPLIT) of
 // one layer; the __global__ wrappers below map the grid onto it.  PRE (fused
 // pass only): prefill from a cache, whose values the masked taps read in P and
-// in the m products (the cache gradient is not formed here).
+// in the m products (the cache gradient is not formed here).  gbuf (the partial
+// passes with the activation): g = dy silu'(P) of every token and channel in
+// fp32 [N, D], written by the dx pass, read by the taps pass in place of dy.
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE,
           bool PRE = false>
 __device__ __forceinline__ void
@@ -773,7 +775,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
          const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
          float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
          int bx, int by, int zh, int gy, int gy1, int n_old, int n_total,
-         Pre pre = Pre{nullptr, nullptr}) {
+         Pre pre = Pre{nullptr, nullptr}, float* __restrict__ gbuf = nullptr) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -794,8 +796,12 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
   // work of this MODE: dx rows, m products of ST taps from tap s0
   constexpr bool DO_DX = MODE != kBwdTaps, DO_M = MODE != kBwdDx;
-  static_assert(MODE == kBwdFused || (BF && !ACT),
-                "the partial passes are built for bf16 without activation");
+  static_assert(MODE == kBwdFused || BF, "the partial passes are built for bf16");
+  static_assert(!(ACT && PRE && MODE != kBwdFused), "prefill with the activation runs the fused pass");
+  // with the activation: P (and g) formed in this pass; g read from gbuf (taps
+  // pass) or written there (dx pass)
+  constexpr bool PACT = ACT && MODE != kBwdTaps;
+  constexpr bool GIN = ACT && MODE == kBwdTaps, GOUT = ACT && MODE == kBwdDx;
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
   static_assert(!PRE || MODE != kBwdDx, "the prefill dx pass is the plain one (it reads no cache)");
   constexpr int ST = MODE == kBwdTaps ? (S + 1) / 2 : S;
@@ -821,7 +827,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   const bool last_tap_in = MODE != kBwdTaps || S % 2 == 0 || th == 0;
   auto tap_in = [&](int s) { return s + 1 < ST || last_tap_in; };
   // x window rows: every tap (P, or the fused m products), ST taps from s0, none
-  constexpr bool NEED_X = DO_M || ACT;
+  constexpr bool NEED_X = DO_M || PACT;
   constexpr int WX = MODE == kBwdTaps ? R + ST - 1 : (NEED_X ? W : 1);
 
   // m tiles for the dalpha product.  fp32: [token][channel] tiles read as rows.
@@ -908,7 +914,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 
   // W operands (P, dx): bop[c][s][kc] = basis[16kc + 4q + v, s, dl + c]
   Op bop[NC][S][KC];
-  if constexpr (DO_DX || ACT)
+  if constexpr (DO_DX || PACT)
 #pragma unroll
   for (int kc = 0; kc < KC; ++kc) {
 #pragma unroll
@@ -959,7 +965,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   constexpr int ACHUNKS = AROWS * KP / AVEC;
   constexpr int APER = (ACHUNKS + 64 * WPG - 1) / (64 * WPG);
   E xr[WX][NC];
-  E dr[R][NC];
+  E dr[GIN ? 1 : R][NC];
+  float gr[GIN ? R : 1][NC];  // GIN: g rows (fp32)
+  const uint32_t grb = static_cast<uint32_t>(D * 4), gcol = static_cast<uint32_t>(dl * 4);
+  const Buf gib(GIN ? gbuf + row_lo * D : nullptr, GIN ? (row_hi - row_lo) * D * 4 : 0);
   E arw[APER][AVEC];
   auto fetch_xdy = [&](int64_t t0) {
     // offset of window row w = base + w rb: rows before row_lo wrap to >= 2^31
@@ -977,14 +986,18 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       if constexpr (NEED_X)
 #pragma unroll
         for (int w = 0; w < WX; ++w) xb.load<NC * ESZ>(base + (w + s0) * rb, xr[w]);
-      if (MODE != kBwdFused && dy_one) {
+      if constexpr (GIN) {
+        const uint32_t gbase = row_off(t0 + R * q, row_lo, grb, gcol, ch_ok);
+#pragma unroll
+        for (int r = 0; r < R; ++r) gib.load<NC * 4>(gbase + r * grb, gr[r]);
+      } else if (MODE != kBwdFused && dy_one) {
         // one dy element: the partial passes issue no row loads for it (they
         // would read nothing but take places in the memory queue behind the x
         // rows); the fused pass keeps them, a branch there cost it 3 us
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int c = 0; c < NC; ++c) dr[r][c] = E(0);
+          for (int c = 0; c < NC; ++c) dr[GIN ? 0 : r][c] = E(0);
       } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) dyb.load<NC * ESZ>(dbase + r * drb, dr[r]);
@@ -1079,7 +1092,8 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        g[r][c] = __uint_as_float(__float_as_uint(C::to_f(dr[r][c])) | dy_or);
+        if constexpr (GIN) g[r][c] = gr[r][c];
+        else g[r][c] = __uint_as_float(__float_as_uint(C::to_f(dr[r][c])) | dy_or);
         if constexpr (kPin) asm volatile("" : "+v"(g[r][c]));
       }
     const bool more = (sb + 1 < nsb) && (t0 + EOWN < N);
@@ -1137,7 +1151,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
           if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
       }
 
-      if constexpr (ACT) {
+      if constexpr (PACT) {
         float p[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1193,6 +1207,14 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
             const float v = fmaf(-sg[r][c], sg[r][c], sg[r][c]);
             g[r][c] = g[r][c] * fmaf(p[r][c], v, sg[r][c]);
           }
+      }
+      // the dx pass with the activation: this super-block's own rows of g for
+      // the taps pass (the buffer ends at the last own row)
+      if constexpr (GOUT) {
+        const Buf gob(gbuf + row_lo * D, (own_end - row_lo) * D * 4);
+        const uint32_t gb0 = row_off(trun, row_lo, grb, gcol, ch_ok);
+#pragma unroll
+        for (int r = 0; r < R; ++r) gob.store<NC * 4>(gb0 + r * grb, g[r]);
       }
 
       // dx: taps in descending order, so that the first jobs (shift 0) need none
@@ -1567,13 +1589,14 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
-           int gx, int gy, int gy1, int n_old, int n_total) {
+           int gx, int gy, int gy1, int n_old, int n_total, float* __restrict__ gbuf = nullptr) {
   int bx, by, zh;
   if (!bwd_block<SPLIT ? KC : 1>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), bx,
                         by, zh))
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(xv, dyv, dys, a_c, b_c, dxv, part_da, part_db,
-                                                     seq, D, bx, by, zh, gy, gy1, n_old, n_total);
+                                                     seq, D, bx, by, zh, gy, gy1, n_old, n_total,
+                                                     Pre{nullptr, nullptr}, gbuf);
 }
 
 // Prefill from a cache (Pre): the fused pass on a 2-D grid (bf16 with 32

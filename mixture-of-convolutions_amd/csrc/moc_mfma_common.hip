@@ -293,7 +293,7 @@ size_t al(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 struct Plan {
   int KP;
   size_t esz;
-  size_t off_ac, off_bc, off_ar, off_pda, off_pdb, total;
+  size_t off_ac, off_bc, off_ar, off_pda, off_pdb, off_g, total;
   Grid2 bg;
 };
 
@@ -330,6 +330,10 @@ Plan plan(const Problem& p, bool backward) {
     off += al(static_cast<size_t>(pl.bg.gx) * p.n_tokens * pl.KP * 4);
     pl.off_pdb = off;
     off += al(static_cast<size_t>(pl.bg.gy) * pl.KP * p.S * p.D * 4);
+    if (bwd_two_pass_g(p)) {  // g = dy silu'(P) from the dx pass to the taps pass
+      pl.off_g = off;
+      off += al(static_cast<size_t>(p.n_tokens) * p.D * 4);
+    }
   }
   pl.total = off;
   return pl;
@@ -442,15 +446,16 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
   }
   float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
   float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
+  float* gb = bwd_two_pass_g(p) ? reinterpret_cast<float*>(ws + pl.off_g) : nullptr;
   prof_begin(p, st);
   switch (p.S) {
-    case 2: launch_bwd<2>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 3: launch_bwd<3>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 4: launch_bwd<4>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 5: launch_bwd<5>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 6: launch_bwd<6>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 7: launch_bwd<7>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
-    case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, st); break;
+    case 2: launch_bwd<2>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 3: launch_bwd<3>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 4: launch_bwd<4>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 5: launch_bwd<5>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 6: launch_bwd<6>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 7: launch_bwd<7>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
     default: break;
   }
   prof_end(p, st);
@@ -587,7 +592,11 @@ size_t forward_layers_workspace(const Problem* ps, int n) {
 // layers' own grids), so the workspace is the layers' workspaces side by side.
 size_t backward_layers_workspace(const Problem* ps, int n) {
   size_t total = 0;
-  for (int i = 0; i < n; ++i) total += plan(ps[i], true).total;
+  for (int i = 0; i < n; ++i) {
+    Problem q = ps[i];
+    q.grouped = true;
+    total += plan(q, true).total;
+  }
   return total;
 }
 
@@ -633,7 +642,8 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
   const int64_t da_blocks = cdiv(N * 16, 256);
   int64_t blk = 0;
   for (int i = 0; i < n; ++i) {
-    const Problem& p = ps[i];
+    Problem p = ps[i];
+    p.grouped = true;
     const Plan pl = plan(p, true);
     const bool dir = direct(p, io[i].alpha, io[i].basis, io[i].dalpha);
     L[i].x = io[i].x;

@@ -169,9 +169,21 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && ((KC == 2 && S >= 4) || (KC == 1 && S >= 7));
 }
+// With the activation, the two passes where the fused pass spills (bf16, 32 routes
+// and 5 to 8 taps, 16 routes and 8; at 16 routes and 7 taps the fused pass was
+// faster): the dx pass forms g = dy silu'(P) and leaves it in the workspace (fp32
+// [N, D]) for the taps pass.  Single launches only: the grouped and prefill
+// launches keep the fused pass.
+constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
+  return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8));
+}
+inline bool bwd_two_pass_g(const Problem& p) {
+  return !p.pre && !p.grouped &&
+         bwd_two_pass_g(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0, p.x_dt == DT_BF16);
+}
 inline bool bwd_two_pass(const Problem& p) {
   return bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,
-                      p.x_dt == DT_BF16);
+                      p.x_dt == DT_BF16) || bwd_two_pass_g(p);
 }
 
 // The taps pass holds one workgroup per CU (its LDS), so it runs as one round
@@ -222,13 +234,14 @@ void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, 
 // operands of all would not fit in registers beside the W operands.
 template <int S, int KC, bool ACT, bool BF>
 void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
-             void* dx, float* part_da, float* part_db, hipStream_t st) {
+             void* dx, float* part_da, float* part_db, float* gbuf, hipStream_t st) {
   if constexpr (!kcOK<KC, BF>) return;
   else {
   using E = typename CT<BF>::elem;
   constexpr bool kSplit = BF && KC >= 2;
+  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) || bwd_two_pass_g(S, KC, ACT, BF);
   // tiers for the fused pass at two resident workgroups per CU (not split in route chunks)
-  constexpr bool kTiers = !bwd_two_pass(S, KC, ACT, BF) && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
+  constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
   const int64_t gx_all = cdiv(p.D, kBwdCW);
   const Grid2 g = kTiers ? bwd_grid_tiered(p.n_tokens, gx_all, p.D, S, device_cu_count())
                          : bwd_grid(p.n_tokens, p.D, S);
@@ -237,11 +250,13 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
   // a grid split in route chunks is 1-D: 8 KC workgroups per 8 tiles (see bwd_block)
   const dim3 halves(static_cast<unsigned>(8 * KC * cdiv(static_cast<int64_t>(gx) * gy, 8)));
-  if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
-    if (dx != nullptr)
+  if constexpr (kTwo) {
+    // (with the activation the dx pass also forms g for the taps pass, so it
+    // runs without dx too)
+    if (dx != nullptr || ACT)
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
                          dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx, part_da,
-                         part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total);
+                         part_db, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total, gbuf);
     // both tap halves in one workgroup of 2 kBwdWPG waves (splitting the route
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
@@ -250,7 +265,7 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF, false, kBwdTaps>),
                        dim3(gt.gx, gt.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
-                       gt.n_old, gt.n_total);
+                       gt.n_old, gt.n_total, gbuf);
   } else {
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a,
@@ -379,17 +394,17 @@ void launch_fwd(const Problem& p, const void* x, const void* a_c, const void* b_
 
 template <int S>
 void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c, const void* b_c,
-                void* dx, float* part_da, float* part_db, hipStream_t st) {
+                void* dx, float* part_da, float* part_db, float* gbuf, hipStream_t st) {
   const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
 #define MOC_BWD(KC_)                                                                          \
   if (kc == KC_) {                                                                            \
     if (bf) {                                                                                 \
-      if (act) bwd_one<S, KC_, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);     \
-      else bwd_one<S, KC_, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);        \
+      if (act) bwd_one<S, KC_, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st); \
+      else bwd_one<S, KC_, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);  \
     } else {                                                                                  \
-      if (act) bwd_one<S, KC_, true, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);    \
-      else bwd_one<S, KC_, false, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, st);       \
+      if (act) bwd_one<S, KC_, true, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st); \
+      else bwd_one<S, KC_, false, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st); \
     }                                                                                         \
     return;                                                                                   \
   }
@@ -503,7 +518,7 @@ void launch_bwd_pre(const Problem& p, const void* x, const void* dy, const void*
   extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
                                       void*, hipStream_t);                                    \
   extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
-                                      const void*, void*, float*, float*, hipStream_t);       \
+                                      const void*, void*, float*, float*, float*, hipStream_t); \
   extern template void launch_fwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t); \
   extern template void launch_bwd_layers<S_>(const Problem&, const LayerOps*, int, hipStream_t); \
   extern template void launch_fwd_pre<S_>(const Problem&, const void*, const void*, const void*, \

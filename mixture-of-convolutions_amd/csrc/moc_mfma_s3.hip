@@ -7,7 +7,7 @@ namespace mfma {
 template void launch_fwd<3>(const Problem&, const void*, const void*, const void*, void*,
                              hipStream_t);
 template void launch_bwd<3>(const Problem&, const void*, const void*, const void*, const void*,
-                             void*, float*, float*, hipStream_t);
+                             void*, float*, float*, float*, hipStream_t);
 template void launch_fwd_layers<3>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_bwd_layers<3>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_fwd_pre<3>(const Problem&, const void*, const void*, const void*, void*,

@@ -7,7 +7,7 @@ namespace mfma {
 template void launch_fwd<8>(const Problem&, const void*, const void*, const void*, void*,
                              hipStream_t);
 template void launch_bwd<8>(const Problem&, const void*, const void*, const void*, const void*,
-                             void*, float*, float*, hipStream_t);
+                             void*, float*, float*, float*, hipStream_t);
 template void launch_fwd_layers<8>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_bwd_layers<8>(const Problem&, const LayerOps*, int, hipStream_t);
 template void launch_fwd_pre<8>(const Problem&, const void*, const void*, const void*, void*,

@@ -196,9 +196,14 @@ def test_layer_entries_validate_and_size():
     for which in ("forward", "backward"):
         q = getattr(L, f"moc_{which}_layers_workspace_bytes")
         single = getattr(L, f"moc_{which}_workspace_bytes")
-        # the single-layer queries cover either activation (no argument there)
+        # the single-layer queries cover either activation (no argument there);
+        # with SiLU a single backward of these shapes also holds g for its
+        # taps pass, which the grouped backward (the fused pass) does not
         total = sum(single(N, d, K, S, _lib.DT_BF16, 3) for d in dims)
-        assert q(arr, 3, N, K, S, _lib.DT_BF16, 1) == total
+        if which == "forward":
+            assert q(arr, 3, N, K, S, _lib.DT_BF16, 1) == total
+        else:
+            assert 0 < q(arr, 3, N, K, S, _lib.DT_BF16, 1) <= total
         assert q(arr, 3, N, K, S, _lib.DT_BF16, 0) <= total
         assert q(arr, 0, N, K, S, _lib.DT_BF16, 0) == 0
         fn = getattr(L, f"moc_{which}_layers")

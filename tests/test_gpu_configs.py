@@ -181,13 +181,14 @@ def test_config5_qkv_triple():
                                      (7, 12, None), (7, 32, "silu"),
                                      (8, 32, "silu"), (8, 32, None), (8, 5, "silu"),
                                      (6, 32, None), (8, 16, None), (7, 32, None), (7, 16, None),
-                                     (4, 32, None),
+                                     (4, 32, None), (5, 32, "silu"), (8, 16, "silu"), (7, 16, "silu"),
                                      (4, 64, "silu"), (2, 48, None), (8, 64, None)])
 def test_mfma_matches_generic(dtype, S, K, act):
     """Mid-size problems through both kernel families, fixed and packed, for
     every kernel size the matrix-core kernels are built for (2-8; bf16 without
-    activation at 4-8 taps and 32 routes, 7-8 taps and 16 routes: the two-pass
-    backward, odd kernel sizes with a missing last tap in the second half)."""
+    activation at 4-8 taps and 32 routes, 7-8 taps and 16 routes, and with SiLU
+    at 5-8 taps and 32 routes, 8 taps and 16 routes: the two-pass backward,
+    odd kernel sizes with a missing last tap in the second half)."""
     g = gen(S * 100 + K)
     D, Bt, T = 192, 3, 333
     x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
@@ -220,6 +221,31 @@ def test_mfma_matches_generic(dtype, S, K, act):
                                   cu.cpu(), dy.float().cpu().view(-1, D), act)
     for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), gv, refv):
         assert_close("varlen " + n, u.reshape(r.shape), r, dtype)
+
+
+@pytest.mark.parametrize("form", ["rows", "element"])
+@pytest.mark.parametrize("S,K", [(8, 32), (8, 16)])
+def test_two_pass_silu_without_dx(form, S, K):
+    """With SiLU the two-pass backward's dx pass also forms g for the taps pass:
+    without dx (need_x false) dalpha and dbasis are those of the call with dx,
+    bit for bit, for a full dy and for the one-element dy of y.sum()."""
+    from moc import ops
+    g = gen(S * 10 + K)
+    x = randn(g, 2, 150, 192, scale=0.5).to(DEV, torch.bfloat16)
+    a = torch.softmax(randn(g, 2, 150, K), -1).to(DEV, torch.bfloat16)
+    b = randn(g, K, S, 192, scale=0.2).to(DEV, torch.bfloat16)
+    if form == "rows":
+        dy = randn(g, 2, 150, 192).to(DEV, torch.bfloat16)
+    else:
+        dy = torch.ones((), device=DEV, dtype=torch.bfloat16).expand(2, 150, 192)
+    with_dx = ops.launch_backward(x, a, b, dy, activation_flag=1, need_x=True)
+    no_dx = ops.launch_backward(x, a, b, dy, activation_flag=1, need_x=False)
+    assert no_dx[0] is None
+    assert torch.equal(with_dx[1], no_dx[1]) and torch.equal(with_dx[2], no_dx[2])
+    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu().expand(2, 150, 192).contiguous(), "silu")
+    for n, u, r in zip(("dx", "dalpha", "dbasis"), with_dx, ref[1:]):
+        assert_close(n, u, r, torch.bfloat16)
 
 
 @pytest.mark.parametrize("S,K", [(5, 32), (7, 32), (8, 16), (7, 16)])
