@@ -783,12 +783,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   using MS = MSplit<BF>;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
   // route chunks of dbasis / dalpha this workgroup accumulates: all KC, or with
-  // SPLIT the single chunk kc0 = zh (W still uses every route)
-  constexpr int KX = SPLIT ? 1 : KC;
+  // SPLIT the single chunk kc0 = zh (W still uses every route; the taps pass of
+  // 64 routes: the chunk pair kc0 = 2 zh)
+  constexpr int KX = SPLIT ? (MODE == kBwdTaps ? 2 : 1) : KC;
   static_assert(!SPLIT || BF, "the route split is built for bf16 operands");
   static_assert(!SPLIT || KC % 2 == 0, "the route split takes an even number of route chunks");
-  static_assert(!(SPLIT && MODE == kBwdTaps), "one split at a time");
-  const int kc0 = SPLIT ? zh : 0;
+  static_assert(!(SPLIT && MODE == kBwdTaps) || KC == 4, "the taps pass splits 64 routes in halves");
+  const int kc0 = SPLIT ? zh * KX : 0;
   constexpr int EOWN = TB - (S - 1);
   constexpr int NP = MS::kParts;
   constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
@@ -1558,6 +1559,11 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   }
 }
 
+// Route parts of a split grid: one per route chunk, or route-chunk pairs for the
+// taps pass.
+template <int KC, bool SPLIT, int MODE>
+constexpr int kRouteParts = SPLIT ? (MODE == kBwdTaps ? KC / 2 : KC) : 1;
+
 // Workgroup -> (channel group bx, token range by, route chunk zh) over a grid of
 // gx channel groups.  Split in NZ route chunks, the grid is 1-D and the NZ
 // parts of a tile are 8 workgroup ids apart: ids go round-robin over the 8
@@ -1591,8 +1597,8 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
            float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
            int gx, int gy, int gy1, int n_old, int n_total, float* __restrict__ gbuf = nullptr) {
   int bx, by, zh;
-  if (!bwd_block<SPLIT ? KC : 1>(gx, gy, static_cast<int>(blockIdx.x), static_cast<int>(blockIdx.y), bx,
-                        by, zh))
+  if (!bwd_block<kRouteParts<KC, SPLIT, MODE>>(gx, gy, static_cast<int>(blockIdx.x),
+                                               static_cast<int>(blockIdx.y), bx, by, zh))
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(xv, dyv, dys, a_c, b_c, dxv, part_da, part_db,
                                                      seq, D, bx, by, zh, gy, gy1, n_old, n_total,

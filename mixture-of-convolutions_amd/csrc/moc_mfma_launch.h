@@ -181,10 +181,20 @@ inline bool bwd_two_pass_g(const Problem& p) {
   return !p.pre && !p.grouped &&
          bwd_two_pass_g(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0, p.x_dt == DT_BF16);
 }
+// 64 routes without activation: the two passes, the taps pass split in route
+// halves (two workgroups per tile, each forming the tile's m products for two of
+// the four route chunks; the fused pass forms them once per chunk).  Single
+// launches only.
+constexpr bool bwd_two_pass_r(int S, int KC, bool act, bool bf) { return bf && !act && KC == 4; }
 inline bool bwd_two_pass(const Problem& p) {
-  return bwd_two_pass(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0,
-                      p.x_dt == DT_BF16) || bwd_two_pass_g(p);
+  const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
+  const bool act = p.activation != 0, bf = p.x_dt == DT_BF16;
+  return bwd_two_pass(S, KC, act, bf) || bwd_two_pass_g(p) ||
+         (!p.pre && !p.grouped && bwd_two_pass_r(S, KC, act, bf));
 }
+// route parts of the taps pass's grid (halves with 64 routes), whose single
+// round of workgroups then covers half as many tiles
+constexpr int taps_route_parts(int KC) { return KC == 4 ? 2 : 1; }
 
 // The taps pass holds one workgroup per CU (its LDS), so it runs as one round
 // of n_cu workgroups, with ranges twice as long as the default grid's.  Two
@@ -197,7 +207,8 @@ inline Grid2 bwd_taps_grid(int64_t N, int64_t gx, int64_t D, int64_t S, int n_cu
 // The grid whose workgroups own the dalpha / dbasis partials (workspace,
 // stage 2): the taps pass's for the two-pass form, else the fused pass's.
 inline Grid2 bwd_partials_grid(const Problem& p) {
-  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, p.S, device_cu_count())
+  return bwd_two_pass(p) ? bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, p.S,
+                                         device_cu_count() / taps_route_parts(route_chunks(p.K)))
                          : bwd_grid_gx(p.n_tokens, cdiv(p.D, kBwdCW), p.D, p.S);
 }
 
@@ -239,7 +250,8 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   else {
   using E = typename CT<BF>::elem;
   constexpr bool kSplit = BF && KC >= 2;
-  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) || bwd_two_pass_g(S, KC, ACT, BF);
+  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) || bwd_two_pass_g(S, KC, ACT, BF) ||
+                        bwd_two_pass_r(S, KC, ACT, BF);
   // tiers for the fused pass at two resident workgroups per CU (not split in route chunks)
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
   const int64_t gx_all = cdiv(p.D, kBwdCW);
@@ -261,9 +273,13 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
     // chunks as well forms every m product twice again: measured slower than
     // the register spills it avoids)
     // (one round of workgroups: bwd_taps_grid)
-    const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, S, device_cu_count());
-    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF, false, kBwdTaps>),
-                       dim3(gt.gx, gt.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
+    // (64 routes: route halves on a 1-D grid, the halves of a tile 8 ids apart)
+    constexpr int kParts = taps_route_parts(KC);
+    const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, S, device_cu_count() / kParts);
+    const dim3 tgrid = kParts > 1 ? dim3(static_cast<unsigned>(8 * kParts * cdiv(int64_t(gt.gx) * gt.gy, 8)))
+                                  : dim3(gt.gx, gt.gy);
+    hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF, (kParts > 1), kBwdTaps>),
+                       tgrid, dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
                        gt.n_old, gt.n_total, gbuf);
   } else {

@@ -182,13 +182,15 @@ def test_config5_qkv_triple():
                                      (8, 32, "silu"), (8, 32, None), (8, 5, "silu"),
                                      (6, 32, None), (8, 16, None), (7, 32, None), (7, 16, None),
                                      (4, 32, None), (5, 32, "silu"), (8, 16, "silu"), (7, 16, "silu"),
+                                     (4, 64, None), (5, 48, None),
                                      (4, 64, "silu"), (2, 48, None), (8, 64, None)])
 def test_mfma_matches_generic(dtype, S, K, act):
     """Mid-size problems through both kernel families, fixed and packed, for
     every kernel size the matrix-core kernels are built for (2-8; bf16 without
     activation at 4-8 taps and 32 routes, 7-8 taps and 16 routes, and with SiLU
     at 5-8 taps and 32 routes, 8 taps and 16 routes: the two-pass backward,
-    odd kernel sizes with a missing last tap in the second half)."""
+    odd kernel sizes with a missing last tap in the second half; 64 routes
+    without activation: the two passes with the taps pass in route halves)."""
     g = gen(S * 100 + K)
     D, Bt, T = 192, 3, 333
     x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
