@@ -466,14 +466,14 @@ int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu6
   return MOC_OK;
 }
 
-bool grouped(const moc::Problem* ps, int n) {
+bool grouped(const moc::Problem* ps, int n, bool backward) {
   for (int i = 0; i < n; ++i)
     if (!use_mfma(ps[i])) return false;
-  return moc::mfma::layers_grouped(ps, n);
+  return moc::mfma::layers_grouped(ps, n, backward);
 }
 
 size_t layers_bytes(const moc::Problem* ps, int n, bool backward) {
-  if (grouped(ps, n))
+  if (grouped(ps, n, backward))
     return backward ? moc::mfma::backward_layers_workspace(ps, n)
                     : moc::mfma::forward_layers_workspace(ps, n);
   size_t total = 0;
@@ -529,7 +529,7 @@ int moc_forward_layers(const MocLayer* layers, int n_layers, const void* cu_seql
                 workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  if (grouped(ps, n_layers)) {
+  if (grouped(ps, n_layers, false)) {
     moc::mfma::LayerIO io[MOC_MAX_LAYERS] = {};
     for (int i = 0; i < n_layers; ++i)
       io[i] = moc::mfma::LayerIO{layers[i].x, layers[i].alpha, layers[i].basis, layers[i].y,
@@ -569,7 +569,7 @@ int moc_backward_layers(const MocLayer* layers, int n_layers, const void* cu_seq
                 workspace_bytes);
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  if (grouped(ps, n_layers)) {
+  if (grouped(ps, n_layers, true)) {
     moc::mfma::LayerIO io[MOC_MAX_LAYERS] = {};
     for (int i = 0; i < n_layers; ++i)
       io[i] = moc::mfma::LayerIO{layers[i].x, layers[i].alpha, layers[i].basis, nullptr,

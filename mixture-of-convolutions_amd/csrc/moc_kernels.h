@@ -76,7 +76,8 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
 
 // Grouped layers: layer i is problem ps[i] (one token axis; K, S, activation
 // shared) on tensors io[i]; layers_grouped tells whether they can run as one
-// launch per pass (bf16, at most 4 layers).
+// launch per pass (bf16, at most 4 layers; for the backward, not the shapes
+// whose single launch runs a form the grouped launch lacks).
 struct LayerIO {
   const void* x;
   const void* alpha;
@@ -87,7 +88,7 @@ struct LayerIO {
   void* dalpha;
   void* dbasis;
 };
-bool layers_grouped(const Problem* ps, int n);
+bool layers_grouped(const Problem* ps, int n, bool backward);
 size_t forward_layers_workspace(const Problem* ps, int n);
 size_t backward_layers_workspace(const Problem* ps, int n);
 void forward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace, hipStream_t st);

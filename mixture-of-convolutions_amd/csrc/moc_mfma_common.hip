@@ -570,7 +570,7 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
 // Grouped layers: bf16 layers on one token axis with the same K, S and
 // activation run every pass as one launch over all their channel groups.
 
-bool layers_grouped(const Problem* ps, int n) {
+bool layers_grouped(const Problem* ps, int n, bool backward) {
   if (n < 1 || n > kMaxLayers) return false;
   for (int i = 0; i < n; ++i) {
     const Problem& p = ps[i];
@@ -578,6 +578,14 @@ bool layers_grouped(const Problem* ps, int n) {
     if (p.K != ps[0].K || p.S != ps[0].S || p.activation != ps[0].activation ||
         p.n_tokens != ps[0].n_tokens || p.path != ps[0].path)
       return false;
+  }
+  // the backward shapes whose single launch runs a two-pass form the grouped
+  // launch does not have (with SiLU; 64 routes) run as single launches, so the
+  // results stay those of the per-layer calls
+  if (backward) {
+    const int S = static_cast<int>(ps[0].S), KC = route_chunks(ps[0].K);
+    const bool act = ps[0].activation != 0;
+    if (bwd_two_pass_g(S, KC, act, true) || bwd_two_pass_r(S, KC, act, true)) return false;
   }
   return true;
 }

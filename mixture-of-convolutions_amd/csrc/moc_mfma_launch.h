@@ -169,13 +169,14 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
   return bf && !act && ((KC == 2 && S >= 4) || (KC == 1 && S >= 7));
 }
-// With the activation, the two passes where the fused pass spills (bf16, 32 routes
-// and 5 to 8 taps, 16 routes and 8; at 16 routes and 7 taps the fused pass was
-// faster): the dx pass forms g = dy silu'(P) and leaves it in the workspace (fp32
-// [N, D]) for the taps pass.  Single launches only: the grouped and prefill
-// launches keep the fused pass.
+// With the activation, the two passes where the fused pass spills or forms the
+// same work per route chunk (bf16: 32 routes and 5 to 8 taps, 16 routes and 8,
+// 64 routes and 3 to 8; measured against the fused pass at each size): the dx
+// pass forms g = dy silu'(P) and leaves it in the workspace (fp32 [N, D]) for the
+// taps pass.  Single launches only: the grouped and prefill launches keep the
+// fused pass.
 constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
-  return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8));
+  return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8) || (KC == 4 && S >= 3));
 }
 inline bool bwd_two_pass_g(const Problem& p) {
   return !p.pre && !p.grouped &&

@@ -182,7 +182,7 @@ def test_config5_qkv_triple():
                                      (8, 32, "silu"), (8, 32, None), (8, 5, "silu"),
                                      (6, 32, None), (8, 16, None), (7, 32, None), (7, 16, None),
                                      (4, 32, None), (5, 32, "silu"), (8, 16, "silu"), (7, 16, "silu"),
-                                     (4, 64, None), (5, 48, None),
+                                     (4, 64, None), (5, 48, None), (6, 64, "silu"), (3, 48, "silu"),
                                      (4, 64, "silu"), (2, 48, None), (8, 64, None)])
 def test_mfma_matches_generic(dtype, S, K, act):
     """Mid-size problems through both kernel families, fixed and packed, for
