@@ -749,16 +749,22 @@ constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 // Two, except for the bf16 fused pass with 8 taps and 32 routes: there the
 // working set exceeds 256 registers, and one wave per SIMD (spills to AGPRs
 // instead of scratch memory) measured 9% faster than two with scratch spills.
-// (The fp32 form of that pass stays at two: LLVM's AGPR-copy rewrite crashes
-// on its one-wave form.)
+// The fp32 fused pass (fp32 rows: twice the registers per window) spills at
+// two waves from 3 taps up; at one wave, B4 T4096 D2048, 16 routes: 4 taps
+// 262 -> 215 us, 8 taps 962 -> 447; 32 routes: 4 taps 607 -> 358, 8 taps
+// 1790 -> 1039.  32 routes with 6 taps stays at two: LLVM's AGPR-copy rewrite
+// crashes on its one-wave form.  16 routes below 4 taps gained nothing.
 #ifndef MOC_BWD_MIN_WAVES
 #define MOC_BWD_MIN_WAVES 2
 #endif
 #ifndef MOC_BWD_TAPS_WAVES
 #define MOC_BWD_TAPS_WAVES MOC_BWD_MIN_WAVES
 #endif
+template <int S, int KC, bool BF>
+constexpr bool kBwdOneWaveFused = BF ? ((S >= 8 && KC >= 2) || KC >= 4)
+                                     : ((KC == 1 && S >= 4) || (KC == 2 && S != 6));
 template <int S, int KC, int MODE, bool BF>
-constexpr int kBwdMinWaves = (MODE == kBwdFused && ((S >= 8 && KC >= 2) || KC >= 4) && BF) ? 1
+constexpr int kBwdMinWaves = (MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>) ? 1
                              : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
 // bwd_tile is the work of workgroup (bx, by) (route chunk zh with SPLIT) of
