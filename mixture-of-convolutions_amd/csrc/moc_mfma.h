@@ -763,9 +763,16 @@ constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 template <int S, int KC, bool BF>
 constexpr bool kBwdOneWaveFused = BF ? ((S >= 8 && KC >= 2) || KC >= 4)
                                      : ((KC == 1 && S >= 4) || (KC == 2 && S != 6));
-template <int S, int KC, int MODE, bool BF>
-constexpr int kBwdMinWaves = (MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>) ? 1
-                             : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
+// The dx pass over four route chunks (64 routes) holds the W operands of all
+// four and spills at two waves from 7 taps up, and from 5 with SiLU (up to 141
+// registers); at one wave, B4 T4096 D2048, 64 routes, backward entry: 8 taps
+// 541 -> 427 us, with SiLU 926 -> 538.  Without SiLU at 6 taps one wave was
+// slower (316 -> 333).
+template <int S, int KC, int MODE, bool BF, bool ACT = false>
+constexpr int kBwdMinWaves = ((MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>) ||
+                              (MODE == kBwdDx && KC >= 4 && (S >= 7 || (ACT && S >= 5))))
+                                 ? 1
+                                 : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
 // bwd_tile is the work of workgroup (bx, by) (route chunk zh with SPLIT) of
 // one layer; the __global__ wrappers below map the grid onto it.  PRE (fused
@@ -1596,7 +1603,7 @@ __device__ __forceinline__ bool bwd_block(int gx, int gy, int idx, int idy, int&
 
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF, ACT>)))
 bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
            const typename CT<BF>::elem* __restrict__ a_c,
            const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
@@ -1657,7 +1664,7 @@ bwd_pre_taps_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, i
 // gx gy blocks of layer i, or its split grid's ids).
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF>)))
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF, ACT>)))
 bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
   using E = typename CT<BF>::elem;
   const int blk = static_cast<int>(blockIdx.x);
