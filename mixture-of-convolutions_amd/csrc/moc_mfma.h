@@ -753,7 +753,9 @@ constexpr int kBwdFused = 0, kBwdDx = 1, kBwdTaps = 2;
 // two waves from 3 taps up; at one wave, B4 T4096 D2048, 16 routes: 4 taps
 // 262 -> 215 us, 8 taps 962 -> 447; 32 routes: 4 taps 607 -> 358, 8 taps
 // 1790 -> 1039.  32 routes with 6 taps stays at two: LLVM's AGPR-copy rewrite
-// crashes on its one-wave form.  16 routes below 4 taps gained nothing.
+// crashes on its one-wave form.  16 routes below 4 taps gained nothing.  The
+// bf16 pass at 16 routes, 6-7 taps spills 16-48 registers at two waves; one
+// wave measured slower there (6 taps 136 -> 150 us, 7 with SiLU 174 -> 196).
 #ifndef MOC_BWD_MIN_WAVES
 #define MOC_BWD_MIN_WAVES 2
 #endif
