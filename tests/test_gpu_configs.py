@@ -183,7 +183,8 @@ def test_config5_qkv_triple():
                                      (6, 32, None), (8, 16, None), (7, 32, None), (7, 16, None),
                                      (4, 32, None), (5, 32, "silu"), (8, 16, "silu"), (7, 16, "silu"),
                                      (4, 64, None), (5, 48, None), (6, 64, "silu"), (3, 48, "silu"),
-                                     (4, 64, "silu"), (2, 48, None), (8, 64, None)])
+                                     (4, 64, "silu"), (2, 48, None), (8, 64, None),
+                                     (2, 32, None), (3, 24, "silu")])
 def test_mfma_matches_generic(dtype, S, K, act):
     """Mid-size problems through both kernel families, fixed and packed, for
     every kernel size the matrix-core kernels are built for (2-8; bf16 without
