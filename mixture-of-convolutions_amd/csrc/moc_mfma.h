@@ -1622,10 +1622,14 @@ bwd_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dy
 
 // Prefill from a cache (Pre): the fused pass on a 2-D grid (bf16 with 32
 // routes, which the plain backward splits, at one wave per SIMD: both route
-// chunks' accumulators and operands stay in registers; with 8 taps or 64
-// routes at two, as LLVM's AGPR-copy rewrite crashes on those one-wave forms).
+// chunks' accumulators and operands stay in registers; with 64 routes at two,
+// as LLVM's AGPR-copy rewrite crashes on that one-wave form).  bf16 with 6-8
+// taps runs it at one wave too (at two it spilled up to 121 registers at 16
+// routes and 440 at 32): B4 T4096 D2048 with SiLU, 16 routes: 6 taps
+// 204 -> 182 us, 7 taps 387 -> 200, 8 taps 537 -> 237; 32 routes, 8 taps
+// 1832 -> 973.
 template <int S, int KC, bool BF>
-constexpr int kBwdPreWaves = (BF && KC == 2 && S < 8) ? 1
+constexpr int kBwdPreWaves = (BF && (KC == 2 || (KC == 1 && S >= 6))) ? 1
                              : (BF && KC >= 2) ? 2 : kBwdMinWaves<S, KC, kBwdFused, BF>;
 // With 64 routes (SPLIT) it is split in route chunks like the plain pass.
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT>
