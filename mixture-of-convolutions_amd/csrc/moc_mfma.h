@@ -233,9 +233,12 @@ __device__ __forceinline__ void tap_bits_rows(const SeqLayout& seq, int64_t row0
 //   fin [n_seqs, D, S] (or null) receives each sequence's last S inputs (the
 //     state a later call continues from), slot S-1 the last token; with T < S
 //     its oldest S-T slots are the cache's newest ones (zeros without a cache).
+//   g (backward, two passes with the activation): fp32 [N, D] g = dy silu'(P),
+//     written by the dx pass (whose P reads the cache), read by the taps pass.
 struct Pre {
   const void* hist;
   void* fin;
+  float* g = nullptr;
 };
 
 // History value of window rows u0 + w (w < NW) for this lane's channels: with
@@ -813,13 +816,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   // work of this MODE: dx rows, m products of ST taps from tap s0
   constexpr bool DO_DX = MODE != kBwdTaps, DO_M = MODE != kBwdDx;
   static_assert(MODE == kBwdFused || BF, "the partial passes are built for bf16");
-  static_assert(!(ACT && PRE && MODE != kBwdFused), "prefill with the activation runs the fused pass");
   // with the activation: P (and g) formed in this pass; g read from gbuf (taps
   // pass) or written there (dx pass)
   constexpr bool PACT = ACT && MODE != kBwdTaps;
   constexpr bool GIN = ACT && MODE == kBwdTaps, GOUT = ACT && MODE == kBwdDx;
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
-  static_assert(!PRE || MODE != kBwdDx, "the prefill dx pass is the plain one (it reads no cache)");
+  static_assert(!PRE || MODE != kBwdDx || ACT,
+                "without the activation the prefill dx pass is the plain one (it reads no cache)");
   constexpr int ST = MODE == kBwdTaps ? (S + 1) / 2 : S;
   // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, ST) and
   // [ST, S): x and dy rows are read once per workgroup and the dalpha sum over
@@ -1650,9 +1653,11 @@ bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_
       pre);
 }
 
-// Prefill from a cache in the two-pass form (the shapes of bwd_two_pass: bf16, no
-// activation): the m products of the taps pass, whose masked taps read the cache;
-// the dx pass is the plain one (dx reads no cache).
+// Prefill from a cache in the two-pass form (bf16; the shapes of bwd_two_pass,
+// and with the activation those of pre_two_pass_g): the m products of the taps pass,
+// whose masked taps read the cache (with the activation from g = pre.g).
+// Without the activation the dx pass is the plain one (dx reads no cache); with
+// it, bwd_pre_dx_kernel, whose P reads the cache and which writes pre.g.
 template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
 __global__ void __launch_bounds__(64 * WPG)
 __attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, kBwdTaps, BF>)))
@@ -1663,7 +1668,22 @@ bwd_pre_taps_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, i
                     int gy1, int n_old, int n_total, Pre pre) {
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, false, kBwdTaps, true>(
       xv, dyv, dys, a_c, b_c, nullptr, part_da, part_db, seq, D, static_cast<int>(blockIdx.x),
-      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre);
+      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre, pre.g);
+}
+
+// (one wave per SIMD from 7 taps: at two it spilled 36 registers at 8 taps;
+// 32 routes with SiLU, B4 T4096 D2048: 8 taps 427 -> 361 us per backward entry)
+template <int S, int KC, int NB, int NC, int WPG, bool BF>
+__global__ void __launch_bounds__(64 * WPG)
+__attribute__((amdgpu_waves_per_eu(S >= 7 ? 1 : 2)))
+bwd_pre_dx_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
+                  const typename CT<BF>::elem* __restrict__ a_c,
+                  const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
+                  SeqLayout seq, int64_t D, int gx, int gy, int gy1, int n_old, int n_total,
+                  Pre pre) {
+  bwd_tile<S, KC, NB, NC, WPG, true, BF, false, kBwdDx, true>(
+      xv, dyv, dys, a_c, b_c, dxv, nullptr, nullptr, seq, D, static_cast<int>(blockIdx.x),
+      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre, pre.g);
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another:

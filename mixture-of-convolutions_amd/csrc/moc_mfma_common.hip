@@ -531,7 +531,9 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
   }
   float* pda = reinterpret_cast<float*>(ws + pl.off_pda);
   float* pdb = reinterpret_cast<float*>(ws + pl.off_pdb);
-  const Pre pre{cache, nullptr};
+  // g = dy silu'(P) from the dx pass to the taps pass (the two-pass shapes with SiLU)
+  float* gb = bwd_two_pass_g(p) ? reinterpret_cast<float*>(ws + pl.off_g) : nullptr;
+  const Pre pre{cache, nullptr, gb};
   prof_begin(p, st);
   switch (p.S) {
     case 2: launch_bwd_pre<2>(p, x, dy, a_c, b_c, dx, pda, pdb, pre, st); break;

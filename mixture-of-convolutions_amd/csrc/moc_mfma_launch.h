@@ -173,14 +173,19 @@ constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
 // same work per route chunk (bf16: 32 routes and 5 to 8 taps, 16 routes and 8,
 // 64 routes and 3 to 8; measured against the fused pass at each size): the dx
 // pass forms g = dy silu'(P) and leaves it in the workspace (fp32 [N, D]) for the
-// taps pass.  Single launches only: the grouped and prefill launches keep the
-// fused pass.
+// taps pass.  Single launches only (the grouped launch keeps the fused pass).
 constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
   return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8) || (KC == 4 && S >= 3));
 }
+// The prefill runs those two passes (the dx pass's P reading the cache) with 32
+// routes and 6-8 taps; elsewhere its fused pass measured faster (B4 T4096
+// D2048 with SiLU: 32 routes, 5 taps 216 against 242 us; 16 routes, 8 taps 232
+// against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 -> 257 / 335 / 429).
+constexpr bool pre_two_pass_g(int S, int KC) { return KC == 2 && S >= 6; }
 inline bool bwd_two_pass_g(const Problem& p) {
-  return !p.pre && !p.grouped &&
-         bwd_two_pass_g(static_cast<int>(p.S), route_chunks(p.K), p.activation != 0, p.x_dt == DT_BF16);
+  const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
+  return !p.grouped && (!p.pre || pre_two_pass_g(S, KC)) &&
+         bwd_two_pass_g(S, KC, p.activation != 0, p.x_dt == DT_BF16);
 }
 // 64 routes without activation: the two passes, the taps pass split in route
 // halves (two workgroups per tile, each forming the tile's m products for two of
@@ -468,6 +473,20 @@ void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_
                          part_da, part_db, p.seq, p.D, static_cast<int>(gd.gx),
                          static_cast<int>(gd.gy), gd.gy1, gd.n_old, gd.n_total);
     }
+    hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF>),
+                       dim3(g.gx, g.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b,
+                       part_da, part_db, p.seq, p.D, static_cast<int>(g.gx),
+                       static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total, pre);
+  } else if constexpr (bwd_two_pass_g(S, KC, ACT, BF) && pre_two_pass_g(S, KC)) {
+    // with the activation: the dx pass forms P with the cache and writes g to
+    // pre.g (also without dx), then the taps pass reads g in place of dy
+    const auto* a = static_cast<const E*>(a_c);
+    const auto* b = static_cast<const E*>(b_c);
+    const Grid2 gd = bwd_grid(p.n_tokens, p.D, S);
+    hipLaunchKernelGGL((bwd_pre_dx_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, BF>), dim3(gd.gx, gd.gy),
+                       dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx, p.seq, p.D,
+                       static_cast<int>(gd.gx), static_cast<int>(gd.gy), gd.gy1, gd.n_old,
+                       gd.n_total, pre);
     hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF>),
                        dim3(g.gx, g.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b,
                        part_da, part_db, p.seq, p.D, static_cast<int>(g.gx),

@@ -67,6 +67,10 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (7, 16, "silu", F32, 6),
     (4, 64, "silu", BF, 21),
     (3, 48, None, BF, 7),
+    (5, 32, "silu", BF, 12),
+    (7, 32, "silu", BF, 70),
+    (6, 24, "silu", BF, 5),
+    (8, 16, "silu", BF, 50),
 ]
 
 
@@ -93,6 +97,22 @@ def test_prefill_entries_against_oracle(S, K, act, dtype, T):
     assert_close("prefill dbasis", db, rb.grad, dtype)
     assert_close("prefill dcache", dc, rc.grad, dtype)
     assert torch.all(dc[:, :, 0] == 0)
+
+
+@pytest.mark.parametrize("S,K", [(8, 32), (6, 32), (7, 24)])
+def test_prefill_two_pass_silu_without_dx(S, K):
+    """With SiLU at these shapes the prefill backward runs two passes, the first
+    forming g = dy silu'(P) with P over the cache: without dx, dalpha, dbasis
+    and dcache equal those of the call with dx bit for bit."""
+    B, T, D = 3, 45, 192
+    x, a, b, c, dy = _inputs(S * 10 + K, B, T, D, K, S, BF)
+    full = ops.launch_backward_prefill(x, a, b, c, dy, activation_flag=1, need_x=True,
+                                       need_cache=True)
+    part = ops.launch_backward_prefill(x, a, b, c, dy, activation_flag=1, need_x=False,
+                                       need_cache=True)
+    assert part[0] is None
+    for n, u, v in zip(("dalpha", "dbasis", "dcache"), full[1:], part[1:]):
+        assert torch.equal(u, v), n
 
 
 @pytest.mark.parametrize("T,S", [(2, 4), (4, 4), (9, 4), (1, 8), (30, 8)])
