@@ -22,7 +22,8 @@ struct Problem {
   int64_t dy_stride = 0;  // backward: elements between token rows of dy (D; 0: one row for all
                           // tokens; -1: one element for every token and channel)
   int path = PATH_AUTO;   // PATH_MFMA_PREP: MFMA kernels, operands always through prep
-  bool pre = false;       // prefill from a cache: the backward is the fused pass for every shape
+  bool pre = false;       // prefill from a cache: with the activation, the two passes only at
+                          // 32 routes and 6-8 taps (pre_two_pass_g)
   bool grouped = false;   // a layer of a grouped launch: with the activation, the fused pass
   hipEvent_t prof_start = nullptr;  // recorded around the main kernel when set
   hipEvent_t prof_stop = nullptr;
