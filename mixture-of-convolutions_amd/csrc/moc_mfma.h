@@ -1658,7 +1658,9 @@ bwd_pre_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_
 // whose masked taps read the cache (with the activation from g = pre.g).
 // Without the activation the dx pass is the plain one (dx reads no cache); with
 // it, bwd_pre_dx_kernel, whose P reads the cache and which writes pre.g.
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF>
+// With 64 routes (SPLIT) the taps pass runs in route halves on a 1-D grid, as
+// the plain one does.
+template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT = false>
 __global__ void __launch_bounds__(64 * WPG)
 __attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, kBwdTaps, BF>)))
 bwd_pre_taps_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
@@ -1666,16 +1668,21 @@ bwd_pre_taps_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, i
                     const typename CT<BF>::elem* __restrict__ b_c, float* __restrict__ part_da,
                     float* __restrict__ part_db, SeqLayout seq, int64_t D, int gx, int gy,
                     int gy1, int n_old, int n_total, Pre pre) {
-  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, false, kBwdTaps, true>(
-      xv, dyv, dys, a_c, b_c, nullptr, part_da, part_db, seq, D, static_cast<int>(blockIdx.x),
-      static_cast<int>(blockIdx.y), 0, gy, gy1, n_old, n_total, pre, pre.g);
+  int bx, by, zh;
+  if (!bwd_block<kRouteParts<KC, SPLIT, kBwdTaps>>(gx, gy, static_cast<int>(blockIdx.x),
+                                                   static_cast<int>(blockIdx.y), bx, by, zh))
+    return;  // whole workgroup, before any barrier
+  bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, kBwdTaps, true>(
+      xv, dyv, dys, a_c, b_c, nullptr, part_da, part_db, seq, D, bx, by, zh, gy, gy1, n_old,
+      n_total, pre, pre.g);
 }
 
 // (one wave per SIMD from 7 taps: at two it spilled 36 registers at 8 taps;
-// 32 routes with SiLU, B4 T4096 D2048: 8 taps 427 -> 361 us per backward entry)
+// 32 routes with SiLU, B4 T4096 D2048: 8 taps 427 -> 361 us per backward entry;
+// with 64 routes from 5 taps, as the plain dx pass)
 template <int S, int KC, int NB, int NC, int WPG, bool BF>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(S >= 7 ? 1 : 2)))
+__attribute__((amdgpu_waves_per_eu((S >= 7 || (KC >= 4 && S >= 5)) ? 1 : 2)))
 bwd_pre_dx_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                   const typename CT<BF>::elem* __restrict__ a_c,
                   const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,

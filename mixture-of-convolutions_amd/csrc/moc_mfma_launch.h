@@ -178,10 +178,11 @@ constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
   return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8) || (KC == 4 && S >= 3));
 }
 // The prefill runs those two passes (the dx pass's P reading the cache) with 32
-// routes and 6-8 taps; elsewhere its fused pass measured faster (B4 T4096
-// D2048 with SiLU: 32 routes, 5 taps 216 against 242 us; 16 routes, 8 taps 232
-// against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 -> 257 / 335 / 429).
-constexpr bool pre_two_pass_g(int S, int KC) { return KC == 2 && S >= 6; }
+// routes and 6-8 taps and with 64 routes; elsewhere its fused pass measured
+// faster (B4 T4096 D2048 with SiLU: 32 routes, 5 taps 216 against 242 us; 16
+// routes, 8 taps 232 against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 ->
+// 257 / 335 / 429).
+constexpr bool pre_two_pass_g(int S, int KC) { return (KC == 2 && S >= 6) || KC == 4; }
 inline bool bwd_two_pass_g(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
   return !p.grouped && (!p.pre || pre_two_pass_g(S, KC)) &&
@@ -189,14 +190,17 @@ inline bool bwd_two_pass_g(const Problem& p) {
 }
 // 64 routes without activation: the two passes, the taps pass split in route
 // halves (two workgroups per tile, each forming the tile's m products for two of
-// the four route chunks; the fused pass forms them once per chunk).  Single
-// launches only.
+// the four route chunks; the fused pass forms them once per chunk).  Single and
+// prefill launches (not grouped); the prefill up to 7 taps: at 8 its taps pass
+// returned non-finite dalpha / dbasis in the second route half (cause not
+// found), so that shape keeps the fused pass.
 constexpr bool bwd_two_pass_r(int S, int KC, bool act, bool bf) { return bf && !act && KC == 4; }
+constexpr bool pre_two_pass_r(int S) { return S < 8; }
 inline bool bwd_two_pass(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
   const bool act = p.activation != 0, bf = p.x_dt == DT_BF16;
   return bwd_two_pass(S, KC, act, bf) || bwd_two_pass_g(p) ||
-         (!p.pre && !p.grouped && bwd_two_pass_r(S, KC, act, bf));
+         (!p.grouped && (!p.pre || pre_two_pass_r(S)) && bwd_two_pass_r(S, KC, act, bf));
 }
 // route parts of the taps pass's grid (halves with 64 routes), whose single
 // round of workgroups then covers half as many tiles
@@ -461,38 +465,41 @@ void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_
   else {
   using E = typename CT<BF>::elem;
   const Grid2 g = bwd_partials_grid(p);
-  if constexpr (bwd_two_pass(S, KC, ACT, BF)) {
-    // two passes as bwd_one runs them: the plain dx pass (dx reads no cache),
-    // then the taps pass with the cache (g is the taps grid here)
+  // the two-pass shapes of the plain backward: without the activation all of
+  // them; with it those of pre_two_pass_g
+  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) ||
+                        (bwd_two_pass_r(S, KC, ACT, BF) && pre_two_pass_r(S)) ||
+                        (bwd_two_pass_g(S, KC, ACT, BF) && pre_two_pass_g(S, KC));
+  if constexpr (kTwo) {
+    // the dx pass: without the activation the plain one (dx reads no cache);
+    // with it bwd_pre_dx_kernel, which forms P with the cache and writes g to
+    // pre.g (also without dx).  Then the taps pass with the cache (reading g in
+    // place of dy with the activation; g is the taps grid here), with 64 routes
+    // in route halves on a 1-D grid as bwd_one runs it.
     const auto* a = static_cast<const E*>(a_c);
     const auto* b = static_cast<const E*>(b_c);
-    if (dx != nullptr) {
-      const Grid2 gd = bwd_grid(p.n_tokens, p.D, S);
+    const Grid2 gd = bwd_grid(p.n_tokens, p.D, S);
+    if constexpr (ACT) {
+      hipLaunchKernelGGL((bwd_pre_dx_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, BF>),
+                         dim3(gd.gx, gd.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx,
+                         p.seq, p.D, static_cast<int>(gd.gx), static_cast<int>(gd.gy), gd.gy1,
+                         gd.n_old, gd.n_total, pre);
+    } else if (dx != nullptr) {
       hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, false, kBwdDx>),
                          dim3(gd.gx, gd.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx,
                          part_da, part_db, p.seq, p.D, static_cast<int>(gd.gx),
                          static_cast<int>(gd.gy), gd.gy1, gd.n_old, gd.n_total);
     }
-    hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF>),
-                       dim3(g.gx, g.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b,
-                       part_da, part_db, p.seq, p.D, static_cast<int>(g.gx),
-                       static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total, pre);
-  } else if constexpr (bwd_two_pass_g(S, KC, ACT, BF) && pre_two_pass_g(S, KC)) {
-    // with the activation: the dx pass forms P with the cache and writes g to
-    // pre.g (also without dx), then the taps pass reads g in place of dy
-    const auto* a = static_cast<const E*>(a_c);
-    const auto* b = static_cast<const E*>(b_c);
-    const Grid2 gd = bwd_grid(p.n_tokens, p.D, S);
-    hipLaunchKernelGGL((bwd_pre_dx_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, BF>), dim3(gd.gx, gd.gy),
-                       dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a, b, dx, p.seq, p.D,
-                       static_cast<int>(gd.gx), static_cast<int>(gd.gy), gd.gy1, gd.n_old,
-                       gd.n_total, pre);
-    hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF>),
-                       dim3(g.gx, g.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b,
-                       part_da, part_db, p.seq, p.D, static_cast<int>(g.gx),
-                       static_cast<int>(g.gy), g.gy1, g.n_old, g.n_total, pre);
+    constexpr int kParts = taps_route_parts(KC);
+    const dim3 tgrid = kParts > 1 ? dim3(static_cast<unsigned>(8 * kParts * cdiv(int64_t(g.gx) * g.gy, 8)))
+                                  : dim3(g.gx, g.gy);
+    hipLaunchKernelGGL((bwd_pre_taps_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, BF, (kParts > 1)>),
+                       tgrid, dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, part_da, part_db,
+                       p.seq, p.D, static_cast<int>(g.gx), static_cast<int>(g.gy), g.gy1, g.n_old,
+                       g.n_total, pre);
   } else {
-    // 64 routes: split in route chunks on a 1-D grid, as bwd_one does
+    // the fused pass; 64 routes (with SiLU and 2 taps, or 8 taps without):
+    // split in route chunks on a 1-D grid, as bwd_one does
     constexpr bool kSplit = BF && KC >= 4;
     const dim3 grid = kSplit ? dim3(static_cast<unsigned>(8 * KC * cdiv(int64_t(g.gx) * g.gy, 8)))
                              : dim3(g.gx, g.gy);

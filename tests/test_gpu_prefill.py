@@ -71,6 +71,12 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
     (7, 32, "silu", BF, 70),
     (6, 24, "silu", BF, 5),
     (8, 16, "silu", BF, 50),
+    (8, 64, None, BF, 40),
+    (7, 64, None, BF, 70),
+    (5, 48, None, BF, 40),
+    (6, 48, "silu", BF, 9),
+    (8, 64, "silu", BF, 70),
+    (2, 64, "silu", BF, 5),
 ]
 
 
@@ -99,7 +105,7 @@ def test_prefill_entries_against_oracle(S, K, act, dtype, T):
     assert torch.all(dc[:, :, 0] == 0)
 
 
-@pytest.mark.parametrize("S,K", [(8, 32), (6, 32), (7, 24)])
+@pytest.mark.parametrize("S,K", [(8, 32), (6, 32), (7, 24), (4, 64), (8, 48)])
 def test_prefill_two_pass_silu_without_dx(S, K):
     """With SiLU at these shapes the prefill backward runs two passes, the first
     forming g = dy silu'(P) with P over the cache: without dx, dalpha, dbasis
