@@ -287,7 +287,7 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
  * All tensors bf16; cache [batch, dim, kernel_size] contiguous, updated in place.
  *   z : [batch, z_dim], router : [k, z_dim], x, y : [batch, dim],
  *   basis : [k, kernel_size, dim]
- * Shapes: kernel_size in {2, 3, 4, 8}, k % 4 == 0, k <= 32, dim % 4 == 0,
+ * Shapes: 2 <= kernel_size <= 8, k % 4 == 0, k <= 32, dim % 4 == 0,
  * z_dim % 64 == 0 (moc_decode_step_supported returns 1 for such shapes).
  */
 int moc_decode_step_supported(int64_t batch, int64_t z_dim, int64_t dim, int64_t k,

@@ -377,7 +377,11 @@ void launch_any(const void* x, const void* alpha, int routing, const void* basis
     case 2: launch_s<2, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
     case 3: launch_s<3, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
     case 4: launch_s<4, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    default: launch_s<8, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 5: launch_s<5, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 6: launch_s<6, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 7: launch_s<7, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    case 8: launch_s<8, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
+    default: break;  // decode_supported admits 2-8 only
   }
 }
 
@@ -385,7 +389,7 @@ void launch_any(const void* x, const void* alpha, int routing, const void* basis
 
 bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                       int64_t cs_b, int64_t cs_d, int64_t cs_s) {
-  const bool s_ok = S == 2 || S == 3 || S == 4 || S == 8;
+  const bool s_ok = S >= 2 && S <= 8;
   // buffers are addressed with 32-bit byte offsets
   const int64_t lim = int64_t(1) << 31;
   return x_dt == DT_BF16 && a_dt == DT_BF16 && b_dt == DT_BF16 && s_ok && K <= 32 && K % 4 == 0 &&
