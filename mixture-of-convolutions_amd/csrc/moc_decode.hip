@@ -363,9 +363,13 @@ void launch_s(const void* x, const void* alpha, int routing, const void* basis, 
   if (K <= 16) {
     if (act) launch_one<S, 1, true, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
     else launch_one<S, 1, false, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
-  } else {
+  } else if (K <= 32) {
     if (act) launch_one<S, 2, true, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
     else launch_one<S, 2, false, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+  } else if constexpr (!FUSED) {
+    // 33-64 routes: given logits / weights only (the fused router GEMV stops at 32)
+    if (act) launch_one<S, 4, true, false>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+    else launch_one<S, 4, false, false>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
   }
 }
 
@@ -392,7 +396,7 @@ bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int 
   const bool s_ok = S >= 2 && S <= 8;
   // buffers are addressed with 32-bit byte offsets
   const int64_t lim = int64_t(1) << 31;
-  return x_dt == DT_BF16 && a_dt == DT_BF16 && b_dt == DT_BF16 && s_ok && K <= 32 && K % 4 == 0 &&
+  return x_dt == DT_BF16 && a_dt == DT_BF16 && b_dt == DT_BF16 && s_ok && K <= 64 && K % 4 == 0 &&
          D % 4 == 0 && cs_s == 1 && cs_d == S && cs_b == D * S && 16 * D * S * 2 < lim &&
          B * K * 2 < lim && K * S * D * 2 < lim;
 }
@@ -406,7 +410,7 @@ void launch_decode(const void* x, const void* alpha, int routing, const void* ba
 
 bool decode_step_supported(int64_t B, int64_t D, int64_t Z, int64_t K, int64_t S) {
   const int64_t lim = int64_t(1) << 31;
-  return decode_supported(B, D, K, S, DT_BF16, DT_BF16, DT_BF16, D * S, S, 1) && Z >= 64 &&
+  return decode_supported(B, D, K, S, DT_BF16, DT_BF16, DT_BF16, D * S, S, 1) && K <= 32 && Z >= 64 &&
          Z % 64 == 0 && 16 * Z * 2 < lim && K * Z * 2 < lim;
 }
 

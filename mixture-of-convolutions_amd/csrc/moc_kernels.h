@@ -98,7 +98,7 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
 }  // namespace mfma
 
 // decode step on the matrix cores (moc_decode.hip): bf16 x, logits / weights
-// and basis, contiguous [B, D, S] cache, 2 <= S <= 8, K % 4 == 0, K <= 32,
+// and basis, contiguous [B, D, S] cache, 2 <= S <= 8, K % 4 == 0, K <= 64,
 // D % 4 == 0
 bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                       int64_t cs_b, int64_t cs_d, int64_t cs_s);

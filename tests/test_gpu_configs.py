@@ -272,7 +272,7 @@ def test_two_pass_small_and_ragged(S, K, B, T, D):
 
 
 @pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 20), (8, 32), (8, 5), (5, 16), (6, 24),
-                                 (7, 32)])
+                                 (7, 32), (4, 48), (8, 64)])
 @pytest.mark.parametrize("route", [None, "softmax", "exp"])
 def test_decode_kernel_matches_oracle_and_generic(S, K, route):
     """Decode steps through the matrix-core kernel and the generic kernel: y
