@@ -201,14 +201,19 @@ size_t moc_backward_workspace_bytes(int64_t n_tokens, int64_t dim, int64_t k,
                                     int64_t kernel_size, int x_dtype, int routing) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
   // the activation is not an argument, and the kernel plan depends on it (bf16
-  // two-pass shapes: the taps pass's partials, and with SiLU the g buffer)
+  // two-pass shapes: the taps pass's partials, and with SiLU the g buffer);
+  // the same query serves moc_backward_prefill, whose plan keeps the fused
+  // pass at some shapes where the plain backward runs two (another grid, so
+  // other partial sizes): the larger of every plan
   size_t need = 0;
-  for (int act = 0; act <= 1; ++act) {
-    const moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size,
-                                        x_dtype, MOC_DT_F32, MOC_DT_F32, act, routing);
-    const size_t b = backward_bytes(p);
-    if (b > need) need = b;
-  }
+  for (int act = 0; act <= 1; ++act)
+    for (int pre = 0; pre <= 1; ++pre) {
+      moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size,
+                                    x_dtype, MOC_DT_F32, MOC_DT_F32, act, routing);
+      p.pre = pre != 0;
+      const size_t b = backward_bytes(p);
+      if (b > need) need = b;
+    }
   return need;
 }
 

@@ -5,6 +5,7 @@
 
 #include <atomic>
 
+#include "moc_bwd_lean.h"
 #include "moc_kernels.h"
 #include "moc_mfma.h"
 
@@ -28,6 +29,12 @@ constexpr int fwd_nb(int S) { return S == 8 ? MOC_FWD_NB8 : kFwdNB; }
 #define MOC_BWD_WPG 4
 #endif
 constexpr int kBwdNB = 2, kBwdNC = 2, kBwdWPG = MOC_BWD_WPG;
+static_assert(kLeanWPG * kLeanCW == 16 * kBwdNC * MOC_BWD_WPG,
+              "the lean backward covers the channel groups of the fused pass's grid");
+// the lean fused backward (moc_bwd_lean.h) for the shapes it serves; 0: bwd_tile's
+#ifndef MOC_BWD_LEAN
+#define MOC_BWD_LEAN 1
+#endif
 // Resident workgroups the grids are sized for (256 CUs).
 #ifndef MOC_FWD_TARGET_WG
 #define MOC_FWD_TARGET_WG 2048
@@ -262,6 +269,8 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
   constexpr bool kSplit = BF && KC >= 2;
   constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) || bwd_two_pass_g(S, KC, ACT, BF) ||
                         bwd_two_pass_r(S, KC, ACT, BF);
+  // the fused pass at four waves per SIMD (moc_bwd_lean.h) where it is built
+  constexpr bool kLean = MOC_BWD_LEAN && !kTwo && bwd_lean(S, KC, BF);
   // tiers for the fused pass at two resident workgroups per CU (not split in route chunks)
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, BF> == 2;
   const int64_t gx_all = cdiv(p.D, kBwdCW);
@@ -292,6 +301,13 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
                        tgrid, dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a, b, nullptr, part_da,
                        part_db, p.seq, p.D, static_cast<int>(gt.gx), static_cast<int>(gt.gy), gt.gy1,
                        gt.n_old, gt.n_total, gbuf);
+  } else if constexpr (kLean) {
+    // (the lean pass's workgroup covers the same kBwdCW channels with 8 waves)
+    // (one dy element for every token and channel: its own instantiation)
+    auto kern = p.dy_stride < 0 ? bwd_lean_kernel<S, ACT, true> : bwd_lean_kernel<S, ACT, false>;
+    hipLaunchKernelGGL(kern, dim3(g.gx, g.gy), dim3(64 * kLeanWPG), 0, st, x, dy, p.dy_stride,
+                       reinterpret_cast<const uint16_t*>(a), reinterpret_cast<const uint16_t*>(b), dx,
+                       part_da, part_db, p.seq, p.D, gy, g.gy1, g.n_old, g.n_total);
   } else {
     hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, BF, kSplit, kBwdFused>),
                        kSplit ? halves : dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a,
@@ -359,6 +375,17 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
                          dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
     hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, true, false, kBwdTaps>),
                        dim3(static_cast<unsigned>(blkt)), dim3(64 * kTapsWPG), 0, st, lt, p.seq);
+  } else if constexpr (MOC_BWD_LEAN && bwd_lean(S, KC, true)) {
+    // (layers whose dy is one element each, or none of them: one instantiation
+    // per form; mixed forms keep every layer's rows by the general one)
+    bool all_one = true;
+    for (int i = 0; i < n; ++i) all_one = all_one && L[i].dys < 0;
+    if (all_one)
+      hipLaunchKernelGGL((bwd_lean_layers_kernel<S, ACT, true>), dim3(static_cast<unsigned>(blk)),
+                         dim3(64 * kLeanWPG), 0, st, ly, p.seq);
+    else
+      hipLaunchKernelGGL((bwd_lean_layers_kernel<S, ACT, false>), dim3(static_cast<unsigned>(blk)),
+                         dim3(64 * kLeanWPG), 0, st, ly, p.seq);
   } else {
     hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, kSplit, kBwdFused>),
                        dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
