@@ -606,8 +606,10 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
   if (!force_generic && moc::decode_supported(batch, dim, k, kernel_size, x_dtype, alpha_dtype,
                                               basis_dtype, cache_stride_b, cache_stride_d,
                                               cache_stride_s)) {
-    moc::launch_decode(x, alpha, moc::route_form(routing), basis, cache, y, batch, dim, k, kernel_size, activation,
-                       static_cast<hipStream_t>(stream));
+    if (!moc::launch_decode(x, alpha, moc::route_form(routing), basis, cache, y, batch, dim, k,
+                            kernel_size, activation, static_cast<hipStream_t>(stream)))
+      return fail(MOC_ERR_ARG, "decode kernel not built for k %lld, kernel_size %lld", (long long)k,
+                  (long long)kernel_size);
     return hip_status("moc_update launch");
   }
   moc::launch_update_generic(x, alpha, basis, cache, cache_stride_b, cache_stride_d,
@@ -638,8 +640,10 @@ int moc_decode_step(const void* z, const void* router, const void* x, const void
                 (long long)batch, (long long)z_dim, (long long)dim, (long long)k,
                 (long long)kernel_size);
   if (!z || !router || !x || !basis || !cache || !y) return fail(MOC_ERR_ARG, "null tensor pointer");
-  moc::launch_decode_step(z, router, x, basis, cache, y, batch, z_dim, dim, k, kernel_size,
-                          activation, routing, static_cast<hipStream_t>(stream));
+  if (!moc::launch_decode_step(z, router, x, basis, cache, y, batch, z_dim, dim, k, kernel_size,
+                               activation, routing, static_cast<hipStream_t>(stream)))
+    return fail(MOC_ERR_ARG, "decode step kernel not built for k %lld, kernel_size %lld",
+                (long long)k, (long long)kernel_size);
   return hip_status("moc_decode_step launch");
 }
 

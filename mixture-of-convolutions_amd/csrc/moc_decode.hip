@@ -185,6 +185,24 @@ __global__ void __launch_bounds__(256) decode_kernel(
   // every load above is issued before the GEMV's products consume its loads
   __builtin_amdgcn_sched_barrier(0);
 
+  // the cache update needs no routing weights: the history shifted one slot and
+  // x appended go out as soon as the rows have landed, so that these 4 S bytes
+  // per channel and token are written while the GEMV, the softmax and the
+  // mixture run, not after them
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int r = 4 * qq + v;
+    CacheRow<S> nr;
+#pragma unroll
+    for (int c = 0; c < kNC; ++c) {
+#pragma unroll
+      for (int s = 0; s + 1 < S; ++s) nr.set(c, s, cr[v].get(c, s + 1));
+      nr.set(c, S - 1, static_cast<uint16_t>(xv[v] >> (16 * c)));
+    }
+    nr.store(cb, ch_ok ? static_cast<uint32_t>((r * D + dl) * S * 2) : kOffNone);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // routing weights in the A-operand layout, rounded as the forward path rounds
   // them (softmax / exp in fp32, then to bf16)
   float l[KC][4];
@@ -330,15 +348,6 @@ __global__ void __launch_bounds__(256) decode_kernel(
                         (static_cast<uint32_t>(f32_to_bf16(yo[1])) << 16);
     __builtin_amdgcn_raw_buffer_store_b32(
         yw, yb.r, static_cast<int>(ch_ok ? static_cast<uint32_t>((r * D + dl) * 2) : kOffNone), 0, 0);
-    // shift the history one slot left and append x
-    CacheRow<S> nr;
-#pragma unroll
-    for (int c = 0; c < kNC; ++c) {
-#pragma unroll
-      for (int s = 0; s + 1 < S; ++s) nr.set(c, s, cr[v].get(c, s + 1));
-      nr.set(c, S - 1, xo[c]);
-    }
-    nr.store(cb, ch_ok ? static_cast<uint32_t>((r * D + dl) * S * 2) : kOffNone);
   }
 }
 
@@ -357,7 +366,7 @@ void launch_one(const void* x, const void* alpha, int routing, const void* basis
 }
 
 template <int S, bool FUSED>
-void launch_s(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+bool launch_s(const void* x, const void* alpha, int routing, const void* basis, void* cache,
               void* y, int64_t B, int64_t D, int64_t K, int act, const void* z, const void* router,
               int64_t Z, hipStream_t st) {
   if (K <= 16) {
@@ -370,22 +379,27 @@ void launch_s(const void* x, const void* alpha, int routing, const void* basis, 
     // 33-64 routes: given logits / weights only (the fused router GEMV stops at 32)
     if (act) launch_one<S, 4, true, false>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
     else launch_one<S, 4, false, false>(x, alpha, routing, basis, cache, y, B, D, K, z, router, Z, st);
+  } else {
+    return false;  // the fused step is built for up to 32 routes
   }
+  return true;
 }
 
+// Returns false (nothing launched) for a shape the kernels are not built for;
+// decode_supported / decode_step_supported admit none of them.
 template <bool FUSED>
-void launch_any(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+bool launch_any(const void* x, const void* alpha, int routing, const void* basis, void* cache,
                 void* y, int64_t B, int64_t D, int64_t K, int64_t S, int act, const void* z,
                 const void* router, int64_t Z, hipStream_t st) {
   switch (S) {
-    case 2: launch_s<2, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 3: launch_s<3, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 4: launch_s<4, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 5: launch_s<5, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 6: launch_s<6, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 7: launch_s<7, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    case 8: launch_s<8, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st); break;
-    default: break;  // decode_supported admits 2-8 only
+    case 2: return launch_s<2, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 3: return launch_s<3, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 4: return launch_s<4, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 5: return launch_s<5, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 6: return launch_s<6, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 7: return launch_s<7, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    case 8: return launch_s<8, FUSED>(x, alpha, routing, basis, cache, y, B, D, K, act, z, router, Z, st);
+    default: return false;
   }
 }
 
@@ -401,10 +415,10 @@ bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int 
          B * K * 2 < lim && K * S * D * 2 < lim;
 }
 
-void launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+bool launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
                    void* y, int64_t B, int64_t D, int64_t K, int64_t S, int activation,
                    hipStream_t st) {
-  decode::launch_any<false>(x, alpha, routing, basis, cache, y, B, D, K, S, activation, nullptr,
+  return decode::launch_any<false>(x, alpha, routing, basis, cache, y, B, D, K, S, activation, nullptr,
                             nullptr, 0, st);
 }
 
@@ -414,10 +428,10 @@ bool decode_step_supported(int64_t B, int64_t D, int64_t Z, int64_t K, int64_t S
          Z % 64 == 0 && 16 * Z * 2 < lim && K * Z * 2 < lim;
 }
 
-void launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
+bool launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
                         void* cache, void* y, int64_t B, int64_t Z, int64_t D, int64_t K,
                         int64_t S, int activation, int routing, hipStream_t st) {
-  decode::launch_any<true>(x, nullptr, routing, basis, cache, y, B, D, K, S, activation, z, router,
+  return decode::launch_any<true>(x, nullptr, routing, basis, cache, y, B, D, K, S, activation, z, router,
                            Z, st);
 }
 

@@ -102,13 +102,15 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
 // D % 4 == 0
 bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                       int64_t cs_b, int64_t cs_d, int64_t cs_s);
-void launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
+// (false: nothing launched, a shape decode_supported does not admit)
+bool launch_decode(const void* x, const void* alpha, int routing, const void* basis, void* cache,
                    void* y, int64_t B, int64_t D, int64_t K, int64_t S, int activation,
                    hipStream_t st);
 
 // decode step with the router GEMM in the same kernel (moc_decode.hip)
 bool decode_step_supported(int64_t B, int64_t D, int64_t Z, int64_t K, int64_t S);
-void launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
+// (false: nothing launched, a shape decode_step_supported does not admit)
+bool launch_decode_step(const void* z, const void* router, const void* x, const void* basis,
                         void* cache, void* y, int64_t B, int64_t Z, int64_t D, int64_t K,
                         int64_t S, int activation, int routing, hipStream_t st);
 

@@ -70,11 +70,17 @@ def _check_layer(label, m, got, ref, dtype):
 
 
 def _hip_layer(m, x, z, dy, **kw):
+    """The layer's forward and backward on the HIP path; dy None: loss = y.sum()
+    (autograd hands the backward one element expanded over y, the form the
+    kernels read in place, row stride -1)."""
     m.zero_grad(set_to_none=True)
     x = x.detach().requires_grad_()
     z = z.detach().requires_grad_()
     y, _ = m(x, z, **kw)
-    y.backward(dy)
+    if dy is None:
+        y.sum().backward()
+    else:
+        y.backward(dy)
     return y.detach(), x.grad, z.grad, m.router.grad.clone(), m.conv_bases.grad.clone()
 
 
@@ -111,6 +117,9 @@ def test_config2_headline_layer():
     got = _hip_layer(m, x, z, dy)
     ref = _oracle_layer(m, x, z, dy, "softmax", "silu")
     _check_layer("", m, got, ref, torch.bfloat16)
+    # the same loss as y.sum(): the one-element gradient the bench's step runs
+    summed = _hip_layer(m, x, z, None)
+    _check_layer("(y.sum())", m, summed, ref, torch.bfloat16)
     other = _with_path("generic", lambda: _hip_layer(m, x, z, dy))
     _check_layer("(mfma vs generic)", m, got, other, torch.bfloat16)
 

@@ -276,3 +276,25 @@ def test_module_prefill_gradients(route):
     assert_close("drouter", m.router.grad, rr, bf)
     assert_close("dbasis", m.conv_bases.grad, rb.grad, bf)
     assert_close("dcache", c.grad, rc.grad, bf)
+
+
+@pytest.mark.parametrize("K,act", [(16, "silu"), (64, None)])
+def test_prefill_backward_multi_range_workspace(K, act):
+    """The prefill backward at a token count that spans many token ranges, at
+    shapes whose plain backward runs the two-pass form while the prefill keeps
+    the fused pass (8 taps: 16 routes with SiLU, 64 without activation), so the
+    two plans' partial grids differ: the workspace the size query returns
+    serves the prefill call, and the gradients match the oracle."""
+    B, T, D, S, dtype = 2, 4096, 128, 8, BF
+    x, a, b, c, dy = _inputs(K + S, B, T, D, K, S, dtype)
+    flag = 1 if act else 0
+    dx, da, db, dc = ops.launch_backward_prefill(x, a, b, c, dy, activation_flag=flag,
+                                                 need_x=True, need_cache=True)
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
+    rc = c.detach().float().cpu().requires_grad_()
+    ry = O.moc_prefill_ref(rx, ra, rb, rc, act)
+    ry.backward(dy.float().cpu())
+    assert_close("dx", dx, rx.grad, dtype)
+    assert_close("dalpha", da, ra.grad, dtype)
+    assert_close("dbasis", db, rb.grad, dtype)
+    assert_close("dcache", dc, rc.grad, dtype)
