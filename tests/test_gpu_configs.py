@@ -347,6 +347,27 @@ def test_fused_decode_step_matches_router_then_update(S, K, route, act):
     assert torch.equal(y1, y2)
 
 
+@pytest.mark.parametrize("S,K,act", [(8, 64, None), (8, 48, None), (4, 64, None)])
+def test_route_half_taps_pass_multi_range(S, K, act):
+    """The plain backward's taps pass in route halves (bf16, 64 routes without
+    activation) at a token count whose token ranges hold many super-blocks
+    each (the shape sweep above runs single super-block ranges): gradients
+    against the oracle."""
+    g = gen(S * 7 + K)
+    B, T, D = 2, 4096, 192
+    x = randn(g, B, T, D, scale=0.5).to(DEV, torch.bfloat16)
+    a = torch.softmax(randn(g, B, T, K), -1).to(DEV, torch.bfloat16)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, torch.bfloat16)
+    dy = randn(g, B, T, D).to(DEV, torch.bfloat16)
+    xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
+    y, _ = moc_triton(xx, aa, bb, activation=act)
+    y.backward(dy)
+    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), act)
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), (y, xx.grad, aa.grad, bb.grad), ref):
+        assert_close(n, u, r, torch.bfloat16)
+
+
 def alpha_pad(alpha, S):
     """Routing weights for the S history rows prepended to the steps (their
     outputs are dropped, so any weights do)."""
