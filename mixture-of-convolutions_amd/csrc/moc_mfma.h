@@ -1372,9 +1372,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                     if constexpr (HXW) {
                       if (use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
                     } else if constexpr (HX) {
-                      if (use_h && !on && tap_in(s))
-                        mval = g[r][c] * hist_at<S, E>(hb, trun - (S - 1) + s0 + r + s, T, N, D, dl,
-                                                       ch_ok, c);
+                      // every lane issues the cache load, with an out-of-range
+                      // offset (zero) where its tap does not reach before the
+                      // sequence, and selects: no divergent branch around a load
+                      const bool want = use_h && !on && tap_in(s);
+                      const float h = hist_at<S, E>(hb, trun - (S - 1) + s0 + r + s, T, N, D, dl,
+                                                    ch_ok && want, c);
+                      mval = want ? g[r][c] * h : mval;
                     }
                     hbits[v] = __float_as_uint(mval) & 0xffff0000u;
                     lo[v] = mval - __uint_as_float(hbits[v]);

@@ -198,11 +198,9 @@ inline bool bwd_two_pass_g(const Problem& p) {
 // 64 routes without activation: the two passes, the taps pass split in route
 // halves (two workgroups per tile, each forming the tile's m products for two of
 // the four route chunks; the fused pass forms them once per chunk).  Single and
-// prefill launches (not grouped); the prefill up to 7 taps: at 8 its taps pass
-// returned non-finite dalpha / dbasis in the second route half (cause not
-// found), so that shape keeps the fused pass.
+// prefill launches (not grouped), every kernel size.
 constexpr bool bwd_two_pass_r(int S, int KC, bool act, bool bf) { return bf && !act && KC == 4; }
-constexpr bool pre_two_pass_r(int S) { return S < 8; }
+constexpr bool pre_two_pass_r(int S) { return S >= 2; }
 inline bool bwd_two_pass(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
   const bool act = p.activation != 0, bf = p.x_dt == DT_BF16;
