@@ -203,9 +203,9 @@ bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t
   __syncthreads();
 
   StartCursor cursor;
-  // dalpha partials of this channel group: rows t, 16 routes (32-bit offsets:
-  // the entry points bound n_tokens below 2^24)
-  const Buf pdab(part_da + static_cast<int64_t>(bx) * N * KP, N * KP * 4);
+  // dalpha partials of this channel group from row `first` on (rows
+  // [first, row_hi), 16 routes; 32-bit offsets within the range)
+  const Buf pdab(part_da + (static_cast<int64_t>(bx) * N + first) * KP, (row_hi - first) * KP * 4);
   for (int sb = 0; sb < nsb; ++sb) {
     const int64_t t0 = first + static_cast<int64_t>(sb) * EOWN;
     if (t0 >= N) break;  // uniform over the workgroup
@@ -442,7 +442,7 @@ bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t
 #pragma unroll
       for (int w = 0; w < WPG; ++w) sum += tv[w];
       const int n_own = static_cast<int>(own_end - t0);
-      const uint32_t off = static_cast<uint32_t>(((t0 + 16 * r2 + row) * KP + c) * 4);
+      const uint32_t off = static_cast<uint32_t>(((t0 - first + 16 * r2 + row) * KP + c) * 4);
       pdab.store<4>(16 * r2 + row < n_own ? off : kOffNone, &sum);
     }
   }

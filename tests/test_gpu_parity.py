@@ -625,3 +625,34 @@ def test_kernels_match_golden(dtype):
         y.backward(dy)
         for key, got in (("y", y), ("dx", x.grad), ("dalpha", al.grad), ("dbasis", b.grad)):
             assert_close(f"{name} {key}", got, torch.from_numpy(a[key]), dtype)
+
+
+def test_longest_token_axis_ends_match_oracle():
+    """The longest token axis the backward entry accepts (65535 * 256 tokens;
+    D 64, K 16, S 4, SiLU, bf16, loss y.sum()).  Every output of a token
+    depends only on the S-1 tokens before it and the S-1 after it, so the first
+    and last 1024 tokens are checked against the oracle run on those windows
+    (the last one with its S-1 rows of history); dbasis, a sum over the whole
+    axis, is checked to be finite."""
+    S, Kr, Dl = 4, 16, 64
+    N = 65535 * 256
+    gd = torch.Generator(device=DEV).manual_seed(5)
+    x = (torch.randn(1, N, Dl, generator=gd, device=DEV) * 0.5).to(torch.bfloat16).requires_grad_()
+    a = torch.softmax(torch.randn(1, N, Kr, generator=gd, device=DEV), -1).to(torch.bfloat16)
+    a.requires_grad_()
+    b = (torch.randn(Kr, S, Dl, generator=gd, device=DEV) * 0.2).to(torch.bfloat16).requires_grad_()
+    y, _ = moc_triton(x, a, b, activation="silu")
+    y.sum().backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(b.grad.float()).all()
+    L, H = 1024, S - 1
+    for lo, keep in ((0, 0), (N - L - H, H)):
+        hi = min(lo + L + H, N)
+        rx, ra, rb = O.reference_inputs(x[:, lo:hi], a[:, lo:hi], b, torch.bfloat16)
+        dy = torch.ones(1, hi - lo, Dl)
+        ry, rdx, rda, _ = O.moc_grads_ref(rx, ra, rb, dy, "silu")
+        rows = slice(keep, keep + L)
+        sl = slice(lo + keep, lo + keep + L)
+        assert_close(f"y[{lo}]", y[:, sl], ry[:, rows], torch.bfloat16)
+        assert_close(f"dx[{lo}]", x.grad[:, sl], rdx[:, rows], torch.bfloat16)
+        assert_close(f"dalpha[{lo}]", a.grad[:, sl], rda[:, rows], torch.bfloat16)
