@@ -44,11 +44,11 @@ METRIC = "fwd+bwd Mtok/s + roofline % (B4 T4096 D2048 K16 S4 bf16); decode us/st
 HBM_PEAK = 8.0e12          # bytes/s, MI355X HBM3E
 CFG = dict(B=4, T=4096, D=2048, Z=2048, K=16, S=4)
 # HBM bytes per launch of the backward stage-1 kernel at CFG: rocprofv3
-# FETCH_SIZE (68681 KiB) and WRITE_SIZE (98388 KiB) per dispatch of
+# FETCH_SIZE (69220 KiB) and WRITE_SIZE (99410 KiB) per dispatch of
 # `bench.py --counters bwd`, each scaled by what the counter reads for a copy of
 # 128 MiB (`--counters copy`: FETCH_SIZE 65548 KiB -> factor 2.0, WRITE_SIZE
 # 131072 KiB -> factor 1.0); profiles/traffic_fwd_bwd_config2.md
-TRAFFIC_BWD = 241_408_000
+TRAFFIC_BWD = 243_558_400
 # input sets the timed loops cycle through: 3 x (x, z) = 402 MB at CFG, more
 # than the 256 MB last-level cache, so each step reads its inputs from HBM
 ROTATE = 3
@@ -651,7 +651,7 @@ def main():
         "config": {"workload": "MoC layer fwd+bwd, BASELINE configs[1]", "B": CFG["B"],
                    "T": CFG["T"], "D": D, "z_dim": CFG["Z"], "K": K, "S": S,
                    "activation": "silu", "routing": "softmax", "loss": "y.sum()"},
-        "roofline": {"bound": "hbm", "kernel": "moc::mfma::bwd_kernel (fused backward stage 1)",
+        "roofline": {"bound": "hbm", "kernel": "moc::mfma::bwd_lean_kernel (fused backward stage 1)",
                      "achieved": round(achieved / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK, 4),
                      "traffic": TRAFFIC_BWD, "algorithmic_bytes": kb,
