@@ -723,7 +723,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 // workgroup barrier per super-block.  Super-block i covers rows [t0, t0 + TB)
 // with t0 = i * EOWN, EOWN = TB - (S-1): its first EOWN rows are its own, the
 // last S-1 rows only provide the later g / W the own rows' dx needs (they are
-// recomputed as own rows of block i+1).  Per super-block and lane:
+// recomputed as own rows of block i+1).  The taps pass forms no dx: an m
+// product needs dy (or g) of its own row and earlier x rows only, so there
+// EOWN = TB and every row of a super-block is its own.  Per super-block and lane:
 //   P (SiLU only) from MFMA W and the register window; g = dy * silu'(P);
 //   dx[u] = sum_s g[u+S-1-s] W_s[u+S-1-s]: W at the later token from an MFMA on
 //     alpha rows shifted by S-1-s, g of the next lane group's first S-1 rows by
@@ -808,7 +810,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(!SPLIT || KC % 2 == 0, "the route split takes an even number of route chunks");
   static_assert(!(SPLIT && MODE == kBwdTaps) || KC == 4, "the taps pass splits 64 routes in halves");
   const int kc0 = SPLIT ? zh * KX : 0;
-  constexpr int EOWN = TB - (S - 1);
+  constexpr int EOWN = MODE == kBwdTaps ? TB : TB - (S - 1);
   constexpr int NP = MS::kParts;
   constexpr int AROWS = TB + S - 1;   // alpha rows a super-block touches
   constexpr int MROW = CW + 4;        // padded LDS row of one m tile (elements)

@@ -97,9 +97,14 @@ inline Grid2 fwd_grid(int64_t N, int64_t D, int64_t S) { return fwd_grid_gx(N, c
 
 // Backward grid over gx channel groups; D is the widest layer's channel count
 // (it bounds the token range of a workgroup's buffers).
+// Own rows per super-block: the fused and dx passes recompute the last S-1 rows
+// of each super-block in the next one (their dx needs later rows' g); the taps
+// pass owns all of them.
+inline int64_t bwd_eown(int64_t S, bool taps = false) { return taps ? 16 * kBwdNB : 16 * kBwdNB - (S - 1); }
+
 inline Grid2 bwd_grid_gx(int64_t N, int64_t gx, int64_t D, int64_t S,
-                         int64_t target_wg = kBwdTargetWG) {
-  const int64_t eown = 16 * kBwdNB - (S - 1);
+                         int64_t target_wg = kBwdTargetWG, bool taps = false) {
+  const int64_t eown = bwd_eown(S, taps);
   const int64_t n_super = cdiv(N, eown);
   int64_t gy_target = target_wg / gx;
   if (gy_target < 1) gy_target = 1;
@@ -155,7 +160,7 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_
   const int64_t gy1 = n_cu / static_cast<int64_t>(g.gx);
   const int64_t gy = g.gy;
   if (gy != 2 * gy1) return g;
-  const int64_t eown = 16 * kBwdNB - (S - 1);
+  const int64_t eown = bwd_eown(S);
   const int64_t n_super = cdiv(N, eown);
   const int64_t max_sb = ((int64_t(1) << 30) / (D * 4) - 16 * kBwdNB) / eown;
   const int64_t n_old = (n_super * kBwdOldShare + 50) / 100;
@@ -216,7 +221,7 @@ constexpr int taps_route_parts(int KC) { return KC == 4 ? 2 : 1; }
 // rounds measured slower: each round pays a prologue of about 6 us, and the
 // second round's workgroups started 15-20 us after the first round's ended.
 inline Grid2 bwd_taps_grid(int64_t N, int64_t gx, int64_t D, int64_t S, int n_cu) {
-  return bwd_grid_gx(N, gx, D, S, n_cu > 0 ? int64_t(n_cu) * kTapsPerCU : kBwdTargetWG / 2);
+  return bwd_grid_gx(N, gx, D, S, n_cu > 0 ? int64_t(n_cu) * kTapsPerCU : kBwdTargetWG / 2, true);
 }
 
 // The grid whose workgroups own the dalpha / dbasis partials (workspace,

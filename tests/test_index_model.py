@@ -28,8 +28,14 @@ def cdiv(a, b):
 # ---------------------------------------------------------------------------
 # grids (csrc/moc_mfma_launch.h)
 
-def bwd_grid_gx(N, gx, D, S, target):
-    eown = 32 - (S - 1)
+def bwd_eown(S, taps=False):
+    """Own rows per 32-row super-block: all of them in the taps pass, the first
+    32 - (S-1) elsewhere."""
+    return 32 if taps else 32 - (S - 1)
+
+
+def bwd_grid_gx(N, gx, D, S, target, taps=False):
+    eown = bwd_eown(S, taps)
     n_super = cdiv(N, eown)
     gy_target = max(target // gx, 1)
     n_sb = cdiv(n_super, gy_target)
@@ -227,10 +233,10 @@ def coverage(N, D, S, KC, mode, SPLIT, n_cu=256):
     """Writes of part_da [gx][N][KP] and part_db [gy][KP][S][D] over the grid
     the launch uses; each entry stage 2 reads must be written exactly once."""
     KP = 16 * KC
-    eown = 32 - (S - 1)
+    eown = bwd_eown(S, mode == "taps")
     if mode == "taps":
         nz = 2 if SPLIT else 1
-        g = bwd_grid_gx(N, cdiv(D, 128), D, S, (n_cu // nz) * 1)
+        g = bwd_grid_gx(N, cdiv(D, 128), D, S, (n_cu // nz) * 1, taps=True)
         WCH, ST, KX = 4, (S + 1) // 2, (2 if SPLIT else KC)
     else:
         nz = KC if SPLIT else 1
