@@ -92,3 +92,38 @@ def test_noalloc_rejects_a_problem_beyond_its_scratch():
     rc = L.moc_backward_noalloc(p, p, p, p, D, p, p, p, None, 0, 0, N, 4096, D, 16, 4, 1, 1, 1, 1,
                                 3, _lib.stream_ptr(torch.device(DEV)))
     assert rc == -3 and b"moc_backward_noalloc holds" in L.moc_last_error()
+
+
+def test_noalloc_backward_replays_in_a_captured_graph():
+    """The caller the no-allocation entry is for: a HIP graph.  One eager call
+    first (the library resolves its scratch address on a device's first call),
+    then the call captured on a side stream and the graph replayed three times,
+    with new dy values written eagerly between replays; every replay must equal
+    the eager moc_backward on the same inputs bit for bit."""
+    L = _lib.lib()
+    T1 = 1024
+    x, a, b, dy = _inputs(4, 2 * T1, 512, 16, 4, torch.bfloat16, True)
+    dt = _lib.dtype_code(x.dtype)
+    N, D, K, S = x.shape[0], b.shape[2], b.shape[0], b.shape[1]
+    _call(True, x, a, b, dy, D, 1, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=T1)
+    dx = torch.empty_like(x)
+    da = torch.empty_like(a)
+    db = torch.empty_like(b)
+    head = (x.data_ptr(), a.data_ptr(), b.data_ptr(), dy.data_ptr(), D, dx.data_ptr(), da.data_ptr(),
+            db.data_ptr(), None, 0, 0, N, T1, D, K, S, dt, dt, dt, 1, _lib.ROUTE_SOFTMAX_WEIGHTS)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=side):
+        rc = L.moc_backward_noalloc(*head, _lib.stream_ptr(torch.device(DEV)))
+    _lib.check(rc, "moc_backward_noalloc (captured)")
+    g = gen(40)
+    for rep in range(3):
+        dy.copy_(randn(g, N, D).to(DEV, dy.dtype))
+        for t in (dx, da, db):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _call(False, x, a, b, dy, D, 1, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=T1)
+        _same(f"replay {rep}", (dx, da, db), ref)
