@@ -826,6 +826,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(!PRE || MODE != kBwdDx || ACT,
                 "without the activation the prefill dx pass is the plain one (it reads no cache)");
   constexpr int ST = MODE == kBwdTaps ? (S + 1) / 2 : S;
+  constexpr bool kOneBody = MODE == kBwdTaps && BF;
   // kBwdTaps: waves w and w + WPG/2 cover the same channels, taps [0, ST) and
   // [ST, S): x and dy rows are read once per workgroup and the dalpha sum over
   // the workgroup's waves covers every tap (one partial per channel group).  With
@@ -1153,7 +1154,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       // (the later rows only for dx)
       constexpr int NOK = DO_DX ? R + S - 1 : R;
       uint32_t ok[NOK];
-      if (MASK) {
+      if (MASK && (!kOneBody || !interior)) {
         tap_bits_rows<S, NOK>(seq, trun, w_lo, w_hi, ok);
       } else {
 #pragma unroll
@@ -1167,7 +1168,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       float hx[HXW ? W : 1][NC];
       bool use_h = false;
       if constexpr (HX) {
-        use_h = pre.hist != nullptr;
+        use_h = pre.hist != nullptr && (!kOneBody || !interior);
         if constexpr (HXW)
           if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
       }
@@ -1356,6 +1357,10 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
               for (int b2 = 0; b2 < NB; b2 += 2) {
                 Op mh[2], ml[2];
+                // M: masked products (MASK, and with one body a super-block
+                // that holds a sequence start)
+                auto form = [&](auto mtag) {
+                constexpr bool M = MASK && decltype(mtag)::value;
 #pragma unroll
                 for (int bb = 0; bb < 2; ++bb) {
                   const int b = b2 + bb;
@@ -1366,14 +1371,14 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                   for (int v = 0; v < 4; ++v) {
                     const int r = 4 * b + v;
                     // (the mask has no bit for a tap past S)
-                    const bool on = !MASK ? tap_in(s) : static_cast<bool>((ok[r] >> (s0 + s)) & 1u);
+                    const bool on = !M ? tap_in(s) : static_cast<bool>((ok[r] >> (s0 + s)) & 1u);
                     float xv;
                     if constexpr (kXOnUse) xv = C::to_f(xr[r + s][c]);
                     else xv = xw[r + s][c];
                     float mval = on ? g[r][c] * xv : 0.f;
-                    if constexpr (HXW) {
+                    if constexpr (HXW && M) {
                       if (use_h && !on) mval = g[r][c] * hx[HXW ? r + s : 0][c];
-                    } else if constexpr (HX) {
+                    } else if constexpr (HX && M) {
                       // every lane issues the cache load, with an out-of-range
                       // offset (zero) where its tap does not reach before the
                       // sequence, and selects: no divergent branch around a load
@@ -1389,6 +1394,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
                   ml[bb] = pack4_bf16(lo[0], lo[1], lo[2], lo[3]);
                   m_tr[wave][0][TT::wslot(j, q, b, c)] = mh[bb];
                   m_tr[wave][1][TT::wslot(j, q, b, c)] = ml[bb];
+                }
+                };
+                if constexpr (kOneBody) {
+                  if (interior) form(std::false_type{});
+                  else form(std::true_type{});
+                } else {
+                  form(std::true_type{});
                 }
 #pragma unroll
                 for (int kx = 0; kx < KX; ++kx) {
@@ -1495,7 +1507,12 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
         }
       }
     };
-    if (interior) body(std::false_type{});
+    // the bf16 taps pass runs one body, choosing masked or plain m products
+    // inside it (a uniform branch per product group): with a body per form,
+    // the dbasis accumulators met at the join in different registers and the
+    // loop copied all of them twice per super-block (128 moves at 8 taps)
+    if constexpr (kOneBody) body(std::true_type{});
+    else if (interior) body(std::false_type{});
     else body(std::true_type{});
     if constexpr (MODE == kBwdTaps) {
       if (more) fetch_xdy(t0 + EOWN);
