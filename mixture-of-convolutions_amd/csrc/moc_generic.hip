@@ -300,6 +300,184 @@ update_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_
 }
 
 // ---------------------------------------------------------------------------
+// Decode step for the shapes the matrix-core decode kernel does not take (fp32
+// or fp16 data, mixed storage dtypes, strided caches, any D), 2 to 8 taps and
+// up to 64 routes; same arithmetic and order as update_kernel, so the two give
+// the same bits.  A block covers 16 tokens x 64 channels: the 16 tokens'
+// routing weights are formed once per block in LDS (thread t < 16: token t),
+// and each thread takes one channel of 4 tokens, loading each basis value once
+// for the 4 and issuing a tap's loads together (update_kernel waits for one
+// load per routing weight and tap).
+constexpr int kTileMaxK = 64;
+
+// Typed element loads for the tile kernel: the storage dtype is chosen once per
+// loop (a uniform branch around it), so a loop's loads issue back to back.
+struct BF16Tag {};
+__device__ __forceinline__ float ld(const void* p, int64_t i, float) { return static_cast<const float*>(p)[i]; }
+__device__ __forceinline__ float ld(const void* p, int64_t i, BF16Tag) {
+  return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+__device__ __forceinline__ float ld(const void* p, int64_t i, _Float16) {
+  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+}
+template <typename F>
+__device__ __forceinline__ void with_dtype(int dt, F&& f) {
+  if (dt == DT_F32) f(float{});
+  else if (dt == DT_BF16) f(BF16Tag{});
+  else f(_Float16{});
+}
+
+template <int S>
+__global__ void __launch_bounds__(256)
+update_tile_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_dt, int routing,
+                   const void* __restrict__ basis, int b_dt, void* __restrict__ cache, int64_t cs_b,
+                   int64_t cs_d, int64_t cs_s, void* __restrict__ y, int x_dt, int64_t B, int64_t D,
+                   int K, int activation) {
+  // basis values of the first KT routes x S taps are loaded with everything
+  // else before the routing weights are formed (one memory round trip for all
+  // of them); further routes in chunks of KT
+  constexpr int KT = S <= 4 ? 16 : 8;
+  __shared__ float l_s[16][kTileMaxK + 1];
+  __shared__ float a_s[16][kTileMaxK];
+  const int tid = threadIdx.x;
+  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 16;
+  const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + (tid & 63);
+  const bool d_ok = d < D;
+  // loads are issued by every lane at a valid index (element 0 where the lane
+  // has nothing to load) and their values selected: a load under a per-lane
+  // condition compiles to a divergent branch that waits for it
+  const int64_t dc = d_ok ? d : 0;
+  const int tg = tid >> 6;  // this thread's tokens b0 + 4 tg + u, u < 4
+  int64_t bt[4];
+  bool on[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    bt[u] = b0 + 4 * tg + u;
+    on[u] = d_ok && bt[u] < B;
+  }
+  char* cb = static_cast<char*>(cache);
+
+  // 1. every load that does not depend on the routing weights
+  // the 16 tokens' logits (or weights): token tid / 16, entries tid % 16 + 16 i
+  float lr[kTileMaxK / 16];
+  {
+    const int tk = tid >> 4, k0 = tid & 15;
+    const bool tok = b0 + tk < B;
+    with_dtype(a_dt, [&](auto t) {
+#pragma unroll
+      for (int i = 0; i < kTileMaxK / 16; ++i) {
+        const int k = k0 + 16 * i;
+        const bool in = tok && k < K;
+        const float v = ld(alpha, in ? (b0 + tk) * K + k : 0, t);
+        lr[i] = in ? v : 0.f;
+      }
+    });
+  }
+  // x and the cache slots the output reads (slots 1 .. S-1 of each token's row),
+  // as raw bits (the shift below moves them unchanged)
+  uint32_t xr[4], hr[4][S];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t xi = on[u] ? bt[u] * D + d : 0, ci = on[u] ? bt[u] * cs_b + d * cs_d : 0;
+    const int64_t cs = on[u] ? cs_s : 0;
+    if (x_dt == DT_F32) {
+      xr[u] = static_cast<const uint32_t*>(x)[xi];
+#pragma unroll
+      for (int s = 1; s < S; ++s) hr[u][s] = reinterpret_cast<const uint32_t*>(cb)[ci + s * cs];
+    } else {
+      xr[u] = static_cast<const uint16_t*>(x)[xi];
+#pragma unroll
+      for (int s = 1; s < S; ++s) hr[u][s] = reinterpret_cast<const uint16_t*>(cb)[ci + s * cs];
+    }
+  }
+  // basis[k][s][d] of the first KT routes
+  float bv[KT][S];
+  auto load_basis = [&](int k0) {
+    with_dtype(b_dt, [&](auto t) {
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+        {
+          const bool in = k0 + kk < K;
+          const float v = ld(basis, (static_cast<int64_t>(in ? k0 + kk : 0) * S + s) * D + dc, t);
+          bv[kk][s] = in ? v : 0.f;
+        }
+    });
+  };
+  load_basis(0);
+
+  // 2. routing weights in update_kernel's order and rounding (thread t < 16: token t)
+  {
+    const int tk = tid >> 4, k0 = tid & 15;
+#pragma unroll
+    for (int i = 0; i < kTileMaxK / 16; ++i) l_s[tk][k0 + 16 * i] = lr[i];
+  }
+  __syncthreads();
+  if (tid < 16 && b0 + tid < B) {
+    float m = -INFINITY, sum = 0.f;
+    if (routing == ROUTE_SOFTMAX) {
+      for (int k = 0; k < K; ++k) m = fmaxf(m, l_s[tid][k]);
+      for (int k = 0; k < K; ++k) sum += __expf(l_s[tid][k] - m);
+    }
+    for (int k = 0; k < K; ++k) {
+      const float l = l_s[tid][k];
+      float a = l;
+      if (routing == ROUTE_SOFTMAX) a = round_to(__expf(l - m) * (1.0f / sum), a_dt);
+      else if (routing == ROUTE_EXP) a = round_to(__expf(l), a_dt);
+      a_s[tid][k] = round_to(a, x_dt);
+    }
+  }
+  __syncthreads();
+  if (!d_ok) return;  // (after the block's barriers)
+
+  // 3. W[u][s] = sum_k alpha[u][k] basis[k][s][d], k ascending
+  float w[4][S];
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+#pragma unroll
+    for (int s = 0; s < S; ++s) w[u][s] = 0.f;
+  for (int k0 = 0; k0 < K; k0 += KT) {
+    if (k0 > 0) load_basis(k0);
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      if (k0 + kk < K) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const float b = round_to(bv[kk][s], x_dt);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) w[u][s] = fmaf(a_s[4 * tg + u][k0 + kk], b, w[u][s]);
+        }
+      }
+    }
+  }
+  const bool f32 = x_dt == DT_F32;
+  auto to_f = [&](uint32_t r) { return f32 ? __uint_as_float(r) : bf16_to_f32(static_cast<uint16_t>(r)); };
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    if (!on[u]) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) v = fmaf(to_f(s == S - 1 ? xr[u] : hr[u][s + 1]), w[u][s], v);
+    if (activation) v = v * sigmoid_f(v);
+    store_any(y, x_dt, bt[u] * D + d, v);
+    // shift the history one slot left (pure copies: bit-exact), append x
+    const int64_t cbase = bt[u] * cs_b + d * cs_d;
+    if (f32) {
+      uint32_t* c = reinterpret_cast<uint32_t*>(cb);
+#pragma unroll
+      for (int s = 0; s + 1 < S; ++s) c[cbase + s * cs_s] = hr[u][s + 1];
+      c[cbase + (S - 1) * cs_s] = xr[u];
+    } else {
+      uint16_t* c = reinterpret_cast<uint16_t*>(cb);
+#pragma unroll
+      for (int s = 0; s + 1 < S; ++s) c[cbase + s * cs_s] = static_cast<uint16_t>(hr[u][s + 1]);
+      c[cbase + (S - 1) * cs_s] = static_cast<uint16_t>(xr[u]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers.
 
 static inline unsigned grid_for(int64_t total, int threads, int64_t cap = 65536) {
@@ -358,6 +536,26 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t cs_b, int64_t cs_d, int64_t cs_s, void* y, int64_t B,
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st) {
+  if (S >= 2 && S <= 8 && K <= kTileMaxK) {
+    const dim3 tgrid(static_cast<unsigned>((D + 63) / 64), static_cast<unsigned>((B + 15) / 16));
+    const int k = static_cast<int>(K), rf = route_form(routing);
+#define MOC_TILE(S_)                                                                                 \
+  case S_:                                                                                           \
+    hipLaunchKernelGGL(update_tile_kernel<S_>, tgrid, dim3(256), 0, st, x, alpha, a_dt, rf, basis, b_dt, \
+                       cache, cs_b, cs_d, cs_s, y, x_dt, B, D, k, activation);                       \
+    return;
+    switch (S) {
+      MOC_TILE(2)
+      MOC_TILE(3)
+      MOC_TILE(4)
+      MOC_TILE(5)
+      MOC_TILE(6)
+      MOC_TILE(7)
+      MOC_TILE(8)
+      default: break;
+    }
+#undef MOC_TILE
+  }
   dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(B));
   hipLaunchKernelGGL(update_kernel, grid, dim3(256), static_cast<size_t>(K) * sizeof(float), st,
                      x, alpha, a_dt, route_form(routing), basis, b_dt, cache, cs_b, cs_d, cs_s, y, x_dt, D, K,

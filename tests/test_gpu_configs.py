@@ -374,6 +374,54 @@ def alpha_pad(alpha, S):
     return torch.cat((torch.zeros_like(alpha[:, :1]).expand(-1, S, -1), alpha), 1)
 
 
+@pytest.mark.parametrize("xdt,adt,bdt,layout,S,K,route", [
+    (torch.float32, torch.float32, torch.float32, "contiguous", 4, 16, "softmax"),
+    (torch.float32, torch.bfloat16, torch.float32, "slot-major", 8, 32, "exp"),
+    (torch.float32, torch.float16, torch.float16, "contiguous", 3, 12, None),
+    (torch.bfloat16, torch.bfloat16, torch.float32, "slot-major", 5, 20, "softmax"),
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, "padded", 4, 64, "softmax"),
+    (torch.float32, torch.float32, torch.float32, "padded", 2, 7, "exp"),
+    (torch.float32, torch.float32, torch.float32, "contiguous", 9, 16, "softmax"),   # 9 taps, 80 routes:
+    (torch.float32, torch.float32, torch.float32, "slot-major", 4, 80, "exp"),       # the per-row kernel
+])
+def test_decode_other_dtypes_and_strided_caches(xdt, adt, bdt, layout, S, K, route):
+    """Decode steps (moc_update) on what the matrix-core decode kernel does not
+    take: fp32 data, mixed storage dtypes (fp16 / bf16 weights or basis), caches with any strides, a
+    channel count that is not a multiple of 4, up to 64 routes and 8 taps (the
+    tile kernel), and past them (the per-row kernel).  y against the oracle
+    step with the weights and basis rounded as the kernels round them; the
+    cache bit-exact."""
+    g = gen(S * 100 + K)
+    Bt, D, steps = 37, 198, 4                      # ragged batch, D % 4 == 2
+    x = randn(g, Bt, steps, D, scale=0.5).to(DEV, xdt)
+    lg = randn(g, Bt, steps, K).to(DEV, adt)
+    if route is None:
+        lg = torch.softmax(lg.float(), -1).to(adt)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, bdt)
+    start = randn(g, Bt, D, S).to(DEV, xdt)
+    if layout == "contiguous":
+        cache = start.clone()
+    elif layout == "slot-major":                   # [B, D, S] view of a [B, S, D] store
+        cache = start.transpose(1, 2).contiguous().transpose(1, 2)
+    else:                                          # a window of a larger buffer
+        big = torch.zeros(Bt, D + 8, S + 3, device=DEV, dtype=xdt)
+        cache = big[:, 4:4 + D, 1:1 + S]
+        cache.copy_(start)
+    code = _lib.ROUTE_ALPHA if route is None else moc.api._ROUTING_CODES[route]
+    ys = [moc.ops.launch_update(x[:, t], lg[:, t], b, cache, activation_flag=1, routing=code)[:, None]
+          for t in range(steps)]
+    y = torch.cat(ys, 1)
+    assert torch.equal(cache, torch.cat((start, x.transpose(1, 2)), -1)[..., -S:])
+    if layout == "padded":                         # nothing outside the window written
+        assert not big[:, :4].any() and not big[:, 4 + D:].any()
+        assert not big[..., :1].any() and not big[..., 1 + S:].any()
+    alpha = lg.float() if route is None else O.route(lg.float(), route, out_dtype=adt)
+    alpha = alpha.to(xdt).float()
+    ref = O.moc_ref(torch.cat((start.transpose(1, 2).float(), x.float()), 1).cpu(),
+                    alpha_pad(alpha, S).cpu(), b.to(xdt).float().cpu(), "silu")[:, S:]
+    assert_close("decode y", y, ref, xdt)
+
+
 def test_config4_decode():
     """configs[3] at its stated size: a batch-256 layer (D 2048, z_dim 2048, K16,
     S4, softmax, SiLU) prefilled from a 1024-token prompt, then 512 single-token
