@@ -5,8 +5,11 @@
 // instantiations (moc_mfma.hip) and the decode step.  They keep the reference's
 // semantics (moc/kernels.py:36-142 forward, 156-268 dx, 282-426 dalpha/dbasis,
 // 442-550 decode) but reduce dalpha / dbasis in a fixed order instead of atomics.
+#include <type_traits>
+
 #include "moc_common.h"
 #include "moc_kernels.h"
+#include "moc_mfma.h"
 
 namespace moc {
 
@@ -301,17 +304,27 @@ update_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_
 
 // ---------------------------------------------------------------------------
 // Decode step for the shapes the matrix-core decode kernel does not take (fp32
-// or fp16 data, mixed storage dtypes, strided caches, any D), 2 to 8 taps and
-// up to 64 routes; same arithmetic and order as update_kernel, so the two give
-// the same bits.  A block covers 16 tokens x 64 channels: the 16 tokens'
-// routing weights are formed once per block in LDS (thread t < 16: token t),
-// and each thread takes one channel of 4 tokens, loading each basis value once
-// for the 4 and issuing a tap's loads together (update_kernel waits for one
-// load per routing weight and tap).
-constexpr int kTileMaxK = 64;
+// data, mixed storage dtypes, strided caches, any D), 2 to 8 taps and up to 64
+// routes.  A workgroup covers 64 channels (one per lane) and 4 T tokens (T per
+// wave):
+//   * every load goes out first: the wave's logits, x, the cache slots and its
+//     quarter of the basis tile (KT routes x S taps x 64 channels), with
+//     clamped indices and selected values (a load under a per-lane condition
+//     compiles to a branch that waits for it);
+//   * the basis quarter goes to LDS (rounded to x's dtype once), and the
+//     shifted cache goes out (it needs no routing weights);
+//   * the routing weights are formed in the wave (lane: token lane / LPT,
+//     routes lane % LPT + LPT i; max and sum over the token's LPT lanes by
+//     shuffles) into the wave's LDS rows;
+//   * after the barrier, W[t][s] = sum_k alpha[t][k] basis[k][s][d] with k
+//     ascending, then y = act(sum_s h_s W_s) with s ascending, as update_kernel
+//     orders them.
+// ROW: the cache rows are contiguous (cache_stride_s == 1) and aligned to the
+// row's vector width, so each lane moves a token's S slots as whole words.
+constexpr int kDecMaxK = 64;
 
-// Typed element loads for the tile kernel: the storage dtype is chosen once per
-// loop (a uniform branch around it), so a loop's loads issue back to back.
+// Typed element loads: the storage dtype is chosen once per loop (a uniform
+// branch around it), so a loop's loads issue back to back.
 struct BF16Tag {};
 __device__ __forceinline__ float ld(const void* p, int64_t i, float) { return static_cast<const float*>(p)[i]; }
 __device__ __forceinline__ float ld(const void* p, int64_t i, BF16Tag) {
@@ -327,153 +340,264 @@ __device__ __forceinline__ void with_dtype(int dt, F&& f) {
   else f(_Float16{});
 }
 
-template <int S>
+// Bytes per access of a whole cache row of S slots of `esize` bytes: the
+// largest power of two dividing the row (at most 16); 0 when the row is not a
+// whole number of 4-byte words.
+__host__ __device__ constexpr int dec_row_vec_bytes(int S, int esize) {
+  return (S * esize) % 4 != 0 ? 0 : (S * esize) % 16 == 0 ? 16 : (S * esize) % 8 == 0 ? 8 : 4;
+}
+__host__ __device__ constexpr int dec_tokens_per_wave(int) { return 4; }
+
+template <int S, bool F32, bool ROW>
 __global__ void __launch_bounds__(256)
 update_tile_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_dt, int routing,
                    const void* __restrict__ basis, int b_dt, void* __restrict__ cache, int64_t cs_b,
-                   int64_t cs_d, int64_t cs_s, void* __restrict__ y, int x_dt, int64_t B, int64_t D,
-                   int K, int activation) {
-  // basis values of the first KT routes x S taps are loaded with everything
-  // else before the routing weights are formed (one memory round trip for all
-  // of them); further routes in chunks of KT
-  constexpr int KT = S <= 4 ? 16 : 8;
-  __shared__ float l_s[16][kTileMaxK + 1];
-  __shared__ float a_s[16][kTileMaxK];
-  const int tid = threadIdx.x;
-  const int64_t b0 = static_cast<int64_t>(blockIdx.y) * 16;
-  const int64_t d = static_cast<int64_t>(blockIdx.x) * 64 + (tid & 63);
-  const bool d_ok = d < D;
-  // loads are issued by every lane at a valid index (element 0 where the lane
-  // has nothing to load) and their values selected: a load under a per-lane
-  // condition compiles to a divergent branch that waits for it
-  const int64_t dc = d_ok ? d : 0;
-  const int tg = tid >> 6;  // this thread's tokens b0 + 4 tg + u, u < 4
-  int64_t bt[4];
-  bool on[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    bt[u] = b0 + 4 * tg + u;
-    on[u] = d_ok && bt[u] < B;
-  }
-  char* cb = static_cast<char*>(cache);
+                   int64_t cs_d, int64_t cs_s, void* __restrict__ y, int64_t B, int64_t D, int K,
+                   int activation) {
+  constexpr int T = dec_tokens_per_wave(S);
+  constexpr int LPT = 64 / T;             // lanes per token in the softmax
+  constexpr int NV = kDecMaxK / LPT;      // routing entries per lane
+  constexpr int KT = S <= 2 ? 32 : S <= 4 ? 16 : 8;  // routes per basis chunk
+  constexpr int R = KT * S;               // basis rows (route, tap) per chunk: 40 to 64
+  constexpr int RP = R + 4;               // padded LDS row of one channel (16-byte reads
+                                          // of 8 lanes fall in distinct banks)
+  constexpr int ES = F32 ? 4 : 2;         // element bytes of x, y and the cache
+  constexpr int x_dt = F32 ? DT_F32 : DT_BF16;
+  using E = std::conditional_t<F32, uint32_t, uint16_t>;
+  static_assert(R % 4 == 0 && R <= 64, "basis chunk: whole 16-byte groups, at most 64 rows");
+  __shared__ float a_s[4][T][kDecMaxK];   // each wave's routing weights
+  __shared__ __align__(16) float b_s[64][RP];  // basis chunk, [channel][k * S + s]
 
-  // 1. every load that does not depend on the routing weights
-  // the 16 tokens' logits (or weights): token tid / 16, entries tid % 16 + 16 i
-  float lr[kTileMaxK / 16];
-  {
-    const int tk = tid >> 4, k0 = tid & 15;
-    const bool tok = b0 + tk < B;
-    with_dtype(a_dt, [&](auto t) {
+  // (the wave index made scalar: addresses built on it stay in SGPRs)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int64_t d = d0 + lane;
+  const bool d_ok = d < D;
+  const int64_t dc = d_ok ? d : d0;
+  const int64_t tb = (static_cast<int64_t>(blockIdx.y) * 4 + wave) * T;
+  const int nt = static_cast<int>(B - tb < 0 ? 0 : (B - tb < T ? B - tb : T));  // tokens of this wave
+  auto tok = [&](int t) { return tb + t < B ? tb + t : B - 1; };  // a valid token for every t
+
+  // 1. loads: logits, x, cache slots, this wave's rows of the first basis chunk
+  float lg[NV];
+  const int tl = lane / LPT, kl = lane % LPT;
+  with_dtype(a_dt, [&](auto tag) {
 #pragma unroll
-      for (int i = 0; i < kTileMaxK / 16; ++i) {
-        const int k = k0 + 16 * i;
-        const bool in = tok && k < K;
-        const float v = ld(alpha, in ? (b0 + tk) * K + k : 0, t);
-        lr[i] = in ? v : 0.f;
+    for (int i = 0; i < NV; ++i) {
+      if (LPT * i >= K) {  // wave-uniform: no loads past the last route
+        lg[i] = 0.f;
+        continue;
       }
-    });
-  }
-  // x and the cache slots the output reads (slots 1 .. S-1 of each token's row),
-  // as raw bits (the shift below moves them unchanged)
-  uint32_t xr[4], hr[4][S];
+      const int k = kl + LPT * i;
+      const bool in = tl < nt && k < K;
+      lg[i] = ld(alpha, in ? (tb + tl) * K + k : 0, tag);
+    }
+  });
+  const E* xe = static_cast<const E*>(x);
+  E xr[T];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int64_t xi = on[u] ? bt[u] * D + d : 0, ci = on[u] ? bt[u] * cs_b + d * cs_d : 0;
-    const int64_t cs = on[u] ? cs_s : 0;
-    if (x_dt == DT_F32) {
-      xr[u] = static_cast<const uint32_t*>(x)[xi];
+  for (int t = 0; t < T; ++t) xr[t] = xe[tok(t) * D + dc];
+  char* cb = static_cast<char*>(cache);
+  constexpr int VB = dec_row_vec_bytes(S, ES);
+  constexpr int RW = ROW ? S * ES / 4 : 1;  // 32-bit words per row
+  uint32_t rw[T][RW];                        // ROW: whole rows
+  E he[T][S];                                // otherwise: slots 1 .. S-1
+  if constexpr (ROW) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-      for (int s = 1; s < S; ++s) hr[u][s] = reinterpret_cast<const uint32_t*>(cb)[ci + s * cs];
-    } else {
-      xr[u] = static_cast<const uint16_t*>(x)[xi];
+    for (int t = 0; t < T; ++t) {
+      const char* row = cb + (tok(t) * cs_b + dc * cs_d) * ES;
 #pragma unroll
-      for (int s = 1; s < S; ++s) hr[u][s] = reinterpret_cast<const uint16_t*>(cb)[ci + s * cs];
+      for (int v = 0; v < RW * 4 / VB; ++v) {
+        if constexpr (VB == 16) {
+          const u32x4 q = *reinterpret_cast<const u32x4*>(row + 16 * v);
+          __builtin_memcpy(&rw[t][4 * v], &q, 16);
+        } else if constexpr (VB == 8) {
+          const u32x2 q = *reinterpret_cast<const u32x2*>(row + 8 * v);
+          __builtin_memcpy(&rw[t][2 * v], &q, 8);
+        } else {
+          rw[t][v] = *reinterpret_cast<const uint32_t*>(row + 4 * v);
+        }
+      }
+    }
+  } else {
+    const E* ce = reinterpret_cast<const E*>(cb);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int64_t base = tok(t) * cs_b + dc * cs_d;
+#pragma unroll
+      for (int s = 1; s < S; ++s) he[t][s] = ce[base + s * cs_s];
     }
   }
-  // basis[k][s][d] of the first KT routes
-  float bv[KT][S];
+  // basis rows r = wave + 4 j of a chunk (route k0 + r / S, tap r % S), through
+  // a buffer resource based at the block's first channel: the row offset is
+  // block-uniform (a scalar offset), the lane's offset fixed; rounded to x's
+  // dtype, zero past route K
+  float bq[R / 4];
   auto load_basis = [&](int k0) {
-    with_dtype(b_dt, [&](auto t) {
+    with_dtype(b_dt, [&](auto tag) {
+      constexpr int BS = std::is_same_v<decltype(tag), float> ? 4 : 2;
+      const mfma::Buf bb(static_cast<const char*>(basis) + d0 * BS, (static_cast<int64_t>(K) * S * D - d0) * BS);
+      const int vo = static_cast<int>((dc - d0) * BS);
 #pragma unroll
-      for (int kk = 0; kk < KT; ++kk)
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-        {
-          const bool in = k0 + kk < K;
-          const float v = ld(basis, (static_cast<int64_t>(in ? k0 + kk : 0) * S + s) * D + dc, t);
-          bv[kk][s] = in ? v : 0.f;
+      for (int j = 0; j < R / 4; ++j) {
+        const int r = wave + 4 * j, k = k0 + r / S;
+        const bool in = k < K;
+        const int so = static_cast<int>((static_cast<int64_t>(in ? k : 0) * S + r % S) * D * BS);
+        float v;
+        if constexpr (BS == 4) {
+          v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(bb.r, vo, so, 0));
+        } else {
+          const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(bb.r, vo, so, 0);
+          if constexpr (std::is_same_v<decltype(tag), BF16Tag>) v = bf16_to_f32(h);
+          else v = static_cast<float>(__builtin_bit_cast(_Float16, h));
         }
+        bq[j] = in ? v : 0.f;
+      }
     });
+  };
+  auto stage_basis = [&]() {
+#pragma unroll
+    for (int j = 0; j < R / 4; ++j) b_s[lane][wave + 4 * j] = round_to(bq[j], x_dt);
   };
   load_basis(0);
 
-  // 2. routing weights in update_kernel's order and rounding (thread t < 16: token t)
-  {
-    const int tk = tid >> 4, k0 = tid & 15;
-#pragma unroll
-    for (int i = 0; i < kTileMaxK / 16; ++i) l_s[tk][k0 + 16 * i] = lr[i];
-  }
-  __syncthreads();
-  if (tid < 16 && b0 + tid < B) {
-    float m = -INFINITY, sum = 0.f;
-    if (routing == ROUTE_SOFTMAX) {
-      for (int k = 0; k < K; ++k) m = fmaxf(m, l_s[tid][k]);
-      for (int k = 0; k < K; ++k) sum += __expf(l_s[tid][k] - m);
+  // 2. the shifted cache (pure copies: bit-exact) with x appended
+  auto slot = [&](int t, int s) -> E {  // slot s >= 1 of token t's history
+    if constexpr (ROW) {
+      if constexpr (F32) return rw[t][s];
+      else return static_cast<E>(rw[t][s >> 1] >> (16 * (s & 1)));
+    } else {
+      return he[t][s];
     }
-    for (int k = 0; k < K; ++k) {
-      const float l = l_s[tid][k];
-      float a = l;
-      if (routing == ROUTE_SOFTMAX) a = round_to(__expf(l - m) * (1.0f / sum), a_dt);
-      else if (routing == ROUTE_EXP) a = round_to(__expf(l), a_dt);
-      a_s[tid][k] = round_to(a, x_dt);
-    }
-  }
-  __syncthreads();
-  if (!d_ok) return;  // (after the block's barriers)
-
-  // 3. W[u][s] = sum_k alpha[u][k] basis[k][s][d], k ascending
-  float w[4][S];
+  };
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int t = 0; t < T; ++t) {
+    if (t >= nt || !d_ok) continue;
+    if constexpr (ROW) {
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+      uint32_t nw[RW];
 #pragma unroll
-    for (int s = 0; s < S; ++s) w[u][s] = 0.f;
-  for (int k0 = 0; k0 < K; k0 += KT) {
-    if (k0 > 0) load_basis(k0);
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      if (k0 + kk < K) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const float b = round_to(bv[kk][s], x_dt);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) w[u][s] = fmaf(a_s[4 * tg + u][k0 + kk], b, w[u][s]);
+      for (int i = 0; i < RW; ++i) {
+        if constexpr (F32) {
+          nw[i] = i + 1 < RW ? rw[t][i + 1] : xr[t];
+        } else {
+          const uint32_t hi = i + 1 < RW ? rw[t][i + 1] : static_cast<uint32_t>(xr[t]);
+          nw[i] = (rw[t][i] >> 16) | (hi << 16);
         }
       }
+      char* row = cb + ((tb + t) * cs_b + d * cs_d) * ES;
+#pragma unroll
+      for (int v = 0; v < RW * 4 / VB; ++v) {
+        if constexpr (VB == 16) {
+          u32x4 q;
+          __builtin_memcpy(&q, &nw[4 * v], 16);
+          *reinterpret_cast<u32x4*>(row + 16 * v) = q;
+        } else if constexpr (VB == 8) {
+          u32x2 q;
+          __builtin_memcpy(&q, &nw[2 * v], 8);
+          *reinterpret_cast<u32x2*>(row + 8 * v) = q;
+        } else {
+          *reinterpret_cast<uint32_t*>(row + 4 * v) = nw[v];
+        }
+      }
+    } else {
+      E* ce = reinterpret_cast<E*>(cb);
+      const int64_t base = (tb + t) * cs_b + d * cs_d;
+#pragma unroll
+      for (int s = 0; s + 1 < S; ++s) ce[base + s * cs_s] = he[t][s + 1];
+      ce[base + (S - 1) * cs_s] = xr[t];
     }
   }
-  const bool f32 = x_dt == DT_F32;
-  auto to_f = [&](uint32_t r) { return f32 ? __uint_as_float(r) : bf16_to_f32(static_cast<uint16_t>(r)); };
+  stage_basis();
+
+  // 3. routing weights of token tl, routes kl + LPT i, rounded as update_kernel
+  //    rounds them (softmax / exp in fp32, to the logits dtype, to x's dtype)
+  {
+    float m = -INFINITY, sum = 0.f;
+    if (routing == ROUTE_SOFTMAX) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    if (!on[u]) continue;
+      for (int i = 0; i < NV; ++i)
+        if (kl + LPT * i < K) m = fmaxf(m, lg[i]);
+#pragma unroll
+      for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        lg[i] = kl + LPT * i < K ? __expf(lg[i] - m) : 0.f;
+        sum += lg[i];
+      }
+#pragma unroll
+      for (int o = 1; o < LPT; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    }
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = kl + LPT * i;
+      float a = lg[i];
+      if (routing == ROUTE_SOFTMAX) a = round_to(a * inv, a_dt);
+      else if (routing == ROUTE_EXP) a = round_to(__expf(a), a_dt);
+      a_s[wave][tl][k] = k < K ? round_to(a, x_dt) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  // 4. W, k ascending (routes past K have zero weight and zero basis values)
+  float w[T][S];
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int s = 0; s < S; ++s) w[t][s] = 0.f;
+  for (int k0 = 0; k0 < K; k0 += KT) {
+    if (k0 > 0) {  // the next chunk, once every wave has read this one
+      load_basis(k0);
+      __syncthreads();
+      stage_basis();
+      __syncthreads();
+    }
+    float bv[R];
+#pragma unroll
+    for (int q = 0; q < R / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(&b_s[lane][4 * q]);
+      bv[4 * q] = v.x;
+      bv[4 * q + 1] = v.y;
+      bv[4 * q + 2] = v.z;
+      bv[4 * q + 3] = v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float a[KT];
+#pragma unroll
+      for (int q = 0; q < KT / 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(&a_s[wave][t][k0 + 4 * q]);
+        a[4 * q] = v.x;
+        a[4 * q + 1] = v.y;
+        a[4 * q + 2] = v.z;
+        a[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+        for (int s = 0; s < S; ++s) w[t][s] = fmaf(a[kk], bv[kk * S + s], w[t][s]);
+    }
+  }
+
+  // 5. y = act(sum_{s < S-1} slot[s+1] W_s + x W_{S-1})
+  auto to_f = [](E r) {
+    if constexpr (F32) return __uint_as_float(r);
+    else return bf16_to_f32(r);
+  };
+  E* ye = static_cast<E*>(y);
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    if (t >= nt || !d_ok) continue;
     float v = 0.f;
 #pragma unroll
-    for (int s = 0; s < S; ++s) v = fmaf(to_f(s == S - 1 ? xr[u] : hr[u][s + 1]), w[u][s], v);
+    for (int s = 0; s < S; ++s) v = fmaf(to_f(s == S - 1 ? xr[t] : slot(t, s + 1)), w[t][s], v);
     if (activation) v = v * sigmoid_f(v);
-    store_any(y, x_dt, bt[u] * D + d, v);
-    // shift the history one slot left (pure copies: bit-exact), append x
-    const int64_t cbase = bt[u] * cs_b + d * cs_d;
-    if (f32) {
-      uint32_t* c = reinterpret_cast<uint32_t*>(cb);
-#pragma unroll
-      for (int s = 0; s + 1 < S; ++s) c[cbase + s * cs_s] = hr[u][s + 1];
-      c[cbase + (S - 1) * cs_s] = xr[u];
-    } else {
-      uint16_t* c = reinterpret_cast<uint16_t*>(cb);
-#pragma unroll
-      for (int s = 0; s + 1 < S; ++s) c[cbase + s * cs_s] = static_cast<uint16_t>(hr[u][s + 1]);
-      c[cbase + (S - 1) * cs_s] = static_cast<uint16_t>(xr[u]);
-    }
+    if constexpr (F32) ye[(tb + t) * D + d] = __float_as_uint(v);
+    else ye[(tb + t) * D + d] = f32_to_bf16(v);
   }
 }
 
@@ -536,25 +660,40 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t cs_b, int64_t cs_d, int64_t cs_s, void* y, int64_t B,
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st) {
-  if (S >= 2 && S <= 8 && K <= kTileMaxK) {
-    const dim3 tgrid(static_cast<unsigned>((D + 63) / 64), static_cast<unsigned>((B + 15) / 16));
+  // (the wave kernel addresses the basis with 32-bit byte offsets)
+  if (S >= 2 && S <= 8 && K <= kDecMaxK && K * S * D * 4 < (int64_t(1) << 31)) {
+    const int es = x_dt == DT_F32 ? 4 : 2;
+    const int vb = dec_row_vec_bytes(static_cast<int>(S), es);
+    const bool row = cs_s == 1 && vb > 0 && reinterpret_cast<uintptr_t>(cache) % vb == 0 &&
+                     (cs_d * es) % vb == 0 && (cs_b * es) % vb == 0;
+    const int tpw = 4 * dec_tokens_per_wave(static_cast<int>(S));
+    const dim3 wgrid(static_cast<unsigned>((D + 63) / 64), static_cast<unsigned>((B + tpw - 1) / tpw));
     const int k = static_cast<int>(K), rf = route_form(routing);
-#define MOC_TILE(S_)                                                                                 \
-  case S_:                                                                                           \
-    hipLaunchKernelGGL(update_tile_kernel<S_>, tgrid, dim3(256), 0, st, x, alpha, a_dt, rf, basis, b_dt, \
-                       cache, cs_b, cs_d, cs_s, y, x_dt, B, D, k, activation);                       \
+#define MOC_WAVE(S_, F32_, ROW_)                                                                   \
+  hipLaunchKernelGGL((update_tile_kernel<S_, F32_, ROW_>), wgrid, dim3(256), 0, st, x, alpha, a_dt, rf, \
+                     basis, b_dt, cache, cs_b, cs_d, cs_s, y, B, D, k, activation)
+#define MOC_WAVE_S(S_)                                                                             \
+  case S_:                                                                                         \
+    if (x_dt == DT_F32) {                                                                          \
+      if (row) MOC_WAVE(S_, true, true);                                                           \
+      else MOC_WAVE(S_, true, false);                                                              \
+    } else {                                                                                       \
+      if (row) MOC_WAVE(S_, false, (dec_row_vec_bytes(S_, 2) > 0));                                \
+      else MOC_WAVE(S_, false, false);                                                             \
+    }                                                                                              \
     return;
     switch (S) {
-      MOC_TILE(2)
-      MOC_TILE(3)
-      MOC_TILE(4)
-      MOC_TILE(5)
-      MOC_TILE(6)
-      MOC_TILE(7)
-      MOC_TILE(8)
+      MOC_WAVE_S(2)
+      MOC_WAVE_S(3)
+      MOC_WAVE_S(4)
+      MOC_WAVE_S(5)
+      MOC_WAVE_S(6)
+      MOC_WAVE_S(7)
+      MOC_WAVE_S(8)
       default: break;
     }
-#undef MOC_TILE
+#undef MOC_WAVE_S
+#undef MOC_WAVE
   }
   dim3 grid(static_cast<unsigned>((D + 255) / 256), static_cast<unsigned>(B));
   hipLaunchKernelGGL(update_kernel, grid, dim3(256), static_cast<size_t>(K) * sizeof(float), st,

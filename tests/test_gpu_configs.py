@@ -381,6 +381,11 @@ def alpha_pad(alpha, S):
     (torch.bfloat16, torch.bfloat16, torch.float32, "slot-major", 5, 20, "softmax"),
     (torch.bfloat16, torch.bfloat16, torch.bfloat16, "padded", 4, 64, "softmax"),
     (torch.float32, torch.float32, torch.float32, "padded", 2, 7, "exp"),
+    (torch.bfloat16, torch.bfloat16, torch.float32, "contiguous", 4, 16, "softmax"),
+    (torch.bfloat16, torch.float32, torch.bfloat16, "contiguous", 6, 24, "exp"),
+    (torch.float32, torch.float32, torch.float32, "contiguous", 8, 64, "softmax"),
+    (torch.float32, torch.bfloat16, torch.float32, "aligned-padded", 4, 40, "softmax"),
+    (torch.bfloat16, torch.bfloat16, torch.float32, "aligned-padded", 8, 16, None),
     (torch.float32, torch.float32, torch.float32, "contiguous", 9, 16, "softmax"),   # 9 taps, 80 routes:
     (torch.float32, torch.float32, torch.float32, "slot-major", 4, 80, "exp"),       # the per-row kernel
 ])
@@ -388,7 +393,8 @@ def test_decode_other_dtypes_and_strided_caches(xdt, adt, bdt, layout, S, K, rou
     """Decode steps (moc_update) on what the matrix-core decode kernel does not
     take: fp32 data, mixed storage dtypes (fp16 / bf16 weights or basis), caches with any strides, a
     channel count that is not a multiple of 4, up to 64 routes and 8 taps (the
-    tile kernel), and past them (the per-row kernel).  y against the oracle
+    tile kernel, with whole-row cache accesses where the rows are contiguous and
+    aligned and per-slot ones otherwise), and past them (the per-row kernel).  y against the oracle
     step with the weights and basis rounded as the kernels round them; the
     cache bit-exact."""
     g = gen(S * 100 + K)
@@ -403,9 +409,13 @@ def test_decode_other_dtypes_and_strided_caches(xdt, adt, bdt, layout, S, K, rou
         cache = start.clone()
     elif layout == "slot-major":                   # [B, D, S] view of a [B, S, D] store
         cache = start.transpose(1, 2).contiguous().transpose(1, 2)
-    else:                                          # a window of a larger buffer
+    elif layout == "padded":                       # a window of a larger buffer
         big = torch.zeros(Bt, D + 8, S + 3, device=DEV, dtype=xdt)
         cache = big[:, 4:4 + D, 1:1 + S]
+        cache.copy_(start)
+    else:                                          # padded rows that keep whole-row alignment
+        big = torch.zeros(Bt, D + 8, 2 * S, device=DEV, dtype=xdt)
+        cache = big[:, 4:4 + D, :S]
         cache.copy_(start)
     code = _lib.ROUTE_ALPHA if route is None else moc.api._ROUTING_CODES[route]
     ys = [moc.ops.launch_update(x[:, t], lg[:, t], b, cache, activation_flag=1, routing=code)[:, None]
@@ -415,6 +425,8 @@ def test_decode_other_dtypes_and_strided_caches(xdt, adt, bdt, layout, S, K, rou
     if layout == "padded":                         # nothing outside the window written
         assert not big[:, :4].any() and not big[:, 4 + D:].any()
         assert not big[..., :1].any() and not big[..., 1 + S:].any()
+    if layout == "aligned-padded":
+        assert not big[:, :4].any() and not big[:, 4 + D:].any() and not big[..., S:].any()
     alpha = lg.float() if route is None else O.route(lg.float(), route, out_dtype=adt)
     alpha = alpha.to(xdt).float()
     ref = O.moc_ref(torch.cat((start.transpose(1, 2).float(), x.float()), 1).cpu(),
