@@ -16,8 +16,10 @@ inputs already resident in HBM.  Printed as one JSON line:
   decode        configs[3]: batch-256 single-token steps: us per MoC.step call
                 (host-synchronised each step, and back to back), per MoC.step
                 replayed from a HIP graph, and per launch of the one-launch
-                decode step alone (graph-replayed); and the 512 steps as one
-                MoC.forward call from the prompt's cache (inputs known up front)
+                decode step alone (graph-replayed); the 512 steps as one
+                MoC.forward call from the prompt's cache (inputs known up front);
+                and (update_us) moc_update per launch in bf16 / fp32 with a
+                contiguous or slot-major cache (matrix-core and generic kernels)
   cpu_baseline  the CPU oracle on a bounded slice of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
@@ -292,6 +294,8 @@ def counter_run(dev, which, reps=3):
       fwd / bwd  one C-ABI entry at the headline config (entry_calls);
       step       the headline layer step (bench_layer's step, inputs rotated);
       decode     the one-launch decode step of configs[3] (batch 256);
+      update     moc_update at configs[3]'s layer shape in the four forms of
+                 update_calls (matrix-core and generic decode kernels);
       c3         the configs[2] varlen layer step (config3_step);
       c5         the configs[4] QKV triple step through MoCGroup;
       prefill    a headline-shape chunk continuing from a cache: the module
@@ -319,6 +323,12 @@ def counter_run(dev, which, reps=3):
             y.sum().backward()
     elif which == "decode":
         fn = decode_step_call(dev)
+    elif which == "update":
+        calls = [f for _, f in update_calls(dev)]
+
+        def fn():
+            for f in calls:
+                f()
     elif which == "prefill":
         fn = prefill_calls(dev, 1)
     elif which == "c3":
@@ -352,6 +362,57 @@ def decode_step_call(dev):
     basis, router = m.conv_bases.detach(), m.router.detach()
     return lambda: ops.launch_decode_step(xt, zt, router, basis, cache, activation_flag=1,
                                           routing=ROUTE_SOFTMAX)
+
+
+UPDATE_FORMS = (("bf16", "contiguous"), ("fp32", "contiguous"), ("bf16", "slot-major"),
+                ("fp32", "slot-major"))
+
+
+def update_calls(dev):
+    """moc_update (one decode step from given logits) at configs[3]'s layer
+    shape (batch 256, D 2048, K 16, S 4, softmax, SiLU) in four forms: bf16 with
+    a contiguous [B, D, S] cache (the matrix-core decode kernel), and fp32 data
+    or a slot-major cache ([B, D, S] view of a [B, S, D] store), which take the
+    generic tile kernel.  Returns [(label, fn)]."""
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX
+    c = DECODE
+    B, D, K, S = c["B"], c["D"], c["K"], c["S"]
+    calls = []
+    for dt_name, layout in UPDATE_FORMS:
+        dt = torch.bfloat16 if dt_name == "bf16" else torch.float32
+        g = torch.Generator().manual_seed(0)
+        x = torch.randn(B, D, generator=g).to(dev, dt)
+        lg = torch.randn(B, K, generator=g).to(dev, dt)
+        b = (torch.randn(K, S, D, generator=g) * 0.2).to(dev, dt)
+        cache = torch.randn(B, D, S, generator=g).to(dev, dt)
+        if layout == "slot-major":
+            cache = cache.transpose(1, 2).contiguous().transpose(1, 2)
+        calls.append((f"{dt_name} {layout}",
+                      lambda x=x, lg=lg, b=b, cache=cache: ops.launch_update(
+                          x, lg, b, cache, activation_flag=1, routing=ROUTE_SOFTMAX)))
+    return calls
+
+
+def bench_update(dev):
+    """us per moc_update launch in each form of update_calls, from a HIP graph
+    of 32 launches replayed 20 times (best of 3)."""
+    out = {}
+    for label, fn in update_calls(dev):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(32):
+                fn()
+        ms = min(time_region(graph.replay, 20, 3) for _ in range(3))
+        out[label] = round(ms * 1e3 / 32, 2)
+    return out
 
 
 def bench_decode(dev):
@@ -452,7 +513,8 @@ def bench_decode(dev):
                 steps_in_one_call_us_per_step=round(loop_ms * 1e3 / c["steps"], 3),
                 kernel_us=round(kernel_us, 3),
                 kernel_GBps=round(kbytes / (kernel_us * 1e-6) / 1e9, 1),
-                kernel_roofline_us=round(kbytes / HBM_PEAK * 1e6, 3))
+                kernel_roofline_us=round(kbytes / HBM_PEAK * 1e6, 3),
+                update_us=bench_update(dev))
 
 
 def cpu_baseline(seconds):
@@ -598,7 +660,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE,
                     help="input sets the timed loops cycle through (1: one set reused, "
                          "which the last-level cache partly holds across steps)")
-    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "c3", "c5", "prefill", "copy"),
+    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "update", "c3", "c5", "prefill",
+                                           "copy"),
                     default=None,
                     help="only run --reps calls of one workload (see counter_run) for a "
                          "rocprofv3 --pmc or --kernel-trace pass; prints no JSON")

@@ -311,11 +311,11 @@ update_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_
 //     quarter of the basis tile (KT routes x S taps x 64 channels), with
 //     clamped indices and selected values (a load under a per-lane condition
 //     compiles to a branch that waits for it);
-//   * the basis quarter goes to LDS (rounded to x's dtype once), and the
-//     shifted cache goes out (it needs no routing weights);
-//   * the routing weights are formed in the wave (lane: token lane / LPT,
-//     routes lane % LPT + LPT i; max and sum over the token's LPT lanes by
-//     shuffles) into the wave's LDS rows;
+//   * the routing weights are formed in the wave as soon as the logits have
+//     landed (lane: token lane / LPT, routes lane % LPT + LPT i; max and sum
+//     over the token's LPT lanes by shuffles) into the wave's LDS rows;
+//   * the shifted cache goes out (it needs no routing weights), and the basis
+//     quarter goes to LDS, rounded to x's dtype once;
 //   * after the barrier, W[t][s] = sum_k alpha[t][k] basis[k][s][d] with k
 //     ascending, then y = act(sum_s h_s W_s) with s ascending, as update_kernel
 //     orders them.
@@ -463,7 +463,36 @@ update_tile_kernel(const void* __restrict__ x, const void* __restrict__ alpha, i
   };
   load_basis(0);
 
-  // 2. the shifted cache (pure copies: bit-exact) with x appended
+  // 2. routing weights of token tl, routes kl + LPT i, rounded as update_kernel
+  //    rounds them (softmax / exp in fp32, to the logits dtype, to x's dtype);
+  //    first, as the logits were loaded first: it waits for them alone
+  {
+    float m = -INFINITY, sum = 0.f;
+    if (routing == ROUTE_SOFTMAX) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (kl + LPT * i < K) m = fmaxf(m, lg[i]);
+#pragma unroll
+      for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        lg[i] = kl + LPT * i < K ? __expf(lg[i] - m) : 0.f;
+        sum += lg[i];
+      }
+#pragma unroll
+      for (int o = 1; o < LPT; o <<= 1) sum += __shfl_xor(sum, o, 64);
+    }
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int k = kl + LPT * i;
+      float a = lg[i];
+      if (routing == ROUTE_SOFTMAX) a = round_to(a * inv, a_dt);
+      else if (routing == ROUTE_EXP) a = round_to(__expf(a), a_dt);
+      a_s[wave][tl][k] = k < K ? round_to(a, x_dt) : 0.f;
+    }
+  }
+  // 3. the shifted cache (pure copies: bit-exact) with x appended
   auto slot = [&](int t, int s) -> E {  // slot s >= 1 of token t's history
     if constexpr (ROW) {
       if constexpr (F32) return rw[t][s];
@@ -513,34 +542,6 @@ update_tile_kernel(const void* __restrict__ x, const void* __restrict__ alpha, i
   }
   stage_basis();
 
-  // 3. routing weights of token tl, routes kl + LPT i, rounded as update_kernel
-  //    rounds them (softmax / exp in fp32, to the logits dtype, to x's dtype)
-  {
-    float m = -INFINITY, sum = 0.f;
-    if (routing == ROUTE_SOFTMAX) {
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (kl + LPT * i < K) m = fmaxf(m, lg[i]);
-#pragma unroll
-      for (int o = 1; o < LPT; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        lg[i] = kl + LPT * i < K ? __expf(lg[i] - m) : 0.f;
-        sum += lg[i];
-      }
-#pragma unroll
-      for (int o = 1; o < LPT; o <<= 1) sum += __shfl_xor(sum, o, 64);
-    }
-    const float inv = 1.0f / sum;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int k = kl + LPT * i;
-      float a = lg[i];
-      if (routing == ROUTE_SOFTMAX) a = round_to(a * inv, a_dt);
-      else if (routing == ROUTE_EXP) a = round_to(__expf(a), a_dt);
-      a_s[wave][tl][k] = k < K ? round_to(a, x_dt) : 0.f;
-    }
-  }
   __syncthreads();
 
   // 4. W, k ascending (routes past K have zero weight and zero basis values)
