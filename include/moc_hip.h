@@ -80,6 +80,17 @@ const char* moc_last_error(void);
 int moc_set_kernel_path(int path);
 
 /*
+ * 1 when moc_forward / moc_backward run the matrix-core kernels for a problem
+ * of this shape and x dtype (under the current moc_set_kernel_path), 0 when
+ * they run the generic kernels.  No counterpart in the reference, whose Triton
+ * kernels take every shape; it lets a caller or a test see which family serves
+ * a shape.  Matrix-core shapes: 2 <= kernel_size <= 8; k <= 32 (k <= 64 with a
+ * bf16 x); dim even; x bf16 or f32.
+ */
+int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
+                              int x_dtype);
+
+/*
  * Sequence description shared by forward / backward:
  *   cu_seqlens == NULL: fixed length, n_tokens = B*T tokens, sequences of
  *                       seq_len = T tokens each ([B,T,D] viewed as [B*T,D]);
@@ -287,7 +298,7 @@ int moc_update(const void* x, const void* alpha, const void* basis, void* cache,
  * All tensors bf16; cache [batch, dim, kernel_size] contiguous, updated in place.
  *   z : [batch, z_dim], router : [k, z_dim], x, y : [batch, dim],
  *   basis : [k, kernel_size, dim]
- * Shapes: 2 <= kernel_size <= 8, k % 4 == 0, k <= 32, dim % 4 == 0,
+ * Shapes: 2 <= kernel_size <= 8, k % 4 == 0, k <= 32, dim even,
  * z_dim % 64 == 0 (moc_decode_step_supported returns 1 for such shapes).
  */
 int moc_decode_step_supported(int64_t batch, int64_t z_dim, int64_t dim, int64_t k,

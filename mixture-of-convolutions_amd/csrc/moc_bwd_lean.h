@@ -146,14 +146,21 @@ bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t
     for (int v = 0; v < 4; ++v) bb.load<ESZ>(row_off((4 * q + v) * S + s, 0, rb, col, ch_ok), &e[v]);
     bop[s] = CT<true>::make(e[0], e[1], e[2], e[3]);
   }
-  // dalpha B operands: bda[s] = basis[j, s, d0 + 4 q + {0..3}]
+  // dalpha B operands: bda[s] = basis[j, s, d0 + 4 q + {0..3}] (channels past D,
+  // with D % 4 == 2 the last two of the final group, zero: the load reaches into
+  // the next row)
   Op bda[S];
   {
     const int64_t ch = d0 + 4 * q;
     const bool on = wave_on && ch < D;
 #pragma unroll
-    for (int s = 0; s < S; ++s)
+    for (int s = 0; s < S; ++s) {
       bb.load<8>(row_off(j * S + s, 0, rb, static_cast<uint32_t>(ch * ESZ), on), &bda[s]);
+      if (ch + 2 >= D) {
+        bda[s][2] = 0;
+        bda[s][3] = 0;
+      }
+    }
   }
   f32x4 dbacc[S];
 #pragma unroll
@@ -447,12 +454,19 @@ bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t
     }
   }
 
-  // this workgroup's dbasis partial: dbacc[s][v] is (k = j, s, channel d0 + 4 q + v)
+  // this workgroup's dbasis partial: dbacc[s][v] is (k = j, s, channel d0 + 4 q + v);
+  // with D % 4 == 2 the rows are 8-byte aligned and the last group of 4 half past D
   if (wave_on && d0 + 4 * q < D) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       float* dst = part_db + ((static_cast<int64_t>(by) * KP + j) * S + s) * D + d0 + 4 * q;
-      *reinterpret_cast<f32x4*>(dst) = dbacc[s];
+      if (D % 4 == 0) {
+        *reinterpret_cast<f32x4*>(dst) = dbacc[s];
+      } else {
+        *reinterpret_cast<f32x2*>(dst) = f32x2{dbacc[s][0], dbacc[s][1]};
+        if (d0 + 4 * q + 2 < D) *reinterpret_cast<f32x2*>(dst + 2) = f32x2{dbacc[s][2], dbacc[s][3]};
+      }
     }
   }
 }

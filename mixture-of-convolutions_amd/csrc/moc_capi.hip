@@ -347,6 +347,15 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
 // ---------------------------------------------------------------------------
 // Prefill from a cache (fixed-length sequences, MFMA kernels).
 
+int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
+                              int x_dtype) {
+  if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
+  if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
+  moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
+                                MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
+  return use_mfma(p) ? 1 : 0;
+}
+
 int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,
                           int64_t kernel_size, int x_dtype, int with_cache) {
   if (n_seqs <= 0 || seq_len <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;

@@ -411,7 +411,7 @@ bool decode_supported(int64_t B, int64_t D, int64_t K, int64_t S, int x_dt, int 
   // buffers are addressed with 32-bit byte offsets
   const int64_t lim = int64_t(1) << 31;
   return x_dt == DT_BF16 && a_dt == DT_BF16 && b_dt == DT_BF16 && s_ok && K <= 64 && K % 4 == 0 &&
-         D % 4 == 0 && cs_s == 1 && cs_d == S && cs_b == D * S && 16 * D * S * 2 < lim &&
+         D % 2 == 0 && cs_s == 1 && cs_d == S && cs_b == D * S && 16 * D * S * 2 < lim &&
          B * K * 2 < lim && K * S * D * 2 < lim;
 }
 

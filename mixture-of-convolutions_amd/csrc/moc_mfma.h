@@ -960,6 +960,9 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     for (int s = 0; s < ST; ++s) {
 #pragma unroll
       for (int cg = 0; cg < NC; ++cg) {
+        // (with D % 4 == 2 the last group's upper two channels read the next
+        // row's first two: finite basis values that meet m products of zero, as
+        // a channel pair past D loads x and dy as zeros)
         const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
         bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s0 + s, 0, rb,

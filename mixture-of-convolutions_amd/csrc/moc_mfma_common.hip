@@ -396,8 +396,10 @@ void launch_stage2(const Problem& p, const Plan& pl, bool dir, char* ws, const v
 bool supported(const Problem& p) {
   const bool s_ok = p.S >= 2 && p.S <= 8;
   // the grids' y dimensions stay within the 65535 launch limit and one
-  // super-block's rows within a buffer's 32-bit range
-  return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && p.x_dt == DT_BF16)) && p.D % 4 == 0 && p.D <= (int64_t(1) << 20) &&
+  // super-block's rows within a buffer's 32-bit range; D even: a lane's two
+  // channels are both in or both past the channel axis, and its 2-channel
+  // accesses stay aligned (rows of D elements start at even elements)
+  return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && p.x_dt == DT_BF16)) && p.D % 2 == 0 && p.D <= (int64_t(1) << 20) &&
          (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
          bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D, p.S).gy <= 65535;
 }

@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "moc_abi_version",
     "moc_last_error",
     "moc_set_kernel_path",
+    "moc_matrix_core_supported",
     "moc_forward_workspace_bytes",
     "moc_forward",
     "moc_backward_workspace_bytes",
@@ -109,6 +110,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_backward.restype = _i
     lib.moc_backward_noalloc.argtypes = bwd + [_p]   # stream
     lib.moc_backward_noalloc.restype = _i
+    lib.moc_matrix_core_supported.argtypes = [_l, _l, _l, _l, _i]
+    lib.moc_matrix_core_supported.restype = _i
     lib.moc_prefill_supported.argtypes = [_l, _l, _l, _l, _l, _i, _i]
     lib.moc_prefill_supported.restype = _i
     lib.moc_forward_prefill.argtypes = [

@@ -201,8 +201,32 @@ def test_mfma_matches_generic(dtype, S, K, act):
     at 5-8 taps and 32 routes, 8 taps and 16 routes: the two-pass backward,
     odd kernel sizes with a missing last tap in the second half; 64 routes
     without activation: the two passes with the taps pass in route halves)."""
+    _mfma_vs_generic(dtype, S, K, act, 192)
+
+
+@pytest.mark.parametrize("dtype,S,K,act", [
+    (torch.bfloat16, 4, 16, "silu"),   # the four-wave fused pass
+    (torch.bfloat16, 3, 16, None),     # fused pass
+    (torch.bfloat16, 8, 32, None),     # two passes
+    (torch.bfloat16, 8, 32, "silu"),   # two passes, g through the workspace
+    (torch.bfloat16, 4, 64, None),     # taps pass in route halves
+    (torch.bfloat16, 3, 32, "silu"),   # fused pass split in route chunks
+    (torch.bfloat16, 6, 48, "silu"),   # 64-route two passes, g through the workspace
+    (torch.float32, 4, 16, "silu"),
+    (torch.float32, 7, 32, None),
+])
+@pytest.mark.parametrize("D", [198, 130])
+def test_mfma_even_channel_tails(dtype, S, K, act, D):
+    """Channel counts that are even but not a multiple of 4 (the last 16-lane
+    column of a wave holds a partial group of channel pairs) run on the
+    matrix-core kernels, against the oracle and the generic kernels."""
+    assert _lib.lib().moc_matrix_core_supported(3 * 333, D, K, S, _lib.dtype_code(dtype)) == 1
+    _mfma_vs_generic(dtype, S, K, act, D)
+
+
+def _mfma_vs_generic(dtype, S, K, act, D):
     g = gen(S * 100 + K)
-    D, Bt, T = 192, 3, 333
+    Bt, T = 3, 333
     x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
     a = torch.softmax(randn(g, Bt, T, K), -1).to(DEV, dtype)
     b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
@@ -283,12 +307,13 @@ def test_two_pass_small_and_ragged(S, K, B, T, D):
 @pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 20), (8, 32), (8, 5), (5, 16), (6, 24),
                                  (7, 32), (4, 48), (8, 64)])
 @pytest.mark.parametrize("route", [None, "softmax", "exp"])
-def test_decode_kernel_matches_oracle_and_generic(S, K, route):
+@pytest.mark.parametrize("D", [196, 198])
+def test_decode_kernel_matches_oracle_and_generic(S, K, route, D):
     """Decode steps through the matrix-core kernel and the generic kernel: y
     against the oracle step (routing weights formed from the same logits),
     caches bit-exact and identical between the two."""
     g = gen(S * 1000 + K)
-    Bt, D, steps = 37, 196, 5                      # ragged batch and channel counts
+    Bt, steps = 37, 5                              # ragged batch and channel counts
     x = randn(g, Bt, steps, D, scale=0.5).to(DEV, torch.bfloat16)
     lg = randn(g, Bt, steps, K).to(DEV, torch.bfloat16)
     b = randn(g, K, S, D, scale=0.2).to(DEV, torch.bfloat16)

@@ -82,7 +82,18 @@ CASES = [  # S, K, activation, dtype, T (T >= S-1: the prefill entries' range)
 
 @pytest.mark.parametrize("S,K,act,dtype,T", CASES)
 def test_prefill_entries_against_oracle(S, K, act, dtype, T):
-    B, D = 3, 192
+    _prefill_case(S, K, act, dtype, T, 192)
+
+
+@pytest.mark.parametrize("S,K,act,dtype,T", [(4, 16, "silu", BF, 40), (8, 32, None, BF, 33),
+                                              (7, 16, "silu", F32, 9), (4, 64, "silu", BF, 21)])
+def test_prefill_even_channel_tail(S, K, act, dtype, T):
+    """An even channel count that is not a multiple of 4 (198)."""
+    _prefill_case(S, K, act, dtype, T, 198)
+
+
+def _prefill_case(S, K, act, dtype, T, D):
+    B = 3
     x, a, b, c, dy = _inputs(S * 100 + K + T, B, T, D, K, S, dtype)
     flag = 1 if act else 0
     assert ops.prefill_supported(x, b, with_cache=True)
