@@ -549,7 +549,37 @@ def cpu_baseline(seconds):
     tok_s = reps * T / el
     return {"value": round(tok_s / 1e6, 5), "unit": "Mtok/s", "cores": cores, "kind": "port",
             "sample": f"CPU oracle, layer fwd+bwd on B=1 T={T} D={CFG['D']} Z={CFG['Z']} "
-                      f"K={CFG['K']} S={CFG['S']} fp32, {reps} reps in {el:.1f}s"}
+                      f"K={CFG['K']} S={CFG['S']} fp32, {reps} reps in {el:.1f}s",
+            "configs0_forward": cpu_configs0_forward(min(seconds, 5.0))}
+
+
+def cpu_configs0_forward(seconds):
+    """BASELINE configs[0] on the CPU oracle: the reference's CPU-runnable
+    forward (B=2, T=512, D=256, z_dim=256, K=4, S=4, fp32; x, z ~ N(0,1) seed 0,
+    router ~ N(0, 0.02), basis ~ N(0, 0.002), softmax routing, no SiLU)."""
+    from oracle import moc_oracle as O
+    B, T, D, Z, K, S = 2, 512, 256, 256, 4, 4
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(B, T, D, generator=g)
+    z = torch.randn(B, T, Z, generator=g)
+    router = torch.randn(K, Z, generator=g) * 0.02
+    basis = torch.randn(K, S, D, generator=g) * 0.002
+
+    def fwd():
+        return O.moc_ref(x, O.route(torch.nn.functional.linear(z, router), "softmax"), basis, None)
+
+    with torch.no_grad():
+        fwd()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fwd()
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds and reps >= 2:
+                break
+    return {"value": round(reps * B * T / el / 1e6, 5), "unit": "Mtok/s",
+            "ms_per_call": round(el / reps * 1e3, 3),
+            "sample": f"CPU oracle forward (router + softmax + MoC) at configs[0], {reps} reps in {el:.1f}s"}
 
 
 def config3_step(dev):
