@@ -58,7 +58,7 @@ extern "C" {
 #define MOC_ERR_WORKSPACE -3
 #define MOC_ERR_HIP       -4
 
-/* ABI version of this header (4: dy_row_stride -1 accepted). */
+/* ABI version of this header (5: MocLayer carries each layer's k and activation). */
 int moc_abi_version(void);
 
 /* Message for the last failed call on this thread ("" if none). */
@@ -228,15 +228,17 @@ int moc_backward_prefill(const void* x, const void* alpha, const void* basis, co
  * Several MoC layers on one token axis in one launch per pass: the q / k / v
  * pattern of the reference README (README.md:80-129), three MoC.forward calls
  * (moc/api.py:372-400) whose forward / backward launches each cover one layer.
- * A MocLayer names one layer's tensors; the layers share cu_seqlens /
- * n_tokens / seq_len, k, kernel_size, x_dtype and activation, and each has its
- * own dim, routing and alpha / basis dtypes.  Fields are those of
- * moc_forward (x, alpha, basis, y) and moc_backward (dy, dy_row_stride, dx or
- * NULL, dalpha, dbasis); each entry uses its own.  When every layer is bf16 and
- * on the matrix-core kernels, each pass (forward; backward stage 1; stage 2)
- * is one launch over all layers' channels; otherwise the layers run one by
- * one.  Results equal moc_forward / moc_backward per layer bit for bit.
- * 1 <= n_layers <= 4.
+ * A MocLayer names one layer's tensors and shape; the layers share cu_seqlens /
+ * n_tokens / seq_len, kernel_size and x_dtype, and each has its own dim, k,
+ * activation, routing and alpha / basis dtypes.  Fields are those of
+ * moc_forward (x, alpha, basis, y, k, activation) and moc_backward (dy,
+ * dy_row_stride, dx or NULL, dalpha, dbasis); each entry uses its own.  When
+ * every layer is bf16 and on the matrix-core kernels, the forward is one launch
+ * over all layers' channels, and the backward one stage-1 launch per route
+ * count present (per route count and activation where the single launches
+ * without activation run the two-pass form) plus one stage-2 launch; otherwise
+ * the layers run one by one.  Results equal moc_forward / moc_backward per
+ * layer bit for bit.  1 <= n_layers <= 4.
  */
 typedef struct MocLayer {
   const void* x;
@@ -252,25 +254,23 @@ typedef struct MocLayer {
   int routing;
   int alpha_dtype;
   int basis_dtype;
+  int activation;
+  int64_t k;
 } MocLayer;
 
 #define MOC_MAX_LAYERS 4
 
 size_t moc_forward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
-                                          int64_t k, int64_t kernel_size, int x_dtype,
-                                          int activation);
+                                          int64_t kernel_size, int x_dtype);
 int moc_forward_layers(const MocLayer* layers, int n_layers,
                        const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
-                       int64_t n_tokens, int64_t seq_len, int64_t k, int64_t kernel_size,
-                       int x_dtype, int activation,
+                       int64_t n_tokens, int64_t seq_len, int64_t kernel_size, int x_dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
 size_t moc_backward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
-                                           int64_t k, int64_t kernel_size, int x_dtype,
-                                           int activation);
+                                           int64_t kernel_size, int x_dtype);
 int moc_backward_layers(const MocLayer* layers, int n_layers,
                         const void* cu_seqlens, int cu_seqlens_i64, int64_t n_seqs,
-                        int64_t n_tokens, int64_t seq_len, int64_t k, int64_t kernel_size,
-                        int x_dtype, int activation,
+                        int64_t n_tokens, int64_t seq_len, int64_t kernel_size, int x_dtype,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*

@@ -66,12 +66,14 @@ constexpr bool bwd_lean(int S, int KC, bool bf) { return bf && KC == 1 && S >= 2
 
 // The work of workgroup (bx, by) of one layer; the __global__ wrappers below
 // map a single launch's 2-D grid or a grouped launch's 1-D grid onto it.
-template <int S, bool ACT, bool DY1>
+template <int S, int ACT, bool DY1>
 __device__ __forceinline__ void
 bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
               const uint16_t* __restrict__ a_c, const uint16_t* __restrict__ b_c,
               void* __restrict__ dxv, float* __restrict__ part_da, float* __restrict__ part_db,
-              SeqLayout seq, int64_t D, int bx, int by, int gy, int gy1, int n_old, int n_total) {
+              SeqLayout seq, int64_t D, int bx, int by, int gy, int gy1, int n_old, int n_total,
+              bool act_rt = false) {
+  const bool act = ACT == kActRuntime ? act_rt : ACT != 0;  // (uniform)
   using E = uint16_t;
   using Op = s16x4;
   constexpr int NB = 2, R = 8, TB = 32, W = R + S - 1, EOWN = TB - (S - 1);
@@ -280,7 +282,7 @@ bwd_lean_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t
         }
       };
 
-      if constexpr (ACT) {
+      if constexpr (ACT != 0) if (act) {  // (act: uniform; always with a fixed ACT)
         float p[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) p[r] = 0.f;
@@ -485,7 +487,7 @@ bwd_lean_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int64
 // Several layers in one launch (1-D grid, the layers' grids one after another,
 // as bwd_layers_kernel maps them), so that a grouped launch returns the
 // per-layer calls' results bit for bit.
-template <int S, bool ACT, bool DY1>
+template <int S, int ACT, bool DY1>
 __global__ void __launch_bounds__(64 * kLeanWPG) __attribute__((amdgpu_waves_per_eu(MOC_LEAN_WAVES)))
 bwd_lean_layers_kernel(BwdLayers ly, SeqLayout seq) {
   const int blk = static_cast<int>(blockIdx.x);
@@ -498,7 +500,7 @@ bwd_lean_layers_kernel(BwdLayers ly, SeqLayout seq) {
   }
   bwd_lean_tile<S, ACT, DY1>(Lp->x, Lp->dy, Lp->dys, static_cast<const uint16_t*>(Lp->a),
                         static_cast<const uint16_t*>(Lp->b), Lp->dx, Lp->part_da, Lp->part_db, seq,
-                        Lp->D, local, row, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total);
+                        Lp->D, local, row, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total, Lp->act != 0);
 }
 
 }  // namespace mfma

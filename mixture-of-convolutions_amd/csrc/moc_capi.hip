@@ -140,7 +140,7 @@ int hip_status(const char* what) {
 
 extern "C" {
 
-int moc_abi_version(void) { return 4; }
+int moc_abi_version(void) { return 5; }
 
 const char* moc_last_error(void) { return g_err; }
 
@@ -454,8 +454,8 @@ namespace {
 
 // Problems of a layer set (checked); n_layers in [1, MOC_MAX_LAYERS].
 int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu64,
-                   int64_t n_seqs, int64_t n_tokens, int64_t seq_len, int64_t k, int64_t ks,
-                   int x_dt, int activation, bool backward, moc::Problem* ps) {
+                   int64_t n_seqs, int64_t n_tokens, int64_t seq_len, int64_t ks, int x_dt,
+                   bool backward, moc::Problem* ps) {
   if (n_layers < 1 || n_layers > MOC_MAX_LAYERS)
     return fail(MOC_ERR_ARG, "n_layers must be in [1, %d], got %d", MOC_MAX_LAYERS, n_layers);
   if (!layers) return fail(MOC_ERR_ARG, "null layer array");
@@ -463,11 +463,11 @@ int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu6
   if ((rc = check_seq(cu, n_seqs, seq_len)) != MOC_OK) return rc;
   for (int i = 0; i < n_layers; ++i) {
     const MocLayer& l = layers[i];
-    if ((rc = check_dims(n_tokens, l.dim, k, ks)) != MOC_OK) return rc;
-    if ((rc = check_common(x_dt, l.alpha_dtype, l.basis_dtype, activation, l.routing)) != MOC_OK)
+    if ((rc = check_dims(n_tokens, l.dim, l.k, ks)) != MOC_OK) return rc;
+    if ((rc = check_common(x_dt, l.alpha_dtype, l.basis_dtype, l.activation, l.routing)) != MOC_OK)
       return rc;
-    ps[i] = make_problem(cu, cu64, n_seqs, n_tokens, seq_len, l.dim, k, ks, x_dt, l.alpha_dtype,
-                         l.basis_dtype, activation, l.routing);
+    ps[i] = make_problem(cu, cu64, n_seqs, n_tokens, seq_len, l.dim, l.k, ks, x_dt, l.alpha_dtype,
+                         l.basis_dtype, l.activation, l.routing);
     if (backward) {
       if (l.dy_row_stride != 0 && l.dy_row_stride != l.dim && l.dy_row_stride != -1)
         return fail(MOC_ERR_ARG, "layer %d: dy_row_stride must be dim (%lld), 0 or -1, got %lld",
@@ -500,12 +500,11 @@ size_t layers_bytes(const moc::Problem* ps, int n, bool backward) {
 extern "C" {
 
 size_t moc_forward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
-                                          int64_t k, int64_t kernel_size, int x_dtype,
-                                          int activation) {
+                                          int64_t kernel_size, int x_dtype) {
   moc::Problem ps[MOC_MAX_LAYERS];
   const char saved = g_err[0];
-  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, k, kernel_size, x_dtype,
-                     activation, false, ps) != MOC_OK) {
+  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, kernel_size, x_dtype,
+                     false, ps) != MOC_OK) {
     g_err[0] = saved;
     return 0;
   }
@@ -513,12 +512,11 @@ size_t moc_forward_layers_workspace_bytes(const MocLayer* layers, int n_layers, 
 }
 
 size_t moc_backward_layers_workspace_bytes(const MocLayer* layers, int n_layers, int64_t n_tokens,
-                                           int64_t k, int64_t kernel_size, int x_dtype,
-                                           int activation) {
+                                           int64_t kernel_size, int x_dtype) {
   moc::Problem ps[MOC_MAX_LAYERS];
   const char saved = g_err[0];
-  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, k, kernel_size, x_dtype,
-                     activation, false, ps) != MOC_OK) {
+  if (layer_problems(layers, n_layers, nullptr, 0, 0, n_tokens, n_tokens, kernel_size, x_dtype,
+                     false, ps) != MOC_OK) {
     g_err[0] = saved;
     return 0;
   }
@@ -527,12 +525,12 @@ size_t moc_backward_layers_workspace_bytes(const MocLayer* layers, int n_layers,
 
 int moc_forward_layers(const MocLayer* layers, int n_layers, const void* cu_seqlens,
                        int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens, int64_t seq_len,
-                       int64_t k, int64_t kernel_size, int x_dtype, int activation,
-                       void* workspace, size_t workspace_bytes, void* stream) {
+                       int64_t kernel_size, int x_dtype, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   g_err[0] = '\0';
   moc::Problem ps[MOC_MAX_LAYERS];
   int rc = layer_problems(layers, n_layers, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len,
-                          k, kernel_size, x_dtype, activation, false, ps);
+                          kernel_size, x_dtype, false, ps);
   if (rc != MOC_OK) return rc;
   for (int i = 0; i < n_layers; ++i)
     if (!layers[i].x || !layers[i].alpha || !layers[i].basis || !layers[i].y)
@@ -555,8 +553,8 @@ int moc_forward_layers(const MocLayer* layers, int n_layers, const void* cu_seql
     const MocLayer& l = layers[i];
     const size_t nb = align_up(forward_bytes(ps[i]));
     rc = moc_forward(l.x, l.alpha, l.basis, l.y, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens,
-                     seq_len, l.dim, k, kernel_size, x_dtype, l.alpha_dtype, l.basis_dtype,
-                     activation, l.routing, nb ? ws : nullptr, nb, stream);
+                     seq_len, l.dim, l.k, kernel_size, x_dtype, l.alpha_dtype, l.basis_dtype,
+                     l.activation, l.routing, nb ? ws : nullptr, nb, stream);
     if (rc != MOC_OK) return rc;
     ws += nb;
   }
@@ -565,12 +563,12 @@ int moc_forward_layers(const MocLayer* layers, int n_layers, const void* cu_seql
 
 int moc_backward_layers(const MocLayer* layers, int n_layers, const void* cu_seqlens,
                         int cu_seqlens_i64, int64_t n_seqs, int64_t n_tokens, int64_t seq_len,
-                        int64_t k, int64_t kernel_size, int x_dtype, int activation,
-                        void* workspace, size_t workspace_bytes, void* stream) {
+                        int64_t kernel_size, int x_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream) {
   g_err[0] = '\0';
   moc::Problem ps[MOC_MAX_LAYERS];
   int rc = layer_problems(layers, n_layers, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len,
-                          k, kernel_size, x_dtype, activation, true, ps);
+                          kernel_size, x_dtype, true, ps);
   if (rc != MOC_OK) return rc;
   for (int i = 0; i < n_layers; ++i) {
     const MocLayer& l = layers[i];

@@ -113,6 +113,11 @@ struct Vec {
 // past the channel axis need no branches: they get an out-of-range offset.
 constexpr uint32_t kOffNone = 0x80000000u;  // an offset no range here reaches
 
+// Values of the kernels' ACT parameter: 0 (no activation), 1 (SiLU), or
+// kActRuntime: the layers of a grouped launch each name theirs in the layer
+// table (a uniform branch; the SiLU code is built in).
+constexpr int kActRuntime = 2;
+
 struct Buf {
   __amdgpu_buffer_rsrc_t r;
   __device__ __forceinline__ Buf(const void* base, int64_t bytes) {
@@ -354,6 +359,8 @@ struct FwdLayer {
   void* y;
   int64_t D;
   int gx, n_sb, blk0;
+  int act;         // this layer's activation (read where the kernel's ACT is kActRuntime)
+  int kc;          // this layer's route chunks (1, 2 or 4)
 };
 struct FwdLayers {
   int n;
@@ -371,6 +378,7 @@ struct BwdLayer {
   float* part_db;  // [gy, KP, S, D]
   int64_t D;
   int gx, gy, gy1, n_old, n_total, blk0;
+  int act;         // this layer's activation (read where the kernel's ACT is kActRuntime)
 };
 struct BwdLayers {
   int n;
@@ -396,13 +404,15 @@ __device__ __forceinline__ int layer_index(const LT& ly, int blk) {
 // routing weights, raw) before it computes super-block i.  fwd_tile is the
 // work of workgroup (bx, by) of one layer.  PRE: prefill from a cache (Pre;
 // fixed-length sequences).
-template <int S, int KC, int NB, int NC, bool ACT, bool BF, bool PRE = false>
+template <int S, int KC, int NB, int NC, int ACT, bool BF, bool PRE = false>
 __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
                                          const typename CT<BF>::elem* __restrict__ a_c,
                                          const typename CT<BF>::elem* __restrict__ b_c,
                                          void* __restrict__ yv, SeqLayout seq, int64_t D, int n_sb,
-                                         int bx, int by, Pre pre = Pre{nullptr, nullptr}) {
+                                         int bx, int by, Pre pre = Pre{nullptr, nullptr},
+                                         bool act_rt = false) {
   using C = CT<BF>;
+  const bool act = ACT == kActRuntime ? act_rt : ACT != 0;  // (uniform)
   using E = typename C::elem;
   using Op = typename C::opnd;
   constexpr int R = 4 * NB, TB = 16 * NB, CW = 16 * NC, KP = 16 * KC, W = R + S - 1;
@@ -550,12 +560,12 @@ __device__ __forceinline__ void fwd_tile(const void* __restrict__ xv,
       for (int r = 0; r < R; ++r) {
         E o[NC];
         if constexpr (BF && NC == 2) {
-          const uint32_t pk = ACT ? pack2_bf16(silu_f(acc[r][0]), silu_f(acc[r][1]))
+          const uint32_t pk = act ? pack2_bf16(silu_f(acc[r][0]), silu_f(acc[r][1]))
                                   : pack2_bf16(acc[r][0], acc[r][1]);
           __builtin_memcpy(o, &pk, 4);
         } else {
 #pragma unroll
-          for (int c = 0; c < NC; ++c) o[c] = C::from_f(ACT ? silu_f(acc[r][c]) : acc[r][c]);
+          for (int c = 0; c < NC; ++c) o[c] = C::from_f(act ? silu_f(acc[r][c]) : acc[r][c]);
         }
         yb.store<NC * ESZ>(ybase + r * rb, o);
       }
@@ -598,9 +608,12 @@ fwd_pre_kernel(const void* __restrict__ xv, const typename CT<BF>::elem* __restr
 }
 
 // Several layers in one launch (1-D grid, the layers' grids one after another).
-template <int S, int KC, int NB, int NC, bool ACT, bool BF>
+// KCM: the route-chunk counts present (bits 1, 2, 4); with more than one, each
+// layer runs the tile of its own count (a uniform branch), so that a layer's y
+// is that of its single launch.
+template <int S, int KCM, int NB, int NC, int ACT, bool BF>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu((S == 8 && KC == 2) ? MOC_FWD8_WAVES : 1)))
+__attribute__((amdgpu_waves_per_eu((S == 8 && KCM == 2) ? MOC_FWD8_WAVES : 1)))
 fwd_layers_kernel(FwdLayers ly, SeqLayout seq) {
   using E = typename CT<BF>::elem;
   const int blk = static_cast<int>(blockIdx.x);
@@ -611,9 +624,30 @@ fwd_layers_kernel(FwdLayers ly, SeqLayout seq) {
     local -= gxl;
     ++row;
   }
-  fwd_tile<S, KC, NB, NC, ACT, BF>(Lp->x, static_cast<const E*>(Lp->a),
-                                   static_cast<const E*>(Lp->b), Lp->y, seq, Lp->D, Lp->n_sb, local,
-                                   row);
+  auto run = [&](auto kc) {
+    fwd_tile<S, decltype(kc)::value, NB, NC, ACT, BF>(Lp->x, static_cast<const E*>(Lp->a),
+                                                      static_cast<const E*>(Lp->b), Lp->y, seq, Lp->D,
+                                                      Lp->n_sb, local, row, Pre{nullptr, nullptr},
+                                                      Lp->act != 0);
+  };
+  if constexpr (KCM == 1 || KCM == 2 || KCM == 4) {
+    run(std::integral_constant<int, KCM>{});
+  } else {
+    const int kc = __builtin_amdgcn_readfirstlane(Lp->kc);
+    if constexpr ((KCM & 1) != 0) {
+      if (kc == 1) {
+        run(std::integral_constant<int, 1>{});
+        return;
+      }
+    }
+    if constexpr ((KCM & 2) != 0) {
+      if (kc == 2 || (KCM & 4) == 0) {
+        run(std::integral_constant<int, 2>{});
+        return;
+      }
+    }
+    if constexpr ((KCM & 4) != 0) run(std::integral_constant<int, 4>{});
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -787,7 +821,7 @@ constexpr int kBwdMinWaves = ((MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>)
 // in the m products (the cache gradient is not formed here).  gbuf (the partial
 // passes with the activation): g = dy silu'(P) of every token and channel in
 // fp32 [N, D], written by the dx pass, read by the taps pass in place of dy.
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE,
+template <int S, int KC, int NB, int NC, int WPG, int ACT, bool BF, bool SPLIT, int MODE,
           bool PRE = false>
 __device__ __forceinline__ void
 bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
@@ -795,7 +829,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
          const typename CT<BF>::elem* __restrict__ b_c, void* __restrict__ dxv,
          float* __restrict__ part_da, float* __restrict__ part_db, SeqLayout seq, int64_t D,
          int bx, int by, int zh, int gy, int gy1, int n_old, int n_total,
-         Pre pre = Pre{nullptr, nullptr}, float* __restrict__ gbuf = nullptr) {
+         Pre pre = Pre{nullptr, nullptr}, float* __restrict__ gbuf = nullptr, bool act_rt = false) {
   using C = CT<BF>;
   using E = typename C::elem;
   using Op = typename C::opnd;
@@ -820,10 +854,13 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(MODE == kBwdFused || BF, "the partial passes are built for bf16");
   // with the activation: P (and g) formed in this pass; g read from gbuf (taps
   // pass) or written there (dx pass)
-  constexpr bool PACT = ACT && MODE != kBwdTaps;
-  constexpr bool GIN = ACT && MODE == kBwdTaps, GOUT = ACT && MODE == kBwdDx;
+  constexpr bool PACT = ACT != 0 && MODE != kBwdTaps;
+  constexpr bool GIN = ACT != 0 && MODE == kBwdTaps, GOUT = ACT != 0 && MODE == kBwdDx;
+  static_assert(ACT != kActRuntime || (MODE == kBwdFused && !PRE),
+                "a per-layer activation is built for the fused pass of grouped launches");
+  const bool act = ACT == kActRuntime ? act_rt : ACT != 0;  // (uniform)
   static_assert(MODE != kBwdDx || !SPLIT, "dx uses every route chunk");
-  static_assert(!PRE || MODE != kBwdDx || ACT,
+  static_assert(!PRE || MODE != kBwdDx || ACT != 0,
                 "without the activation the prefill dx pass is the plain one (it reads no cache)");
   constexpr int ST = MODE == kBwdTaps ? (S + 1) / 2 : S;
   constexpr bool kOneBody = MODE == kBwdTaps && BF;
@@ -1098,7 +1135,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
     // without copies: configs[2] and configs[4] steps -1%; the SiLU pass
     // measured 1 us slower this way, and the prefill pass's one-wave forms
     // crash LLVM's AGPR-copy rewrite with it
-    constexpr bool kPin = MODE != kBwdTaps && !PRE && !ACT;
+    constexpr bool kPin = MODE != kBwdTaps && !PRE && ACT == 0;
     // the taps pass converts each x value where an m product uses it instead of
     // keeping an fp32 copy of the window (22 registers for about 40 more VALU:
     // the pass waits far more than it issues, and its spills waited on memory)
@@ -1176,7 +1213,7 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
           if (use_h) hist_window<S, W, NC, E>(hb, trun - (S - 1), T, N, D, dl, ch_ok, hx);
       }
 
-      if constexpr (PACT) {
+      if constexpr (PACT) if (act) {  // (act: uniform; always with a fixed ACT)
         float p[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -1721,9 +1758,9 @@ bwd_pre_dx_kernel(const void* __restrict__ xv, const void* __restrict__ dyv, int
 
 // Several layers in one launch (1-D grid, the layers' grids one after another:
 // gx gy blocks of layer i, or its split grid's ids).
-template <int S, int KC, int NB, int NC, int WPG, bool ACT, bool BF, bool SPLIT, int MODE>
+template <int S, int KC, int NB, int NC, int WPG, int ACT, bool BF, bool SPLIT, int MODE>
 __global__ void __launch_bounds__(64 * WPG)
-__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF, ACT>)))
+__attribute__((amdgpu_waves_per_eu(kBwdMinWaves<S, KC, MODE, BF, ACT != 0>)))
 bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
   using E = typename CT<BF>::elem;
   const int blk = static_cast<int>(blockIdx.x);
@@ -1742,7 +1779,8 @@ bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(
       Lp->x, Lp->dy, Lp->dys, static_cast<const E*>(Lp->a), static_cast<const E*>(Lp->b), Lp->dx,
-      Lp->part_da, Lp->part_db, seq, Lp->D, bx, by, zh, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total);
+      Lp->part_da, Lp->part_db, seq, Lp->D, bx, by, zh, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total,
+      Pre{nullptr, nullptr}, nullptr, Lp->act != 0);
 }
 
 }  // namespace mfma

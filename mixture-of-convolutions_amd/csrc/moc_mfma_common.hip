@@ -182,7 +182,7 @@ stage2_kernel(const float* __restrict__ part_da, int64_t n_da, const float* __re
 }
 
 // Stage 2 of several layers in one launch: layer i owns blocks [blk0, blk0 +
-// da_blocks + its dbasis blocks) of the grid.
+// da_blocks + its dbasis blocks) of the grid and has its own K (kc route chunks).
 struct Stage2Layer {
   const float* part_da;
   int64_t n_da, n_db;
@@ -194,22 +194,28 @@ struct Stage2Layer {
   int b_dt;
   const float* part_db;
   int64_t D, blk0;
+  int K, kc;
 };
 struct Stage2Layers {
   int n;
   Stage2Layer l[kMaxLayers];
 };
 
-template <int KC>
 __global__ void __launch_bounds__(256)
-stage2_layers_kernel(Stage2Layers ly, int64_t N, int K, int S, int64_t da_blocks) {
+stage2_layers_kernel(Stage2Layers ly, int64_t N, int S, int64_t da_blocks) {
   const int64_t b = static_cast<int64_t>(blockIdx.x);
   Stage2Layer L = ly.l[0];
 #pragma unroll
   for (int i = 1; i < kMaxLayers; ++i)
     if (i < ly.n && b >= ly.l[i].blk0) L = ly.l[i];
-  stage2_block<KC>(L.part_da, L.n_da, L.part_db, L.n_db, L.a_r, L.a_w, L.dalpha, L.a_dt,
-                   L.routing, L.dbasis, L.b_dt, N, K, S, L.D, da_blocks, b - L.blk0);
+  auto run = [&](auto kc) {
+    stage2_block<decltype(kc)::value>(L.part_da, L.n_da, L.part_db, L.n_db, L.a_r, L.a_w, L.dalpha,
+                                      L.a_dt, L.routing, L.dbasis, L.b_dt, N, L.K, S, L.D, da_blocks,
+                                      b - L.blk0);
+  };
+  if (L.kc == 1) run(std::integral_constant<int, 1>{});
+  else if (L.kc == 2) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 4>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -571,28 +577,43 @@ void backward_prefill(const Problem& p, const void* x, const void* alpha, const 
 }
 
 // ---------------------------------------------------------------------------
-// Grouped layers: bf16 layers on one token axis with the same K, S and
-// activation run every pass as one launch over all their channel groups.
+// Grouped layers: bf16 layers on one token axis with the same S, each with its
+// own K and activation.  The forward is one launch over all their channel
+// groups; the backward one stage-1 launch per class of layers that share the
+// route chunks (and, where the single launch's form depends on it, the
+// activation), then one stage-2 launch.  Every layer's results are those of its
+// single launch, bit for bit.
 
 bool layers_grouped(const Problem* ps, int n, bool backward) {
   if (n < 1 || n > kMaxLayers) return false;
   for (int i = 0; i < n; ++i) {
     const Problem& p = ps[i];
     if (!supported(p) || p.x_dt != DT_BF16) return false;
-    if (p.K != ps[0].K || p.S != ps[0].S || p.activation != ps[0].activation ||
-        p.n_tokens != ps[0].n_tokens || p.path != ps[0].path)
-      return false;
+    if (p.S != ps[0].S || p.n_tokens != ps[0].n_tokens || p.path != ps[0].path) return false;
   }
   // the backward shapes whose single launch runs a two-pass form the grouped
   // launch does not have (with SiLU; 64 routes) run as single launches, so the
   // results stay those of the per-layer calls
   if (backward) {
-    const int S = static_cast<int>(ps[0].S), KC = route_chunks(ps[0].K);
-    const bool act = ps[0].activation != 0;
-    if (bwd_two_pass_g(S, KC, act, true) || bwd_two_pass_r(S, KC, act, true)) return false;
+    for (int i = 0; i < n; ++i) {
+      const int S = static_cast<int>(ps[i].S), KC = route_chunks(ps[i].K);
+      const bool act = ps[i].activation != 0;
+      if (bwd_two_pass_g(S, KC, act, true) || bwd_two_pass_r(S, KC, act, true)) return false;
+    }
   }
   return true;
 }
+
+namespace {
+// Stage-1 class of a layer in a grouped backward: its route chunks, and its
+// activation where the layers without one run the two-pass form (the layers
+// with one run the fused pass: they cannot share that launch).
+int bwd_class(const Problem& p) {
+  const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
+  const int act = bwd_two_pass(S, KC, false, true) ? (p.activation != 0 ? 1 : 0) : 2;
+  return KC * 4 + act;
+}
+}  // namespace
 
 size_t forward_layers_workspace(const Problem* ps, int n) {
   size_t total = 0;
@@ -628,6 +649,8 @@ void forward_layers(const Problem* ps, const LayerIO* io, int n, void* workspace
     }
     L[i].y = io[i].y;
     L[i].D = ps[i].D;
+    L[i].act = ps[i].activation != 0;
+    L[i].kc = route_chunks(ps[i].K);
     ws += pl.total;
   }
   prof_begin(ps[0], st);
@@ -672,6 +695,8 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
     L[i].part_da = reinterpret_cast<float*>(ws + pl.off_pda);
     L[i].part_db = reinterpret_cast<float*>(ws + pl.off_pdb);
     L[i].D = p.D;
+    L[i].act = p.activation != 0;
+    L[i].kc = route_chunks(p.K);
     const int grad = route_grad(p.routing);
     s2.l[i] = Stage2Layer{L[i].part_da,
                           static_cast<int64_t>(pl.bg.gx),
@@ -686,27 +711,38 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
                           p.b_dt,
                           L[i].part_db,
                           p.D,
-                          blk};
+                          blk,
+                          static_cast<int>(p.K),
+                          L[i].kc};
     blk += da_blocks + cdiv(p.K * p.S * p.D, 256);
     ws += pl.total;
   }
+  // stage 1: one launch per class, the classes in the order of their first layer
   prof_begin(ps[0], st);
-  switch (ps[0].S) {
-    case 2: launch_bwd_layers<2>(ps[0], L, n, st); break;
-    case 3: launch_bwd_layers<3>(ps[0], L, n, st); break;
-    case 4: launch_bwd_layers<4>(ps[0], L, n, st); break;
-    case 5: launch_bwd_layers<5>(ps[0], L, n, st); break;
-    case 6: launch_bwd_layers<6>(ps[0], L, n, st); break;
-    case 7: launch_bwd_layers<7>(ps[0], L, n, st); break;
-    case 8: launch_bwd_layers<8>(ps[0], L, n, st); break;
-    default: break;
+  bool done[kMaxLayers] = {};
+  for (int i = 0; i < n; ++i) {
+    if (done[i]) continue;
+    LayerOps C[kMaxLayers] = {};
+    int nc = 0;
+    for (int j = i; j < n; ++j)
+      if (!done[j] && bwd_class(ps[j]) == bwd_class(ps[i])) {
+        C[nc++] = L[j];
+        done[j] = true;
+      }
+    switch (ps[0].S) {
+      case 2: launch_bwd_layers<2>(ps[i], C, nc, st); break;
+      case 3: launch_bwd_layers<3>(ps[i], C, nc, st); break;
+      case 4: launch_bwd_layers<4>(ps[i], C, nc, st); break;
+      case 5: launch_bwd_layers<5>(ps[i], C, nc, st); break;
+      case 6: launch_bwd_layers<6>(ps[i], C, nc, st); break;
+      case 7: launch_bwd_layers<7>(ps[i], C, nc, st); break;
+      case 8: launch_bwd_layers<8>(ps[i], C, nc, st); break;
+      default: break;
+    }
   }
   prof_end(ps[0], st);
-  const int K = static_cast<int>(ps[0].K), S = static_cast<int>(ps[0].S);
-  auto kern = K <= 16 ? stage2_layers_kernel<1>
-                      : (K <= 32 ? stage2_layers_kernel<2> : stage2_layers_kernel<4>);
-  hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, s2, N, K, S,
-                     da_blocks);
+  hipLaunchKernelGGL(stage2_layers_kernel, dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, s2, N,
+                     static_cast<int>(ps[0].S), da_blocks);
 }
 
 }  // namespace mfma

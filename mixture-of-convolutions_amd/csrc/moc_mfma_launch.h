@@ -245,6 +245,8 @@ struct LayerOps {
   float* part_da;
   float* part_db;
   int64_t D;
+  int act;   // the layer's activation (0 / 1)
+  int kc;    // the layer's route chunks (1, 2 or 4)
 };
 
 template <int S, int KC, bool ACT, bool BF>
@@ -320,8 +322,11 @@ void bwd_one(const Problem& p, const void* x, const void* dy, const void* a_c, c
 }
 
 // Grouped launches (bf16): one kernel over the layers' own grids, one after
-// another on a 1-D grid (see FwdLayers / BwdLayers).
-template <int S, int KC, bool ACT>
+// another on a 1-D grid (see FwdLayers / BwdLayers).  ACT: 0 / 1 when the layers
+// share it, kActRuntime when each reads its own.  The forward takes layers of
+// any route counts (KCM: the counts present); the backward the layers of one
+// count (one launch per count present).
+template <int S, int KCM, int ACT>
 void fwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
   FwdLayers ly{};
   ly.n = n;
@@ -329,17 +334,29 @@ void fwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
   for (int i = 0; i < n; ++i) {
     const Grid2 g = fwd_grid(p.n_tokens, L[i].D, S);
     ly.l[i] = FwdLayer{L[i].x, L[i].a_c, L[i].b_c, L[i].y, L[i].D, static_cast<int>(g.gx),
-                       g.n_sb, static_cast<int>(blk)};
+                       g.n_sb, static_cast<int>(blk), L[i].act, L[i].kc};
     blk += static_cast<int64_t>(g.gx) * g.gy;
   }
-  hipLaunchKernelGGL((fwd_layers_kernel<S, KC, fwd_nb(S), kFwdNC, ACT, true>),
+  hipLaunchKernelGGL((fwd_layers_kernel<S, KCM, fwd_nb(S), kFwdNC, ACT, true>),
                      dim3(static_cast<unsigned>(blk)), dim3(256), 0, st, ly, p.seq);
 }
 
-template <int S, int KC, bool ACT>
+// 0 / 1: every layer's activation; kActRuntime: mixed
+inline int layers_act(const LayerOps* L, int n) {
+  bool any = false, all = true;
+  for (int i = 0; i < n; ++i) {
+    any = any || L[i].act != 0;
+    all = all && L[i].act != 0;
+  }
+  return all ? 1 : (any ? kActRuntime : 0);
+}
+
+template <int S, int KC, int ACT>
 void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
   constexpr bool kSplit = KC >= 2;
-  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, true);
+  // (mixed activations run the fused pass: grouping admits them only where
+  // both activations' single launches run it)
+  constexpr bool kTwo = ACT != kActRuntime && bwd_two_pass(S, KC, ACT == 1, true);
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, true> == 2;
   const int n_cu = device_cu_count();
   // each layer's grid as bwd_one forms it (the taps pass has its own)
@@ -353,7 +370,7 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
                            : bwd_grid(p.n_tokens, L[i].D, S);
     ly.l[i] = BwdLayer{L[i].x, L[i].dy, L[i].dys, L[i].a_c, L[i].b_c, L[i].dx, L[i].part_da,
                        L[i].part_db, L[i].D, static_cast<int>(g.gx), static_cast<int>(g.gy),
-                       g.gy1, g.n_old, g.n_total, static_cast<int>(blk)};
+                       g.gy1, g.n_old, g.n_total, static_cast<int>(blk), L[i].act};
     const int64_t tiles = static_cast<int64_t>(g.gx) * g.gy;
     // the dx pass of the two-pass form skips layers without dx (no blocks:
     // layer_index then never selects them)
@@ -397,32 +414,47 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
 
 template <int S>
 void launch_fwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
-  const bool act = p.activation != 0;
-  if (p.K <= 16) {
-    if (act) fwd_layers_one<S, 1, true>(p, L, n, st);
-    else fwd_layers_one<S, 1, false>(p, L, n, st);
-  } else if (p.K <= 32) {
-    if (act) fwd_layers_one<S, 2, true>(p, L, n, st);
-    else fwd_layers_one<S, 2, false>(p, L, n, st);
-  } else {
-    if (act) fwd_layers_one<S, 4, true>(p, L, n, st);
-    else fwd_layers_one<S, 4, false>(p, L, n, st);
+  int mask = 0;
+  for (int i = 0; i < n; ++i) mask |= L[i].kc;
+  const int act = layers_act(L, n);
+#define MOC_FWDL(M_)                                                          \
+  case M_:                                                                    \
+    if constexpr (M_ == 1 || M_ == 2 || M_ == 4) {                            \
+      if (act == 0) fwd_layers_one<S, M_, 0>(p, L, n, st);                    \
+      else if (act == 1) fwd_layers_one<S, M_, 1>(p, L, n, st);               \
+      else fwd_layers_one<S, M_, kActRuntime>(p, L, n, st);                   \
+    } else {                                                                  \
+      fwd_layers_one<S, M_, kActRuntime>(p, L, n, st);                        \
+    }                                                                         \
+    break;
+  switch (mask) {
+    MOC_FWDL(1)
+    MOC_FWDL(2)
+    MOC_FWDL(3)
+    MOC_FWDL(4)
+    MOC_FWDL(5)
+    MOC_FWDL(6)
+    MOC_FWDL(7)
+    default: break;
   }
+#undef MOC_FWDL
 }
 
+// The layers here share their route chunks (L[0].kc).
 template <int S>
 void launch_bwd_layers(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
-  const bool act = p.activation != 0;
-  if (p.K <= 16) {
-    if (act) bwd_layers_one<S, 1, true>(p, L, n, st);
-    else bwd_layers_one<S, 1, false>(p, L, n, st);
-  } else if (p.K <= 32) {
-    if (act) bwd_layers_one<S, 2, true>(p, L, n, st);
-    else bwd_layers_one<S, 2, false>(p, L, n, st);
-  } else {
-    if (act) bwd_layers_one<S, 4, true>(p, L, n, st);
-    else bwd_layers_one<S, 4, false>(p, L, n, st);
+  const int act = layers_act(L, n);
+#define MOC_BWDL(KC_)                                              \
+  if (L[0].kc == KC_) {                                            \
+    if (act == 0) bwd_layers_one<S, KC_, 0>(p, L, n, st);          \
+    else if (act == 1) bwd_layers_one<S, KC_, 1>(p, L, n, st);     \
+    else bwd_layers_one<S, KC_, kActRuntime>(p, L, n, st);         \
+    return;                                                        \
   }
+  MOC_BWDL(1)
+  MOC_BWDL(2)
+  MOC_BWDL(4)
+#undef MOC_BWDL
 }
 
 // Dispatch over (KC, activation, dtype) for one S.

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libmoc_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 ROUTE_ALPHA, ROUTE_SOFTMAX, ROUTE_EXP = 0, 1, 2
@@ -65,7 +65,7 @@ class MocLayer(ctypes.Structure):
         ("y", ctypes.c_void_p), ("dy", ctypes.c_void_p), ("dy_row_stride", ctypes.c_int64),
         ("dx", ctypes.c_void_p), ("dalpha", ctypes.c_void_p), ("dbasis", ctypes.c_void_p),
         ("dim", ctypes.c_int64), ("routing", ctypes.c_int), ("alpha_dtype", ctypes.c_int),
-        ("basis_dtype", ctypes.c_int),
+        ("basis_dtype", ctypes.c_int), ("activation", ctypes.c_int), ("k", ctypes.c_int64),
     ]
 
 
@@ -139,10 +139,12 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_set_kernel_path.restype = _i
     for name in ("moc_forward_layers", "moc_backward_layers"):
         fn = getattr(lib, name)
-        fn.argtypes = [_p, _i, _p, _i, _l, _l, _l, _l, _l, _i, _i, _p, _z, _p]
+        # layers, n_layers, cu_seqlens, cu_seqlens_i64, n_seqs, n_tokens, seq_len,
+        # kernel_size, x_dtype, workspace, bytes, stream
+        fn.argtypes = [_p, _i, _p, _i, _l, _l, _l, _l, _i, _p, _z, _p]
         fn.restype = _i
         q = getattr(lib, name + "_workspace_bytes")
-        q.argtypes = [_p, _i, _l, _l, _l, _i, _i]
+        q.argtypes = [_p, _i, _l, _l, _i]   # layers, n_layers, n_tokens, kernel_size, x_dtype
         q.restype = _z
     lib.moc_update.argtypes = [
         _p, _p, _p, _p,            # x, alpha, basis, cache

@@ -297,11 +297,11 @@ class _MoCGroupFunction(torch.autograd.Function):
             saved_b.append(b)
         flags = [activation_flag(a) for a in acts]
         codes = [_WEIGHTS_CODES[r] for r in routes]
-        # one launch over all layers when they share K, S and the activation
-        together = (len({tuple(b.shape[:2]) for b in saved_b}) == 1 and len(set(flags)) == 1
-                    and len({x.dtype for x in saved_x}) == 1)
+        # one call for all layers when they share S and the dtype (each its own K
+        # and activation)
+        together = len({b.shape[1] for b in saved_b}) == 1 and len({x.dtype for x in saved_x}) == 1
         if together:
-            ys = ops.launch_forward_layers(saved_x, weights, saved_b, activation_flag=flags[0],
+            ys = ops.launch_forward_layers(saved_x, weights, saved_b, activation_flags=flags,
                                            routings=codes, cu_seqlens=cu)
         else:
             ys = [ops.launch_forward(x, w, b, activation_flag=f, cu_seqlens=cu, routing=c)
@@ -322,7 +322,7 @@ class _MoCGroupFunction(torch.autograd.Function):
         dys = [dy if dy is not None else torch.zeros_like(x) for dy, x in zip(dys, xs)]
         need = [ctx.needs_input_grad[2 + n + g] for g in range(n)]
         if together:
-            res = ops.launch_backward_layers(xs, weights, bases, dys, activation_flag=acts[0],
+            res = ops.launch_backward_layers(xs, weights, bases, dys, activation_flags=acts,
                                              routings=codes, need_xs=need, cu_seqlens=cu)
         else:
             res = [ops.launch_backward(x, w, b, dy, activation_flag=f, need_x=nx, cu_seqlens=cu,

@@ -345,37 +345,37 @@ def _layer_table(entries):
     return arr
 
 
-def launch_forward_layers(xs, alphas, bases, *, activation_flag: int, routings,
+def launch_forward_layers(xs, alphas, bases, *, activation_flags, routings,
                           cu_seqlens: torch.Tensor | None = None) -> list[torch.Tensor]:
-    """y of several MoC layers on one token axis (same K, S, activation) in one
-    call: one forward launch over every layer's channels where the library
-    can (bf16 matrix-core layers), the layers one by one otherwise."""
+    """y of several MoC layers on one token axis (same S and dtype; each its own
+    K and activation) in one call: one forward launch over every layer's
+    channels where the library can (bf16 matrix-core layers), the layers one
+    by one otherwise."""
     L = _lib.lib()
     xs = [x.contiguous() for x in xs]
     aa = [_operand(a) for a in alphas]
     bb = [_operand(b) for b in bases]
-    K, S, _ = bb[0].shape
+    S = bb[0].shape[1]
     cu_ptr, cu64, n_seqs, n_tokens, seq_len, _ = _seq_args(xs[0], cu_seqlens)
     ys = [torch.empty_like(x) for x in xs]
     table = _layer_table([dict(x=x.data_ptr(), alpha=a.data_ptr(), basis=b.data_ptr(),
                                y=y.data_ptr(), dim=x.shape[-1], routing=int(r),
                                alpha_dtype=_lib.dtype_code(a.dtype),
-                               basis_dtype=_lib.dtype_code(b.dtype))
-                          for x, a, b, y, r in zip(xs, aa, bb, ys, routings)])
+                               basis_dtype=_lib.dtype_code(b.dtype), activation=int(f),
+                               k=b.shape[0])
+                          for x, a, b, y, r, f in zip(xs, aa, bb, ys, routings, activation_flags)])
     x_dt = _lib.dtype_code(xs[0].dtype)
     dev = xs[0].device
     with _lib.device_guard(dev):
-        nbytes = L.moc_forward_layers_workspace_bytes(table, len(xs), n_tokens, K, S, x_dt,
-                                                      int(activation_flag))
+        nbytes = L.moc_forward_layers_workspace_bytes(table, len(xs), n_tokens, S, x_dt)
         ws = _workspace(nbytes, dev)
-        rc = L.moc_forward_layers(table, len(xs), cu_ptr, cu64, n_seqs, n_tokens, seq_len, K, S,
-                                  x_dt, int(activation_flag), ws.data_ptr(), ws.numel(),
-                                  _lib.stream_ptr(dev))
+        rc = L.moc_forward_layers(table, len(xs), cu_ptr, cu64, n_seqs, n_tokens, seq_len, S,
+                                  x_dt, ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "moc_forward_layers")
     return ys
 
 
-def launch_backward_layers(xs, alphas, bases, dys, *, activation_flag: int, routings, need_xs,
+def launch_backward_layers(xs, alphas, bases, dys, *, activation_flags, routings, need_xs,
                            cu_seqlens: torch.Tensor | None = None):
     """[(dx or None, dalpha, dbasis)] of several MoC layers on one token axis in
     one call (see launch_forward_layers); per layer the results of
@@ -384,7 +384,7 @@ def launch_backward_layers(xs, alphas, bases, dys, *, activation_flag: int, rout
     xs = [x.contiguous() for x in xs]
     aa = [_operand(a) for a in alphas]
     bb = [_operand(b) for b in bases]
-    K, S, _ = bb[0].shape
+    S = bb[0].shape[1]
     cu_ptr, cu64, n_seqs, n_tokens, seq_len, _ = _seq_args(xs[0], cu_seqlens)
     dyo = [dy_operand(dy, x.dtype) for dy, x in zip(dys, xs)]
     dxs = [torch.empty_like(x) if nx else None for x, nx in zip(xs, need_xs)]
@@ -395,18 +395,17 @@ def launch_backward_layers(xs, alphas, bases, dys, *, activation_flag: int, rout
                                dx=None if dx is None else dx.data_ptr(), dalpha=da.data_ptr(),
                                dbasis=db.data_ptr(), dim=x.shape[-1], routing=int(r),
                                alpha_dtype=_lib.dtype_code(a.dtype),
-                               basis_dtype=_lib.dtype_code(b.dtype))
-                          for x, a, b, d, dx, da, db, r in zip(xs, aa, bb, dyo, dxs, das, dbs,
-                                                               routings)])
+                               basis_dtype=_lib.dtype_code(b.dtype), activation=int(f),
+                               k=b.shape[0])
+                          for x, a, b, d, dx, da, db, r, f in zip(xs, aa, bb, dyo, dxs, das, dbs,
+                                                                  routings, activation_flags)])
     x_dt = _lib.dtype_code(xs[0].dtype)
     dev = xs[0].device
     with _lib.device_guard(dev):
-        nbytes = L.moc_backward_layers_workspace_bytes(table, len(xs), n_tokens, K, S, x_dt,
-                                                       int(activation_flag))
+        nbytes = L.moc_backward_layers_workspace_bytes(table, len(xs), n_tokens, S, x_dt)
         ws = _workspace(nbytes, dev)
-        rc = L.moc_backward_layers(table, len(xs), cu_ptr, cu64, n_seqs, n_tokens, seq_len, K, S,
-                                   x_dt, int(activation_flag), ws.data_ptr(), ws.numel(),
-                                   _lib.stream_ptr(dev))
+        rc = L.moc_backward_layers(table, len(xs), cu_ptr, cu64, n_seqs, n_tokens, seq_len, S,
+                                   x_dt, ws.data_ptr(), ws.numel(), _lib.stream_ptr(dev))
     _lib.check(rc, "moc_backward_layers")
     out = []
     for dx, da, db, a, b in zip(dxs, das, dbs, alphas, bases):

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_lib.EXPORTED_SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.moc_abi_version() == _lib.ABI_VERSION == 4
+    assert L.moc_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_header_constants_match_binding():
@@ -172,7 +172,7 @@ def test_backward_noalloc_rejects_before_touching_the_device():
     assert small <= _lib.NOALLOC_SCRATCH_BYTES    # the headline shape fits
 
 
-def _layers(dims, **kw):
+def _layers(dims, k=32, activation=0, **kw):
     arr = (_lib.MocLayer * max(len(dims), 1))()
     for i, d in enumerate(dims):
         arr[i].x = arr[i].alpha = arr[i].basis = arr[i].y = FAKE
@@ -181,17 +181,18 @@ def _layers(dims, **kw):
         arr[i].dim = d
         arr[i].routing = 3
         arr[i].alpha_dtype = arr[i].basis_dtype = _lib.DT_BF16
-        for k, v in kw.items():
-            setattr(arr[i], k, v)
+        arr[i].k = k[i] if isinstance(k, list) else k
+        arr[i].activation = activation[i] if isinstance(activation, list) else activation
+        for name, v in kw.items():
+            setattr(arr[i], name, v)
     return arr
 
 
 def test_layer_entries_validate_and_size():
     """moc_*_layers: argument checks before any launch; grouped bf16 layers need
-    the per-layer workspaces side by side."""
+    the per-layer workspaces side by side, each sized for its own k."""
     L = _lib.lib()
     dims = [4096, 1024, 1024]
-    arr = _layers(dims)
     N, K, S = 16384, 32, 8
     for which in ("forward", "backward"):
         q = getattr(L, f"moc_{which}_layers_workspace_bytes")
@@ -201,20 +202,27 @@ def test_layer_entries_validate_and_size():
         # taps pass, which the grouped backward (the fused pass) does not
         total = sum(single(N, d, K, S, _lib.DT_BF16, 3) for d in dims)
         if which == "forward":
-            assert q(arr, 3, N, K, S, _lib.DT_BF16, 1) == total
+            assert q(_layers(dims, activation=1), 3, N, S, _lib.DT_BF16) == total
         else:
-            assert 0 < q(arr, 3, N, K, S, _lib.DT_BF16, 1) <= total
-        assert q(arr, 3, N, K, S, _lib.DT_BF16, 0) <= total
-        assert q(arr, 0, N, K, S, _lib.DT_BF16, 0) == 0
+            assert 0 < q(_layers(dims, activation=1), 3, N, S, _lib.DT_BF16) <= total
+        assert q(_layers(dims), 3, N, S, _lib.DT_BF16) <= total
+        assert q(_layers(dims), 0, N, S, _lib.DT_BF16) == 0
+        ks = [16, 32, 64]
+        mixed = sum(single(N, d, k, S, _lib.DT_BF16, 3) for d, k in zip(dims, ks))
+        if which == "forward":
+            assert q(_layers(dims, k=ks, activation=[1, 0, 1]), 3, N, S, _lib.DT_BF16) == mixed
+        arr = _layers(dims)
         fn = getattr(L, f"moc_{which}_layers")
-        assert fn(arr, 5, None, 0, 0, N, N, K, S, 1, 0, FAKE, 1 << 40, None) == -1
+        assert fn(arr, 5, None, 0, 0, N, N, S, 1, FAKE, 1 << 40, None) == -1
         assert b"n_layers" in L.moc_last_error()
-        assert fn(arr, 3, None, 0, 0, N, N, K, S, 1, 0, FAKE, 16, None) == -3
-    bad = _layers([64, 64], dy_row_stride=7)
-    assert L.moc_backward_layers(bad, 2, None, 0, 0, 8, 8, 16, 4, 1, 0, FAKE, 1 << 30, None) == -1
+        assert fn(arr, 3, None, 0, 0, N, N, S, 1, FAKE, 16, None) == -3
+        assert fn(_layers(dims, k=0), 3, None, 0, 0, N, N, S, 1, FAKE, 1 << 40, None) == -1
+        assert fn(_layers(dims, activation=2), 3, None, 0, 0, N, N, S, 1, FAKE, 1 << 40, None) == -1
+    bad = _layers([64, 64], k=16, dy_row_stride=7)
+    assert L.moc_backward_layers(bad, 2, None, 0, 0, 8, 8, 4, 1, FAKE, 1 << 30, None) == -1
     assert b"dy_row_stride" in L.moc_last_error()
-    nul = _layers([64], dalpha=None)
-    assert L.moc_backward_layers(nul, 1, None, 0, 0, 8, 8, 16, 4, 1, 0, FAKE, 1 << 30, None) == -1
+    nul = _layers([64], k=16, dalpha=None)
+    assert L.moc_backward_layers(nul, 1, None, 0, 0, 8, 8, 4, 1, FAKE, 1 << 30, None) == -1
     assert b"null" in L.moc_last_error()
 
 

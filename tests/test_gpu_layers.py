@@ -1,9 +1,11 @@
 """Grouped layer launches (moc_forward_layers / moc_backward_layers) against the
 single-layer entries, through the C ABI: every layer's y, dx, dalpha and dbasis
 bit for bit.  The grouped kernels run each layer's own grid inside one launch,
-so each workgroup does exactly the work of the single-layer launch; layers that
-cannot share one launch (fp32, or the generic kernels) run one by one inside
-the same entry."""
+so each workgroup does exactly the work of the single-layer launch; layers may
+differ in K and activation (one forward launch; one backward stage-1 launch
+per route count, and per activation where the layers without one run the
+two-pass form); layers that cannot share one launch (fp32, or the generic
+kernels) run one by one inside the same entry."""
 from __future__ import annotations
 
 import itertools
@@ -17,7 +19,8 @@ from tests._parity import gen, randn
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
-# (layer dims, K, S, activation, routing codes, need_x per layer, dtype)
+# (layer dims, K, S, activation, routing codes, need_x per layer, dtype); K and
+# the activation are one value for every layer or a list with one per layer
 CASES = [
     ([512, 256, 128], 16, 4, 1, [3, 4, 3], [True, True, True], torch.bfloat16),   # fused, tiered
     ([512, 128, 128], 32, 8, 0, [4, 4, 3], [True, False, True], torch.bfloat16),  # dx + taps passes
@@ -30,30 +33,45 @@ CASES = [
     ([256, 128], 32, 6, 0, [4, 3], [True, False], torch.bfloat16),               # 6 taps, two passes
     ([192, 64], 32, 4, 0, [0, 4], [True, True], torch.bfloat16),                  # 4 taps, two passes
     ([128, 64], 16, 8, 0, [0, 3], [True, True], torch.bfloat16),                  # 16 routes, two passes
+    # per-layer activation and K
+    ([512, 256, 128], 16, 4, [1, 0, 1], [3, 4, 3], [True, True, False], torch.bfloat16),  # four-wave pass
+    ([256, 128], 16, 6, [1, 0], [3, 0], [True, True], torch.bfloat16),           # fused pass, 6 taps
+    ([256, 192], 32, 3, [0, 1], [4, 3], [True, True], torch.bfloat16),           # route halves
+    ([256, 128, 192], [16, 32, 16], 4, [1, 0, 0], [3, 4, 0], [True, True, True],
+     torch.bfloat16),                                                            # 16 | 32 (two passes)
+    ([128, 256], [16, 32], 3, [0, 1], [0, 3], [False, True], torch.bfloat16),    # 16 | 32 with SiLU
+    ([128, 64, 96], [32, 16, 12], 5, [1, 1, 0], [3, 3, 4], [True, True, True], torch.bfloat16),
+    ([128, 64], 32, 8, [0, 1], [3, 3], [True, True], torch.bfloat16),            # one by one (SiLU two passes)
 ]
+
+
+def _per_layer(v, n):
+    return list(v) if isinstance(v, (list, tuple)) else [v] * n
 
 
 def _inputs(dims, K, S, dtype, lead, seed):
     g = gen(seed)
+    ks = _per_layer(K, len(dims))
     xs = [randn(g, *lead, D, scale=0.5).to(DEV, dtype) for D in dims]
-    ws = [torch.softmax(randn(g, *lead, K), -1).to(DEV, dtype) for _ in dims]
-    bs = [randn(g, K, S, D, scale=0.1).to(DEV, dtype) for D in dims]
+    ws = [torch.softmax(randn(g, *lead, k), -1).to(DEV, dtype) for k in ks]
+    bs = [randn(g, k, S, D, scale=0.1).to(DEV, dtype) for k, D in zip(ks, dims)]
     dys = [randn(g, *lead, D).to(DEV, dtype) for D in dims]
     return xs, ws, bs, dys
 
 
 def _check(dims, K, S, act, codes, need, dtype, lead, cu=None, generic=False):
-    xs, ws, bs, dys = _inputs(dims, K, S, dtype, lead, sum(dims) + K + S)
+    xs, ws, bs, dys = _inputs(dims, K, S, dtype, lead, sum(dims) + sum(_per_layer(K, 1)) + S)
+    acts = _per_layer(act, len(dims))
     ctx = _lib.kernel_path(_lib.PATH_GENERIC) if generic else _lib.kernel_path(_lib.PATH_AUTO)
     with ctx:
-        ys = ops.launch_forward_layers(xs, ws, bs, activation_flag=act, routings=codes,
+        ys = ops.launch_forward_layers(xs, ws, bs, activation_flags=acts, routings=codes,
                                        cu_seqlens=cu)
-        grads = ops.launch_backward_layers(xs, ws, bs, dys, activation_flag=act, routings=codes,
+        grads = ops.launch_backward_layers(xs, ws, bs, dys, activation_flags=acts, routings=codes,
                                            need_xs=need, cu_seqlens=cu)
         for i in range(len(dims)):
-            y1 = ops.launch_forward(xs[i], ws[i], bs[i], activation_flag=act, routing=codes[i],
+            y1 = ops.launch_forward(xs[i], ws[i], bs[i], activation_flag=acts[i], routing=codes[i],
                                     cu_seqlens=cu)
-            g1 = ops.launch_backward(xs[i], ws[i], bs[i], dys[i], activation_flag=act,
+            g1 = ops.launch_backward(xs[i], ws[i], bs[i], dys[i], activation_flag=acts[i],
                                      need_x=need[i], routing=codes[i], cu_seqlens=cu)
             assert torch.equal(ys[i], y1), f"y[{i}]"
             assert (grads[i][0] is None) == (not need[i])
@@ -67,7 +85,7 @@ def test_layers_match_single_layer_entries(dims, K, S, act, codes, need, dtype):
     _check(dims, K, S, act, codes, need, dtype, (3, 211))
 
 
-@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3])
+@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3] + CASES[11:15])
 def test_layers_match_single_layer_entries_packed(dims, K, S, act, codes, need, dtype):
     lengths = [1, 90, 3, 250, 17, 199, 73]
     cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int32, device=DEV)
@@ -84,7 +102,7 @@ def test_layers_broadcast_dy():
     dims, K, S = [256, 128], 16, 4
     xs, ws, bs, _ = _inputs(dims, K, S, torch.bfloat16, (2, 300), 5)
     dys = [torch.ones((), device=DEV, dtype=torch.bfloat16).expand(2, 300, D) for D in dims]
-    got = ops.launch_backward_layers(xs, ws, bs, dys, activation_flag=1, routings=[3, 3],
+    got = ops.launch_backward_layers(xs, ws, bs, dys, activation_flags=[1, 1], routings=[3, 3],
                                      need_xs=[True, True])
     for i in range(2):
         ref = ops.launch_backward(xs[i], ws[i], bs[i], torch.ones_like(xs[i]), activation_flag=1,

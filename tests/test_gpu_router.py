@@ -180,28 +180,43 @@ def test_router_forward_routed_weights(K, route):
 
 
 def _qkv_layers(specs, Z, seed):
-    """MoC layers (dim, k, S, activation, router_activation) on one z_dim, bf16."""
+    """MoC layers (dim, k, S, activation, router_activation) on one z_dim, bf16;
+    router and basis drawn from the seeded generator."""
     g = gen(seed)
     layers = []
     for D, K, S, act, route in specs:
         m = MoC(D, Z, S, K, activation=act, init_std=0.1, router_activation=route)
         with torch.no_grad():
             m.router.copy_(randn(g, K, Z, scale=0.05))
+            m.conv_bases.copy_(randn(g, K, S, D, scale=0.1))
         layers.append(m.to(DEV, BF))
     return layers, g
 
 
+def _bf16_ulp(t):
+    a = t.detach().float().abs().clamp_min(2.0 ** -126)
+    return torch.pow(2.0, torch.floor(torch.log2(a)) - 7)
+
+
 def _run_layers(layers, xs, z, dys, grouped, **kw):
+    """Outputs and gradients; separately (grouped False) each layer gets its own
+    z leaf, and dz is their fp32 sum with, as a second value, the rounding of
+    the per-layer bf16 dz (half an ulp each) as an allowance."""
     for m in layers:
         m.zero_grad(set_to_none=True)
     xi = [x.clone().requires_grad_() for x in xs]
-    zi = z.clone().requires_grad_()
     if grouped:
+        zi = z.clone().requires_grad_()
         outs = moc.MoCGroup(*layers)(xi, zi, **kw)
     else:
-        outs = [m(x, zi, **kw) for m, x in zip(layers, xi)]
+        zs = [z.clone().requires_grad_() for _ in layers]
+        outs = [m(x, zl, **kw) for m, x, zl in zip(layers, xi, zs)]
     torch.autograd.backward([y for y, _ in outs], dys)
-    return ([y.detach() for y, _ in outs], [x.grad for x in xi], zi.grad,
+    if grouped:
+        dz = zi.grad
+    else:
+        dz = (sum(zl.grad.float() for zl in zs), sum(0.5 * _bf16_ulp(zl.grad) for zl in zs))
+    return ([y.detach() for y, _ in outs], [x.grad for x in xi], dz,
             [m.router.grad.clone() for m in layers], [m.conv_bases.grad.clone() for m in layers])
 
 
@@ -212,21 +227,24 @@ QKV_SPECS = [
     [(192, 16, 4, "silu", "softmax"), (128, 20, 3, None, "exp")],
     [(128, 8, 2, "silu", "softmax"), (64, 4, 4, None, "exp"), (64, 12, 4, None, "softmax"),
      (32, 32, 8, "silu", "exp")],
+    # one S, each layer its own K and activation (one grouped call)
+    [(192, 16, 4, "silu", "softmax"), (128, 32, 4, None, "exp"), (64, 12, 4, "silu", "softmax")],
+    [(256, 32, 6, None, "exp"), (64, 16, 6, "silu", "exp"), (128, 16, 6, None, "softmax")],
 ]
 
 
 @pytest.mark.parametrize("specs", QKV_SPECS)
 @pytest.mark.parametrize("varlen", [False, True])
 def test_group_matches_separate_layers(specs, varlen):
-    """MoCGroup (one router pass over the concatenated routers, one forward and
-    one backward launch over all layers when they share K, S and activation,
-    one router backward) against the same layers called one by one: y, dx,
+    """MoCGroup (one router pass over the concatenated routers, one grouped
+    forward and backward call over all layers when they share S, one router
+    backward) against the same layers called one by one: y, dx,
     drouter and dbasis bit for bit (every workgroup does the work of its own
     layer's launch, same reduction order); dz, which the group sums over all
-    routes in fp32 while autograd adds the layers' bf16 dz, within the bf16
-    rule."""
+    routes in fp32 and rounds once, against the fp32 sum of the layers' own bf16
+    dz, within the bf16 rule plus half an ulp of each rounding."""
     Z, B, T = 128, 2, 61
-    layers, g = _qkv_layers(specs, Z, len(specs) * 10 + varlen)
+    layers, g = _qkv_layers(specs, Z, sum(s[0] + s[1] for s in specs) + 10 * len(specs) + varlen)
     if varlen:
         lengths = [5, 40, 1, 70, 7]
         cu = torch.tensor([0] + list(torch.tensor(lengths).cumsum(0)), dtype=torch.int32,
@@ -244,7 +262,8 @@ def test_group_matches_separate_layers(specs, varlen):
                        ("dbasis", got[4], ref[4])):
         for i, (u, v) in enumerate(zip(a, b)):
             assert torch.equal(u, v), f"{name}[{i}]"
-    assert_close("dz", got[2], ref[2].float(), BF)
+    ref_dz, rounding = ref[2]
+    assert_close("dz", got[2], ref_dz, BF, extra=rounding + 0.5 * _bf16_ulp(ref_dz))
 
 
 def test_group_falls_back_to_layers():
