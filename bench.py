@@ -13,6 +13,8 @@ inputs already resident in HBM.  Printed as one JSON line:
   prefill       a headline-shape chunk continuing from a cache (bench_prefill)
   config3_varlen, config5_qkv  BASELINE configs[2] and configs[4] (the
                 `--config 3` / `--config 5` measurements)
+  shapes        forward / backward entry us at other kernel sizes (8, 12, 16
+                taps) and an even channel count that is not a multiple of 4
   decode        configs[3]: batch-256 single-token steps: us per MoC.step call
                 (host-synchronised each step, and back to back), per MoC.step
                 replayed from a HIP graph, and per launch of the one-launch
@@ -216,6 +218,46 @@ def entry_calls(dev, rotate=ROTATE):
     return fwd, bwd
 
 
+SHAPES = (("bf16 S4 D2048", torch.bfloat16, 4, 2048), ("bf16 S4 D2050", torch.bfloat16, 4, 2050),
+          ("bf16 S8 D2048", torch.bfloat16, 8, 2048), ("bf16 S12 D2048", torch.bfloat16, 12, 2048),
+          ("bf16 S16 D2048", torch.bfloat16, 16, 2048), ("fp32 S8 D2048", torch.float32, 8, 2048),
+          ("fp32 S12 D2048", torch.float32, 12, 2048))
+
+
+def shape_calls(dev):
+    """Forward and backward entries (moc_forward / moc_backward) at the headline
+    token count (B 4 x T 4096), K 16, SiLU, softmax weights given, full dy, for
+    the kernel sizes and channel counts of SHAPES: the headline shape, an even
+    channel count that is not a multiple of 4, and 8 / 12 / 16 taps (bf16 and
+    fp32).  Returns [(label, fwd, bwd)]."""
+    from moc import ops
+    from moc._lib import ROUTE_SOFTMAX_WEIGHTS
+    B, T, K = CFG["B"], CFG["T"], CFG["K"]
+    out = []
+    for label, dt, S, D in SHAPES:
+        g = torch.Generator().manual_seed(S * 10000 + D)
+        x = torch.randn(B, T, D, generator=g).to(dev, dt)
+        w = torch.softmax(torch.randn(B, T, K, generator=g), -1).to(dev, dt)
+        b = ((torch.rand(K, S, D, generator=g) * 2 - 1) * 0.002 * 3 ** 0.5).to(dev, dt)
+        dy = torch.randn(B, T, D, generator=g).to(dev, dt)
+        out.append((label,
+                    lambda x=x, w=w, b=b: ops.launch_forward(x, w, b, activation_flag=1,
+                                                             routing=ROUTE_SOFTMAX_WEIGHTS),
+                    lambda x=x, w=w, b=b, dy=dy: ops.launch_backward(
+                        x, w, b, dy, activation_flag=1, need_x=True, routing=ROUTE_SOFTMAX_WEIGHTS)))
+    return out
+
+
+def bench_shapes(dev, steps, warmup):
+    """us per forward / backward entry for each of shape_calls."""
+    res = {}
+    for label, fwd, bwd in shape_calls(dev):
+        res[label] = {"fwd_us": round(time_region(fwd, steps, warmup) * 1e3, 2),
+                      "bwd_us": round(time_region(bwd, steps, warmup) * 1e3, 2)}
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_prefill(dev, steps, warmup, rotate=ROTATE):
     """A chunk of the headline layer shape continuing from a cache (chunked
     prefill, moc/api.py:299-309): B=4 x T=4096 new tokens per sequence at D=2048,
@@ -296,6 +338,8 @@ def counter_run(dev, which, reps=3):
       decode     the one-launch decode step of configs[3] (batch 256);
       update     moc_update at configs[3]'s layer shape in the four forms of
                  update_calls (matrix-core and generic decode kernels);
+      shapes     the forward and backward entries of shape_calls (other kernel
+                 sizes and channel counts at the headline token count);
       c3         the configs[2] varlen layer step (config3_step);
       c5         the configs[4] QKV triple step through MoCGroup;
       prefill    a headline-shape chunk continuing from a cache: the module
@@ -325,6 +369,12 @@ def counter_run(dev, which, reps=3):
         fn = decode_step_call(dev)
     elif which == "update":
         calls = [f for _, f in update_calls(dev)]
+
+        def fn():
+            for f in calls:
+                f()
+    elif which == "shapes":
+        calls = [f for _, fw, bw in shape_calls(dev) for f in (fw, bw)]
 
         def fn():
             for f in calls:
@@ -690,8 +740,8 @@ def main():
     ap.add_argument("--rotate", type=int, default=ROTATE,
                     help="input sets the timed loops cycle through (1: one set reused, "
                          "which the last-level cache partly holds across steps)")
-    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "update", "c3", "c5", "prefill",
-                                           "copy"),
+    ap.add_argument("--counters", choices=("fwd", "bwd", "step", "decode", "update", "shapes", "c3", "c5",
+                                           "prefill", "copy"),
                     default=None,
                     help="only run --reps calls of one workload (see counter_run) for a "
                          "rocprofv3 --pmc or --kernel-trace pass; prints no JSON")
@@ -762,6 +812,8 @@ def main():
         out["prefill"] = bench_prefill(dev, min(args.steps, 20), min(args.warmup, 5), args.rotate)
     if not args.no_decode:
         out["decode"] = bench_decode(dev)
+    if not args.no_configs:
+        out["shapes"] = bench_shapes(dev, min(args.steps, 20), min(args.warmup, 5))
     if not args.no_configs:
         # BASELINE configs[2] (varlen) and configs[4] (QKV triple), as the
         # `--config 3` / `--config 5` lines report them

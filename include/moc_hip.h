@@ -80,15 +80,17 @@ const char* moc_last_error(void);
 int moc_set_kernel_path(int path);
 
 /*
- * 1 when moc_forward / moc_backward run the matrix-core kernels for a problem
- * of this shape and x dtype (under the current moc_set_kernel_path), 0 when
- * they run the generic kernels.  No counterpart in the reference, whose Triton
- * kernels take every shape; it lets a caller or a test see which family serves
- * a shape.  Matrix-core shapes: 2 <= kernel_size <= 8; k <= 32 (k <= 64 with a
- * bf16 x); dim even; x bf16 or f32.
+ * 1 when moc_forward (backward = 0) or moc_backward (backward = 1) runs the
+ * matrix-core kernels for a problem of this shape and x dtype (under the
+ * current moc_set_kernel_path), 0 when it runs the generic kernels.  No
+ * counterpart in the reference, whose Triton kernels take every shape; it lets
+ * a caller or a test see which family serves a shape.  Matrix-core forward:
+ * 2 <= kernel_size <= 16; k <= 32 (k <= 64 with a bf16 x); dim even; x bf16 or
+ * f32.  Backward: the same with kernel_size <= 8, and for bf16 x with k <= 16
+ * up to kernel_size 16.
  */
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
-                              int x_dtype);
+                              int x_dtype, int backward);
 
 /*
  * Sequence description shared by forward / backward:

@@ -121,13 +121,18 @@ bool use_mfma(const moc::Problem& p) {
   if (p.path == MOC_PATH_GENERIC) return false;
   return moc::mfma::supported(p);
 }
+// the backward's family (the matrix-core backward covers fewer shapes)
+bool use_mfma_bwd(const moc::Problem& p) {
+  if (p.path == MOC_PATH_GENERIC) return false;
+  return moc::mfma::bwd_supported(p);
+}
 
 size_t forward_bytes(const moc::Problem& p) {
   return use_mfma(p) ? moc::mfma::forward_workspace(p) : fwd_bytes(p.n_tokens, p.D, p.K, p.S);
 }
 
 size_t backward_bytes(const moc::Problem& p) {
-  return use_mfma(p) ? moc::mfma::backward_workspace(p) : bwd_bytes(p);
+  return use_mfma_bwd(p) ? moc::mfma::backward_workspace(p) : bwd_bytes(p);
 }
 
 int hip_status(const char* what) {
@@ -248,7 +253,7 @@ int backward_problem(const void* x, const void* alpha, const void* basis, const 
 int backward_launch(const moc::Problem& p, const void* x, const void* alpha, const void* basis,
                     const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
                     hipStream_t st) {
-  if (use_mfma(p)) {
+  if (use_mfma_bwd(p)) {
     moc::mfma::backward(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
     return hip_status("moc_backward launch");
   }
@@ -348,12 +353,12 @@ int moc_backward_noalloc(const void* x, const void* alpha, const void* basis, co
 // Prefill from a cache (fixed-length sequences, MFMA kernels).
 
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
-                              int x_dtype) {
+                              int x_dtype, int backward) {
   if (n_tokens <= 0 || dim <= 0 || k <= 0 || kernel_size <= 0) return 0;
   if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return use_mfma(p) ? 1 : 0;
+  return (backward ? use_mfma_bwd(p) : use_mfma(p)) ? 1 : 0;
 }
 
 int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,
@@ -362,7 +367,7 @@ int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t 
   if (n_seqs > kMaxTokens / seq_len) return 0;
   moc::Problem p = make_problem(nullptr, 0, n_seqs, n_seqs * seq_len, seq_len, dim, k,
                                 kernel_size, x_dtype, MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return use_mfma(p) && moc::mfma::prefill_supported(p, with_cache != 0) ? 1 : 0;
+  return use_mfma_bwd(p) && moc::mfma::prefill_supported(p, with_cache != 0) ? 1 : 0;
 }
 
 }  // extern "C"
@@ -386,7 +391,7 @@ int prefill_problem(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k, int
   p = make_problem(nullptr, 0, n_seqs, n_tokens, seq_len, dim, k, kernel_size, x_dtype,
                    alpha_dtype, basis_dtype, activation, routing);
   p.pre = true;
-  if (!use_mfma(p) || !moc::mfma::prefill_supported(p, has_cache))
+  if (!use_mfma_bwd(p) || !moc::mfma::prefill_supported(p, has_cache))
     return fail(MOC_ERR_ARG,
                 "prefill not supported for this problem (seq_len %lld, dim %lld, k %lld, "
                 "kernel_size %lld%s); see moc_prefill_supported",
@@ -482,7 +487,7 @@ int layer_problems(const MocLayer* layers, int n_layers, const void* cu, int cu6
 
 bool grouped(const moc::Problem* ps, int n, bool backward) {
   for (int i = 0; i < n; ++i)
-    if (!use_mfma(ps[i])) return false;
+    if (!(backward ? use_mfma_bwd(ps[i]) : use_mfma(ps[i]))) return false;
   return moc::mfma::layers_grouped(ps, n, backward);
 }
 

@@ -52,9 +52,12 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st);
 
-// MFMA path (moc_mfma_common.hip): 2 <= S <= 8, K <= 64, D % 4 == 0
+// MFMA path (moc_mfma_common.hip): supported() for the forward (2 <= S <= 16,
+// K <= 32 or <= 64 with bf16 x, D even), bwd_supported() for the backward (the
+// same with S <= 8, or bf16 with K <= 16 up to S = 16)
 namespace mfma {
 bool supported(const Problem& p);
+bool bwd_supported(const Problem& p);
 size_t forward_workspace(const Problem& p);
 size_t backward_workspace(const Problem& p);
 void forward(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,

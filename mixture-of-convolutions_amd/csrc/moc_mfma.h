@@ -1284,12 +1284,15 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       // kc0 = 0 workgroups only)
       if (DO_DX && dx != nullptr && kc0 == 0) {
         // g of the S-1 rows after this lane's run: first rows of lane group q+1
+        // (row R + e of this lane's run is row e % R of lane group q + 1 + e / R:
+        // past 9 taps the rows of two later groups)
         float gf[S - 1][NC];
-        const int src_lane = (lane + 16) & 63;
 #pragma unroll
-        for (int e = 0; e < S - 1; ++e)
+        for (int e = 0; e < S - 1; ++e) {
+          const int src_lane = (lane + 16 * (1 + e / R)) & 63;
 #pragma unroll
-          for (int c = 0; c < NC; ++c) gf[e][c] = __shfl(g[e][c], src_lane, 64);
+          for (int c = 0; c < NC; ++c) gf[e][c] = __shfl(g[e % R][c], src_lane, 64);
+        }
         float dxa[R][NC];
 #pragma unroll
         for (int r = 0; r < R; ++r)

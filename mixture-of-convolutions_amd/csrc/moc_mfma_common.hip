@@ -400,7 +400,7 @@ void launch_stage2(const Problem& p, const Plan& pl, bool dir, char* ws, const v
 }  // namespace
 
 bool supported(const Problem& p) {
-  const bool s_ok = p.S >= 2 && p.S <= 8;
+  const bool s_ok = p.S >= 2 && p.S <= 16;
   // the grids' y dimensions stay within the 65535 launch limit and one
   // super-block's rows within a buffer's 32-bit range; D even: a lane's two
   // channels are both in or both past the channel axis, and its 2-channel
@@ -408,6 +408,11 @@ bool supported(const Problem& p) {
   return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && p.x_dt == DT_BF16)) && p.D % 2 == 0 && p.D <= (int64_t(1) << 20) &&
          (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
          bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D, p.S).gy <= 65535;
+}
+
+// 9 to 16 taps: the backward for bf16 with up to 16 routes (the two-pass form)
+bool bwd_supported(const Problem& p) {
+  return supported(p) && (p.S <= 8 || (p.x_dt == DT_BF16 && p.K <= 16));
 }
 
 size_t forward_workspace(const Problem& p) { return plan(p, false).total; }
@@ -434,6 +439,14 @@ void forward(const Problem& p, const void* x, const void* alpha, const void* bas
     case 6: launch_fwd<6>(p, x, a_c, b_c, y, st); break;
     case 7: launch_fwd<7>(p, x, a_c, b_c, y, st); break;
     case 8: launch_fwd<8>(p, x, a_c, b_c, y, st); break;
+    case 9: launch_fwd<9>(p, x, a_c, b_c, y, st); break;
+    case 10: launch_fwd<10>(p, x, a_c, b_c, y, st); break;
+    case 11: launch_fwd<11>(p, x, a_c, b_c, y, st); break;
+    case 12: launch_fwd<12>(p, x, a_c, b_c, y, st); break;
+    case 13: launch_fwd<13>(p, x, a_c, b_c, y, st); break;
+    case 14: launch_fwd<14>(p, x, a_c, b_c, y, st); break;
+    case 15: launch_fwd<15>(p, x, a_c, b_c, y, st); break;
+    case 16: launch_fwd<16>(p, x, a_c, b_c, y, st); break;
     default: break;
   }
   prof_end(p, st);
@@ -464,6 +477,14 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
     case 6: launch_bwd<6>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
     case 7: launch_bwd<7>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
     case 8: launch_bwd<8>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 9: launch_bwd<9>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 10: launch_bwd<10>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 11: launch_bwd<11>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 12: launch_bwd<12>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 13: launch_bwd<13>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 14: launch_bwd<14>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 15: launch_bwd<15>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
+    case 16: launch_bwd<16>(p, x, dy, a_c, b_c, dx, pda, pdb, gb, st); break;
     default: break;
   }
   prof_end(p, st);
@@ -471,7 +492,8 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
 }
 
 bool prefill_supported(const Problem& p, bool has_cache) {
-  if (!supported(p) || p.seq.cu != nullptr || p.seq.seq_len <= 0 ||
+  // (prefill kernels are built for 2 to 8 taps)
+  if (!bwd_supported(p) || p.S > 8 || p.seq.cu != nullptr || p.seq.seq_len <= 0 ||
       p.n_tokens % p.seq.seq_len != 0)
     return false;
   if (has_cache && p.seq.seq_len < p.S - 1) return false;
@@ -588,7 +610,8 @@ bool layers_grouped(const Problem* ps, int n, bool backward) {
   if (n < 1 || n > kMaxLayers) return false;
   for (int i = 0; i < n; ++i) {
     const Problem& p = ps[i];
-    if (!supported(p) || p.x_dt != DT_BF16) return false;
+    // (grouped kernels are built for 2 to 8 taps)
+    if (!supported(p) || p.x_dt != DT_BF16 || p.S > 8) return false;
     if (p.S != ps[0].S || p.n_tokens != ps[0].n_tokens || p.path != ps[0].path) return false;
   }
   // the backward shapes whose single launch runs a two-pass form the grouped

@@ -485,6 +485,15 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
                 void* dx, float* part_da, float* part_db, float* gbuf, hipStream_t st) {
   const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
+  // 9 to 16 taps: bf16 with up to 16 routes (its two-pass form; the others
+  // spill past what the compiler handles, or past the LDS, and stay generic:
+  // bwd_supported)
+  if constexpr (S > 8) {
+    if (kc == 1 && bf) {
+      if (act) bwd_one<S, 1, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+      else bwd_one<S, 1, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+    }
+  } else {
 #define MOC_BWD(KC_)                                                                          \
   if (kc == KC_) {                                                                            \
     if (bf) {                                                                                 \
@@ -500,6 +509,7 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
   MOC_BWD(2)
   MOC_BWD(4)
 #undef MOC_BWD
+  }
 }
 
 // Prefill from a cache (Pre, fixed-length sequences): the forward on
@@ -639,6 +649,21 @@ MOC_DECLARE_S(6)
 MOC_DECLARE_S(7)
 MOC_DECLARE_S(8)
 #undef MOC_DECLARE_S
+// 9 to 16 taps: the single-layer forward and backward only
+#define MOC_DECLARE_S_LONG(S_)                                                                \
+  extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
+                                      void*, hipStream_t);                                    \
+  extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
+                                      const void*, void*, float*, float*, float*, hipStream_t);
+MOC_DECLARE_S_LONG(9)
+MOC_DECLARE_S_LONG(10)
+MOC_DECLARE_S_LONG(11)
+MOC_DECLARE_S_LONG(12)
+MOC_DECLARE_S_LONG(13)
+MOC_DECLARE_S_LONG(14)
+MOC_DECLARE_S_LONG(15)
+MOC_DECLARE_S_LONG(16)
+#undef MOC_DECLARE_S_LONG
 
 }  // namespace mfma
 }  // namespace moc

@@ -1,0 +1,14 @@
+// MFMA forward / backward kernels instantiated for kernel size S = 11 (single
+// launches; the grouped and prefill entries take 2 to 8 taps).
+#include "moc_mfma_launch.h"
+
+namespace moc {
+namespace mfma {
+
+template void launch_fwd<11>(const Problem&, const void*, const void*, const void*, void*,
+                              hipStream_t);
+template void launch_bwd<11>(const Problem&, const void*, const void*, const void*, const void*,
+                              void*, float*, float*, float*, hipStream_t);
+
+}  // namespace mfma
+}  // namespace moc

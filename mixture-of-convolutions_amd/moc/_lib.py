@@ -110,7 +110,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.moc_backward.restype = _i
     lib.moc_backward_noalloc.argtypes = bwd + [_p]   # stream
     lib.moc_backward_noalloc.restype = _i
-    lib.moc_matrix_core_supported.argtypes = [_l, _l, _l, _l, _i]
+    lib.moc_matrix_core_supported.argtypes = [_l, _l, _l, _l, _i, _i]
     lib.moc_matrix_core_supported.restype = _i
     lib.moc_prefill_supported.argtypes = [_l, _l, _l, _l, _l, _i, _i]
     lib.moc_prefill_supported.restype = _i

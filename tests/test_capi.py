@@ -244,22 +244,31 @@ def _pre_bwd(**kw):
 
 def test_matrix_core_supported_names_the_kernel_family():
     """moc_matrix_core_supported: 1 for the shapes the matrix-core kernels are
-    built for (2-8 taps; up to 32 routes, 64 with bf16 x; an even channel
-    count), 0 elsewhere and while the generic family is forced."""
+    built for (forward: 2-16 taps, up to 32 routes or 64 with bf16 x, an even
+    channel count; backward: the same up to 8 taps, and bf16 with up to 16
+    routes up to 16 taps), 0 elsewhere and while the generic family is forced."""
     L = _lib.lib()
     bf, f32 = _lib.DT_BF16, _lib.DT_F32
-    assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf) == 1
-    assert L.moc_matrix_core_supported(1024, 198, 16, 4, bf) == 1     # D % 4 == 2
-    assert L.moc_matrix_core_supported(1024, 2050, 32, 8, f32) == 1
-    assert L.moc_matrix_core_supported(1024, 197, 16, 4, bf) == 0     # D odd
-    assert L.moc_matrix_core_supported(1024, 2048, 64, 2, bf) == 1
-    assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32) == 0   # K > 32 with fp32 x
-    assert L.moc_matrix_core_supported(1024, 2048, 16, 9, bf) == 0    # S > 8
-    assert L.moc_matrix_core_supported(1024, 2048, 16, 1, bf) == 0
-    assert L.moc_matrix_core_supported(1024, 2048, 16, 4, _lib.DT_F16) == 0
-    assert L.moc_matrix_core_supported(0, 2048, 16, 4, bf) == 0
+    for bwd in (0, 1):
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, bwd) == 1
+        assert L.moc_matrix_core_supported(1024, 198, 16, 4, bf, bwd) == 1    # D % 4 == 2
+        assert L.moc_matrix_core_supported(1024, 2050, 32, 8, f32, bwd) == 1
+        assert L.moc_matrix_core_supported(1024, 197, 16, 4, bf, bwd) == 0    # D odd
+        assert L.moc_matrix_core_supported(1024, 2048, 64, 2, bf, bwd) == 1
+        assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, bwd) == 0  # K > 32 with fp32 x
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 12, bf, bwd) == 1  # 9-16 taps, 16 routes
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 17, bf, bwd) == 0
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 1, bf, bwd) == 0
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 4, _lib.DT_F16, bwd) == 0
+        assert L.moc_matrix_core_supported(0, 2048, 16, 4, bf, bwd) == 0
+    # 9-16 taps: the forward for every route count, the backward bf16 up to 16 routes
+    assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 0) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 1) == 0
+    assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 0) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 0
     with _lib.kernel_path(_lib.PATH_GENERIC):
-        assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf) == 0
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 0) == 0
+        assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 1) == 0
 
 
 def test_prefill_entries_validate_before_touching_the_device():
@@ -272,7 +281,7 @@ def test_prefill_entries_validate_before_touching_the_device():
     assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 1) == 0   # T < S-1 with a cache
     assert L.moc_prefill_supported(2, 2, 16, 4, 4, _lib.DT_BF16, 0) == 1   # no cache: any T
     assert L.moc_prefill_supported(2, 8, 16, 4, 5, _lib.DT_BF16, 1) == 1   # S = 5
-    assert L.moc_prefill_supported(2, 8, 16, 4, 9, _lib.DT_BF16, 1) == 0   # no matrix-core S = 9
+    assert L.moc_prefill_supported(2, 8, 16, 4, 9, _lib.DT_BF16, 1) == 0   # no prefill kernels at S = 9
     assert L.moc_prefill_supported(2, 8, 18, 4, 4, _lib.DT_BF16, 1) == 1   # D even
     assert L.moc_prefill_supported(2, 8, 17, 4, 4, _lib.DT_BF16, 1) == 0   # D odd
     assert L.moc_prefill_supported(2, 8, 16, 33, 4, _lib.DT_F32, 1) == 0   # K > 32

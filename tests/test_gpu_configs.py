@@ -220,8 +220,30 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
     """Channel counts that are even but not a multiple of 4 (the last 16-lane
     column of a wave holds a partial group of channel pairs) run on the
     matrix-core kernels, against the oracle and the generic kernels."""
-    assert _lib.lib().moc_matrix_core_supported(3 * 333, D, K, S, _lib.dtype_code(dtype)) == 1
+    for bwd in (0, 1):
+        assert _lib.lib().moc_matrix_core_supported(3 * 333, D, K, S, _lib.dtype_code(dtype), bwd) == 1
     _mfma_vs_generic(dtype, S, K, act, D)
+
+
+@pytest.mark.parametrize("dtype,S,K,act,bwd", [
+    (torch.bfloat16, 9, 16, "silu", 1),
+    (torch.bfloat16, 12, 8, None, 1),
+    (torch.bfloat16, 13, 16, None, 1),
+    (torch.bfloat16, 16, 16, "silu", 1),
+    (torch.bfloat16, 16, 12, None, 1),
+    (torch.bfloat16, 10, 32, "silu", 0),    # forward only on the matrix cores
+    (torch.bfloat16, 16, 64, None, 0),
+    (torch.float32, 11, 16, None, 0),
+    (torch.float32, 16, 32, "silu", 0),
+])
+def test_mfma_long_kernels(dtype, S, K, act, bwd):
+    """9 to 16 taps: the forward on the matrix cores for every route count, the
+    backward for bf16 with up to 16 routes (its two-pass form; the others on
+    the generic kernels), against the oracle and the generic kernels."""
+    L = _lib.lib()
+    assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 0) == 1
+    assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 1) == bwd
+    _mfma_vs_generic(dtype, S, K, act, 192)
 
 
 def _mfma_vs_generic(dtype, S, K, act, D):
