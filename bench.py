@@ -218,23 +218,24 @@ def entry_calls(dev, rotate=ROTATE):
     return fwd, bwd
 
 
-SHAPES = (("bf16 S4 D2048", torch.bfloat16, 4, 2048), ("bf16 S4 D2050", torch.bfloat16, 4, 2050),
-          ("bf16 S8 D2048", torch.bfloat16, 8, 2048), ("bf16 S12 D2048", torch.bfloat16, 12, 2048),
-          ("bf16 S16 D2048", torch.bfloat16, 16, 2048), ("fp32 S8 D2048", torch.float32, 8, 2048),
-          ("fp32 S12 D2048", torch.float32, 12, 2048))
+SHAPES = (("bf16 S4 D2048", torch.bfloat16, 4, 2048, 16), ("bf16 S4 D2050", torch.bfloat16, 4, 2050, 16),
+          ("bf16 S8 D2048", torch.bfloat16, 8, 2048, 16), ("bf16 S12 D2048", torch.bfloat16, 12, 2048, 16),
+          ("bf16 S16 D2048", torch.bfloat16, 16, 2048, 16), ("fp32 S8 D2048", torch.float32, 8, 2048, 16),
+          ("fp32 S12 D2048", torch.float32, 12, 2048, 16), ("fp32 S4 K32 D2048", torch.float32, 4, 2048, 32),
+          ("fp32 S4 K64 D2048", torch.float32, 4, 2048, 64))
 
 
 def shape_calls(dev):
     """Forward and backward entries (moc_forward / moc_backward) at the headline
-    token count (B 4 x T 4096), K 16, SiLU, softmax weights given, full dy, for
-    the kernel sizes and channel counts of SHAPES: the headline shape, an even
-    channel count that is not a multiple of 4, and 8 / 12 / 16 taps (bf16 and
-    fp32).  Returns [(label, fwd, bwd)]."""
+    token count (B 4 x T 4096), SiLU, softmax weights given, full dy, for the
+    kernel sizes, channel counts and route counts of SHAPES: the headline shape,
+    an even channel count that is not a multiple of 4, 8 / 12 / 16 taps (bf16
+    and fp32), and fp32 with 32 and 64 routes.  Returns [(label, fwd, bwd)]."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX_WEIGHTS
-    B, T, K = CFG["B"], CFG["T"], CFG["K"]
+    B, T = CFG["B"], CFG["T"]
     out = []
-    for label, dt, S, D in SHAPES:
+    for label, dt, S, D, K in SHAPES:
         g = torch.Generator().manual_seed(S * 10000 + D)
         x = torch.randn(B, T, D, generator=g).to(dev, dt)
         w = torch.softmax(torch.randn(B, T, K, generator=g), -1).to(dev, dt)

@@ -85,9 +85,10 @@ int moc_set_kernel_path(int path);
  * current moc_set_kernel_path), 0 when it runs the generic kernels.  No
  * counterpart in the reference, whose Triton kernels take every shape; it lets
  * a caller or a test see which family serves a shape.  Matrix-core forward:
- * 2 <= kernel_size <= 16; k <= 32 (k <= 64 with a bf16 x); dim even; x bf16 or
- * f32.  Backward: the same with kernel_size <= 8, and for bf16 x with k <= 16
- * up to kernel_size 16.
+ * 2 <= kernel_size <= 16; k <= 32 (k <= 64 with a bf16 x, or up to
+ * kernel_size 8); dim even; x bf16 or f32.  Backward: kernel_size <= 8 with
+ * k <= 64 for bf16 x and k <= 32 for f32 x, and for bf16 x with k <= 16 up to
+ * kernel_size 16.
  */
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
                               int x_dtype, int backward);

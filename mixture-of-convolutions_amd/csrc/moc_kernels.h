@@ -53,8 +53,9 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int activation, int routing, hipStream_t st);
 
 // MFMA path (moc_mfma_common.hip): supported() for the forward (2 <= S <= 16,
-// K <= 32 or <= 64 with bf16 x, D even), bwd_supported() for the backward (the
-// same with S <= 8, or bf16 with K <= 16 up to S = 16)
+// K <= 32, or <= 64 with bf16 x or S <= 8; D even), bwd_supported() for the
+// backward (the same with S <= 8 and K <= 32 for fp32 x, or bf16 with K <= 16 up
+// to S = 16)
 namespace mfma {
 bool supported(const Problem& p);
 bool bwd_supported(const Problem& p);

@@ -405,14 +405,18 @@ bool supported(const Problem& p) {
   // super-block's rows within a buffer's 32-bit range; D even: a lane's two
   // channels are both in or both past the channel axis, and its 2-channel
   // accesses stay aligned (rows of D elements start at even elements)
-  return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && p.x_dt == DT_BF16)) && p.D % 2 == 0 && p.D <= (int64_t(1) << 20) &&
+  return s_ok && p.K >= 1 && (p.K <= 32 || (p.K <= 64 && (p.x_dt == DT_BF16 || p.S <= 8))) && p.D % 2 == 0 &&
+         p.D <= (int64_t(1) << 20) &&
          (p.x_dt == DT_BF16 || p.x_dt == DT_F32) &&
          bwd_grid(p.n_tokens, p.D, p.S).gy <= 65535 && fwd_grid(p.n_tokens, p.D, p.S).gy <= 65535;
 }
 
-// 9 to 16 taps: the backward for bf16 with up to 16 routes (the two-pass form)
+// The backward: fp32 with up to 32 routes (the fused fp32 tile over 64 routes
+// crashes LLVM's AGPR-copy rewrite); 9 to 16 taps for bf16 with up to 16 routes
+// (the two-pass form)
 bool bwd_supported(const Problem& p) {
-  return supported(p) && (p.S <= 8 || (p.x_dt == DT_BF16 && p.K <= 16));
+  return supported(p) && (p.x_dt == DT_BF16 || p.K <= 32) &&
+         (p.S <= 8 || (p.x_dt == DT_BF16 && p.K <= 16));
 }
 
 size_t forward_workspace(const Problem& p) { return plan(p, false).total; }

@@ -62,6 +62,10 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int route_chunks(int64_t K) { return K <= 16 ? 1 : (K <= 32 ? 2 : 4); }
 template <int KC, bool BF>
 constexpr bool kcOK = KC <= 2 || BF;
+// the forward also takes fp32 with 64 routes up to 8 taps (236-434 VGPRs, no
+// spills; past 8 taps it spills)
+template <int S, int KC, bool BF>
+constexpr bool kcOKFwd = kcOK<KC, BF> || S <= 8;
 
 // Forward: about kFwdTargetWG workgroups, each wave walking at most
 // kFwdMaxSb super-blocks; larger problems get more workgroups rather than
@@ -252,7 +256,7 @@ struct LayerOps {
 template <int S, int KC, bool ACT, bool BF>
 void fwd_one(const Problem& p, const void* x, const void* a_c, const void* b_c, void* y,
              hipStream_t st) {
-  if constexpr (!kcOK<KC, BF>) return;
+  if constexpr (!kcOKFwd<S, KC, BF>) return;
   else {
   using E = typename CT<BF>::elem;
   const Grid2 g = fwd_grid(p.n_tokens, p.D, S);

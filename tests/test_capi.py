@@ -255,7 +255,7 @@ def test_matrix_core_supported_names_the_kernel_family():
         assert L.moc_matrix_core_supported(1024, 2050, 32, 8, f32, bwd) == 1
         assert L.moc_matrix_core_supported(1024, 197, 16, 4, bf, bwd) == 0    # D odd
         assert L.moc_matrix_core_supported(1024, 2048, 64, 2, bf, bwd) == 1
-        assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, bwd) == 0  # K > 32 with fp32 x
+        assert L.moc_matrix_core_supported(1024, 2048, 48, 12, f32, bwd) == 0  # fp32 x, K > 32, S > 8
         assert L.moc_matrix_core_supported(1024, 2048, 16, 12, bf, bwd) == 1  # 9-16 taps, 16 routes
         assert L.moc_matrix_core_supported(1024, 2048, 16, 17, bf, bwd) == 0
         assert L.moc_matrix_core_supported(1024, 2048, 16, 1, bf, bwd) == 0
@@ -266,6 +266,9 @@ def test_matrix_core_supported_names_the_kernel_family():
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 1) == 0
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 0) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 0
+    # fp32 with 33-64 routes: the forward up to 8 taps, the backward generic
+    assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 0) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 1) == 0
     with _lib.kernel_path(_lib.PATH_GENERIC):
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 0) == 0
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 1) == 0
@@ -284,7 +287,7 @@ def test_prefill_entries_validate_before_touching_the_device():
     assert L.moc_prefill_supported(2, 8, 16, 4, 9, _lib.DT_BF16, 1) == 0   # no prefill kernels at S = 9
     assert L.moc_prefill_supported(2, 8, 18, 4, 4, _lib.DT_BF16, 1) == 1   # D even
     assert L.moc_prefill_supported(2, 8, 17, 4, 4, _lib.DT_BF16, 1) == 0   # D odd
-    assert L.moc_prefill_supported(2, 8, 16, 33, 4, _lib.DT_F32, 1) == 0   # K > 32
+    assert L.moc_prefill_supported(2, 8, 16, 33, 4, _lib.DT_F32, 1) == 0   # K > 32 with fp32 x
     assert L.moc_prefill_supported(0, 8, 16, 4, 4, _lib.DT_BF16, 1) == 0
     fwd_need = L.moc_forward_workspace_bytes(16, 16, 4, 4, _lib.DT_BF16, 0)
     assert fwd_need > 0
