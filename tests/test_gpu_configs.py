@@ -249,9 +249,22 @@ def test_mfma_long_kernels(dtype, S, K, act, bwd):
     _mfma_vs_generic(dtype, S, K, act, 192)
 
 
-def _mfma_vs_generic(dtype, S, K, act, D):
+@pytest.mark.parametrize("dtype,S,K,act,D", [
+    (torch.bfloat16, 17, 16, "silu", 192),   # past 16 taps
+    (torch.bfloat16, 4, 80, None, 192),      # past 64 routes
+    (torch.bfloat16, 4, 16, "silu", 197),    # odd channel count
+])
+def test_generic_path_matches_oracle(dtype, S, K, act, D):
+    """The shapes outside the matrix-core kernels (forward and backward) run
+    the generic kernels, against the oracle, fixed and packed."""
+    L = _lib.lib()
+    for bwd in (0, 1):
+        assert L.moc_matrix_core_supported(3 * 333, D, K, S, _lib.dtype_code(dtype), bwd) == 0
+    _mfma_vs_generic(dtype, S, K, act, D)
+
+
+def _mfma_vs_generic(dtype, S, K, act, D, Bt=3, T=333, lengths=(1, 2, 70, 3, 200, 17, 400, 5, 301)):
     g = gen(S * 100 + K)
-    Bt, T = 3, 333
     x = randn(g, Bt, T, D, scale=0.5).to(DEV, dtype)
     a = torch.softmax(randn(g, Bt, T, K), -1).to(DEV, dtype)
     b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
@@ -274,10 +287,9 @@ def _mfma_vs_generic(dtype, S, K, act, D):
     for n, u, v, r in zip(("y", "dx", "dalpha", "dbasis"), got, other, ref):
         assert_close(n, u, r, dtype)
         assert_close(n + " (mfma vs generic)", u, v, dtype)
-    lengths = [1, 2, 70, 3, 200, 17, 400, 5, 301]
     cu = torch.tensor([0, *itertools.accumulate(lengths)], device=DEV, dtype=torch.int64)
     assert cu[-1] == Bt * T
-    gv = run(cu_seqlens=cu, max_seqlen=400)
+    gv = run(cu_seqlens=cu, max_seqlen=max(lengths))
     refv = O.moc_varlen_grads_ref(rx.detach().view(-1, D), ra.detach().view(-1, K), rb.detach(),
                                   cu.cpu(), dy.float().cpu().view(-1, D), act)
     for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), gv, refv):
