@@ -87,8 +87,8 @@ int moc_set_kernel_path(int path);
  * a caller or a test see which family serves a shape.  Matrix-core forward:
  * 2 <= kernel_size <= 16; k <= 32 (k <= 64 with a bf16 x, or up to
  * kernel_size 8); dim even; x bf16 or f32.  Backward: kernel_size <= 8 with
- * k <= 64 for bf16 x and k <= 32 for f32 x, and for bf16 x with k <= 16 up to
- * kernel_size 16.
+ * k <= 64 (for f32 x past 32 routes in two route halves), and for bf16 x with
+ * k <= 16 up to kernel_size 16.
  */
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
                               int x_dtype, int backward);

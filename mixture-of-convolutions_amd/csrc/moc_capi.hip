@@ -126,13 +126,19 @@ bool use_mfma_bwd(const moc::Problem& p) {
   if (p.path == MOC_PATH_GENERIC) return false;
   return moc::mfma::bwd_supported(p);
 }
+// fp32 with 33-64 routes: the backward in two route halves on the matrix cores
+bool use_routesplit(const moc::Problem& p) {
+  if (p.path == MOC_PATH_GENERIC) return false;
+  return !moc::mfma::bwd_supported(p) && moc::mfma::routesplit_supported(p);
+}
 
 size_t forward_bytes(const moc::Problem& p) {
   return use_mfma(p) ? moc::mfma::forward_workspace(p) : fwd_bytes(p.n_tokens, p.D, p.K, p.S);
 }
 
 size_t backward_bytes(const moc::Problem& p) {
-  return use_mfma_bwd(p) ? moc::mfma::backward_workspace(p) : bwd_bytes(p);
+  if (use_mfma_bwd(p)) return moc::mfma::backward_workspace(p);
+  return use_routesplit(p) ? moc::mfma::routesplit_workspace(p) : bwd_bytes(p);
 }
 
 int hip_status(const char* what) {
@@ -257,6 +263,10 @@ int backward_launch(const moc::Problem& p, const void* x, const void* alpha, con
     moc::mfma::backward(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
     return hip_status("moc_backward launch");
   }
+  if (use_routesplit(p)) {
+    moc::mfma::backward_routesplit(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
+    return hip_status("moc_backward launch");
+  }
   Carve cv{static_cast<char*>(workspace), 0};
   float* a_r = cv.take<float>(size_t(p.n_tokens * p.K));
   float* basis_c = cv.take<float>(size_t(p.K * p.S * p.D));
@@ -358,7 +368,7 @@ int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t 
   if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return (backward ? use_mfma_bwd(p) : use_mfma(p)) ? 1 : 0;
+  return (backward ? use_mfma_bwd(p) || use_routesplit(p) : use_mfma(p)) ? 1 : 0;
 }
 
 int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,

@@ -621,6 +621,11 @@ void launch_prep(const Problem& p, const void* alpha, const void* basis, float* 
                      basis, p.b_dt, nb, p.x_dt, basis_c);
 }
 
+void launch_prep_alpha(const Problem& p, const void* alpha, float* a_r, hipStream_t st) {
+  hipLaunchKernelGGL(prep_alpha_kernel, dim3(grid_for(p.n_tokens, 256, 1LL << 30)), dim3(256),
+                     0, st, alpha, p.a_dt, route_form(p.routing), p.n_tokens, p.K, a_r);
+}
+
 void launch_forward_generic(const Problem& p, const void* x, const float* a_r,
                             const float* basis_c, void* y, hipStream_t st) {
   hipLaunchKernelGGL(fwd_generic_kernel, dim3(grid_for(p.n_tokens * p.D, 256)), dim3(256), 0,

@@ -40,6 +40,8 @@ inline void prof_end(const Problem& p, hipStream_t st) {
 // generic path (moc_generic.hip)
 void launch_prep(const Problem& p, const void* alpha, const void* basis, float* a_r,
                  float* basis_c, hipStream_t st);
+// a_r alone (the routing weights as the router activation forms them, fp32)
+void launch_prep_alpha(const Problem& p, const void* alpha, float* a_r, hipStream_t st);
 void launch_forward_generic(const Problem& p, const void* x, const float* a_r,
                             const float* basis_c, void* y, hipStream_t st);
 size_t generic_bwd_scratch_floats(const Problem& p);
@@ -54,11 +56,19 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
 
 // MFMA path (moc_mfma_common.hip): supported() for the forward (2 <= S <= 16,
 // K <= 32, or <= 64 with bf16 x or S <= 8; D even), bwd_supported() for the
-// backward (the same with S <= 8 and K <= 32 for fp32 x, or bf16 with K <= 16 up
-// to S = 16)
+// backward in one pass family (the same with S <= 8 and K <= 32 for fp32 x, or
+// bf16 with K <= 16 up to S = 16), routesplit_supported() for fp32 with 33-64
+// routes up to S = 8
 namespace mfma {
 bool supported(const Problem& p);
 bool bwd_supported(const Problem& p);
+// the backward of fp32 layers with 33-64 routes up to 8 taps in two route
+// halves on the 32-route kernels (moc_routesplit.hip)
+bool routesplit_supported(const Problem& p);
+size_t routesplit_workspace(const Problem& p);
+void backward_routesplit(const Problem& p, const void* x, const void* alpha, const void* basis,
+                         const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+                         hipStream_t st);
 size_t forward_workspace(const Problem& p);
 size_t backward_workspace(const Problem& p);
 void forward(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,

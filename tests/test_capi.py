@@ -266,9 +266,11 @@ def test_matrix_core_supported_names_the_kernel_family():
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 1) == 0
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 0) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 0
-    # fp32 with 33-64 routes: the forward up to 8 taps, the backward generic
+    # fp32 with 33-64 routes up to 8 taps: the forward, and the backward in two
+    # route halves
     assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 0) == 1
-    assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 1) == 0
+    assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 1) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 64, 8, f32, 1) == 1
     with _lib.kernel_path(_lib.PATH_GENERIC):
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 0) == 0
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, bf, 1) == 0

@@ -235,14 +235,17 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
     (torch.bfloat16, 16, 64, None, 0),
     (torch.float32, 11, 16, None, 0),
     (torch.float32, 16, 32, "silu", 0),
-    (torch.float32, 4, 48, "silu", 0),      # fp32, 33-64 routes: the forward only
-    (torch.float32, 8, 64, None, 0),
+    (torch.float32, 4, 48, "silu", 1),      # fp32, 33-64 routes: the backward in route halves
+    (torch.float32, 8, 64, None, 1),
+    (torch.float32, 3, 40, "silu", 1),
 ])
 def test_mfma_long_kernels(dtype, S, K, act, bwd):
     """9 to 16 taps: the forward on the matrix cores for every route count, the
     backward for bf16 with up to 16 routes (its two-pass form; the others on
     the generic kernels); fp32 with 33-64 routes: the forward on the matrix
-    cores, the backward generic.  Against the oracle and the generic kernels."""
+    cores, the backward in two route halves on the 32-route kernels (dy = g
+    from the forward's P, the router gradient over all routes at the end).
+    Against the oracle and the generic kernels."""
     L = _lib.lib()
     assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 0) == 1
     assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 1) == bwd
