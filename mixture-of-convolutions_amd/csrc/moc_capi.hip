@@ -131,6 +131,12 @@ bool use_routesplit(const moc::Problem& p) {
   if (p.path == MOC_PATH_GENERIC) return false;
   return !moc::mfma::bwd_supported(p) && moc::mfma::routesplit_supported(p);
 }
+// bf16 with 9-16 taps and 17-64 routes: the dx pass, then the taps pass per
+// 16-route chunk
+bool use_chunks(const moc::Problem& p) {
+  if (p.path == MOC_PATH_GENERIC) return false;
+  return !moc::mfma::bwd_supported(p) && moc::mfma::chunks_supported(p);
+}
 
 size_t forward_bytes(const moc::Problem& p) {
   return use_mfma(p) ? moc::mfma::forward_workspace(p) : fwd_bytes(p.n_tokens, p.D, p.K, p.S);
@@ -138,6 +144,7 @@ size_t forward_bytes(const moc::Problem& p) {
 
 size_t backward_bytes(const moc::Problem& p) {
   if (use_mfma_bwd(p)) return moc::mfma::backward_workspace(p);
+  if (use_chunks(p)) return moc::mfma::chunks_workspace(p);
   return use_routesplit(p) ? moc::mfma::routesplit_workspace(p) : bwd_bytes(p);
 }
 
@@ -267,6 +274,10 @@ int backward_launch(const moc::Problem& p, const void* x, const void* alpha, con
     moc::mfma::backward_routesplit(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
     return hip_status("moc_backward launch");
   }
+  if (use_chunks(p)) {
+    moc::mfma::backward_chunks(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
+    return hip_status("moc_backward launch");
+  }
   Carve cv{static_cast<char*>(workspace), 0};
   float* a_r = cv.take<float>(size_t(p.n_tokens * p.K));
   float* basis_c = cv.take<float>(size_t(p.K * p.S * p.D));
@@ -368,7 +379,7 @@ int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t 
   if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return (backward ? use_mfma_bwd(p) || use_routesplit(p) : use_mfma(p)) ? 1 : 0;
+  return (backward ? use_mfma_bwd(p) || use_routesplit(p) || use_chunks(p) : use_mfma(p)) ? 1 : 0;
 }
 
 int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,

@@ -66,6 +66,13 @@ bool bwd_supported(const Problem& p);
 // halves on the 32-route kernels (moc_routesplit.hip)
 bool routesplit_supported(const Problem& p);
 size_t routesplit_workspace(const Problem& p);
+// the backward of bf16 layers with 9-16 taps and 17-64 routes: the dx pass over
+// every route, then the taps pass per 16-route chunk (moc_mfma_common.hip)
+bool chunks_supported(const Problem& p);
+size_t chunks_workspace(const Problem& p);
+void backward_chunks(const Problem& p, const void* x, const void* alpha, const void* basis,
+                     const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+                     hipStream_t st);
 void backward_routesplit(const Problem& p, const void* x, const void* alpha, const void* basis,
                          const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
                          hipStream_t st);

@@ -811,7 +811,8 @@ constexpr bool kBwdOneWaveFused = BF ? ((S >= 8 && KC >= 2) || KC >= 4)
 // slower (316 -> 333).
 template <int S, int KC, int MODE, bool BF, bool ACT = false>
 constexpr int kBwdMinWaves = ((MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>) ||
-                              (MODE == kBwdDx && KC >= 4 && (S >= 7 || (ACT && S >= 5))))
+                              (MODE == kBwdDx && KC >= 4 && (S >= 7 || (ACT && S >= 5))) ||
+                              (MODE == kBwdDx && KC >= 2 && S > 8))
                                  ? 1
                                  : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 

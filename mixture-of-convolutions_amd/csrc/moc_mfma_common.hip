@@ -495,6 +495,135 @@ void backward(const Problem& p, const void* x, const void* alpha, const void* ba
   launch_stage2(p, pl, dir, ws, alpha, dalpha, dbasis, st);
 }
 
+// ---------------------------------------------------------------------------
+// Backward of bf16 layers with 9 to 16 taps and 17 to 64 routes: the dx pass
+// over every route (dx; with the activation also g = dy silu'(P) in fp32),
+// then per 16-route chunk the taps pass on that chunk's operands and a stage 2
+// with the chunk's weights given (its weight gradient, fp32, and its dbasis
+// rows in place), then the router gradient over all routes.  Each part keeps a
+// fixed summation order, so results are bitwise reproducible.
+
+namespace {
+
+// columns [c0, c0 + 16) of a [N, KP] (bf16) into a16 [N, 16]
+__global__ void cols16_kernel(const uint16_t* __restrict__ a, uint16_t* __restrict__ a16, int64_t N,
+                              int KP, int c0) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N * 16) return;
+  const int64_t t = i >> 4;
+  a16[i] = a[t * KP + c0 + (i & 15)];
+}
+
+// dalpha [N, K] from the chunks' weight gradients (chunk c: [N, kc] at
+// c N 16, kc = min(16, K - 16 c)) and the router gradient over all K routes on
+// a_r (nullptr: weights given, no gradient to take); one 64-lane wave per token
+__global__ void __launch_bounds__(64)
+route_grad_chunks_kernel(const float* __restrict__ da_w, const float* __restrict__ a_r,
+                         void* __restrict__ dalpha, int a_dt, int routing, int64_t N, int K) {
+  const int64_t t = blockIdx.x;
+  const int k = threadIdx.x;
+  const bool on = k < K;
+  const int c = k >> 4, kc = K - 16 * c < 16 ? K - 16 * c : 16;
+  const float v = on ? da_w[static_cast<int64_t>(c) * N * 16 + t * kc + (k & 15)] : 0.f;
+  const float a = (on && a_r != nullptr) ? a_r[t * K + k] : 0.f;
+  float dot = a * v;
+  for (int o = 32; o > 0; o >>= 1) dot += __shfl_xor(dot, o, 64);
+  float r = v;
+  if (routing == ROUTE_SOFTMAX) r = a * (v - dot);
+  else if (routing == ROUTE_EXP) r = a * v;
+  if (on) store_any(dalpha, a_dt, t * K + k, r);
+}
+
+Problem chunk_problem(const Problem& p, int64_t kc) {
+  Problem q = p;
+  q.K = kc;
+  q.routing = ROUTE_ALPHA;  // the chunk's weights are given
+  q.a_dt = DT_F32;          // its weight gradient in fp32
+  q.prof_start = q.prof_stop = nullptr;
+  return q;
+}
+
+struct ChunkPlan {
+  Plan full;       // prep of the whole problem: a_c, b_c, a_r
+  size_t a16, da, wq, total;
+  Plan q;          // one chunk's partials and g (offsets from wq)
+};
+
+ChunkPlan chunk_plan(const Problem& p) {
+  ChunkPlan c{};
+  c.full.KP = 16 * route_chunks(p.K);
+  c.full.esz = 2;
+  size_t off = 0;
+  c.full.off_ac = off; off += al(static_cast<size_t>(p.n_tokens) * c.full.KP * 2);
+  c.full.off_bc = off; off += al(static_cast<size_t>(c.full.KP) * p.S * p.D * 2);
+  c.full.off_ar = off;
+  if (route_grad(p.routing) != ROUTE_ALPHA) off += al(static_cast<size_t>(p.n_tokens) * p.K * 4);
+  c.a16 = off; off += al(static_cast<size_t>(p.n_tokens) * 16 * 2);
+  c.da = off; off += al(static_cast<size_t>(p.n_tokens) * c.full.KP * 4);
+  c.wq = off;
+  c.q = plan(chunk_problem(p, 16), true);
+  off += c.q.total;
+  c.total = off;
+  return c;
+}
+
+}  // namespace
+
+bool chunks_supported(const Problem& p) {
+  return p.x_dt == DT_BF16 && p.S > 8 && p.S <= 16 && p.K > 16 && p.K <= 64 && supported(p);
+}
+
+size_t chunks_workspace(const Problem& p) { return chunk_plan(p).total; }
+
+void backward_chunks(const Problem& p, const void* x, const void* alpha, const void* basis,
+                     const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+                     hipStream_t st) {
+  const ChunkPlan c = chunk_plan(p);
+  char* ws = static_cast<char*>(workspace);
+  launch_prep(p, c.full, alpha, basis, ws, true, st);
+  const auto* a_c = reinterpret_cast<const uint16_t*>(ws + c.full.off_ac);
+  const auto* b_c = reinterpret_cast<const uint16_t*>(ws + c.full.off_bc);
+  const float* a_r = route_grad(p.routing) != ROUTE_ALPHA
+                         ? reinterpret_cast<const float*>(ws + c.full.off_ar) : nullptr;
+  auto* a16 = reinterpret_cast<uint16_t*>(ws + c.a16);
+  float* da_w = reinterpret_cast<float*>(ws + c.da);
+  char* wq = ws + c.wq;
+  float* pda = reinterpret_cast<float*>(wq + c.q.off_pda);
+  float* pdb = reinterpret_cast<float*>(wq + c.q.off_pdb);
+  float* gb = p.activation != 0 ? reinterpret_cast<float*>(wq + c.q.off_g) : nullptr;
+  const int64_t N = p.n_tokens, SD = p.S * p.D;
+  const size_t esz_b = p.b_dt == DT_F32 ? 4 : 2;
+  prof_begin(p, st);
+  switch (p.S) {
+#define MOC_CHUNKS_DX(S_) \
+    case S_: launch_dx_pass<S_>(p, x, dy, a_c, b_c, dx, gb, st); break;
+    MOC_CHUNKS_DX(9) MOC_CHUNKS_DX(10) MOC_CHUNKS_DX(11) MOC_CHUNKS_DX(12)
+    MOC_CHUNKS_DX(13) MOC_CHUNKS_DX(14) MOC_CHUNKS_DX(15) MOC_CHUNKS_DX(16)
+#undef MOC_CHUNKS_DX
+    default: break;
+  }
+  for (int c0 = 0; c0 < p.K; c0 += 16) {
+    const int64_t kc = p.K - c0 < 16 ? p.K - c0 : 16;
+    const Problem q = chunk_problem(p, kc);
+    hipLaunchKernelGGL(cols16_kernel, dim3(static_cast<unsigned>(cdiv(N * 16, 256))), dim3(256), 0, st,
+                       a_c, a16, N, c.full.KP, c0);
+    const uint16_t* b16 = b_c + static_cast<int64_t>(c0) * SD;
+    switch (p.S) {
+#define MOC_CHUNKS_TAPS(S_) \
+      case S_: launch_taps_chunk<S_>(q, x, dy, a16, b16, pda, pdb, gb, st); break;
+      MOC_CHUNKS_TAPS(9) MOC_CHUNKS_TAPS(10) MOC_CHUNKS_TAPS(11) MOC_CHUNKS_TAPS(12)
+      MOC_CHUNKS_TAPS(13) MOC_CHUNKS_TAPS(14) MOC_CHUNKS_TAPS(15) MOC_CHUNKS_TAPS(16)
+#undef MOC_CHUNKS_TAPS
+      default: break;
+    }
+    launch_stage2(q, c.q, false, wq, nullptr, da_w + static_cast<int64_t>(c0) * N,
+                  static_cast<char*>(dbasis) + static_cast<size_t>(c0 * SD) * esz_b, st);
+  }
+  prof_end(p, st);
+  hipLaunchKernelGGL(route_grad_chunks_kernel, dim3(static_cast<unsigned>(N)), dim3(64), 0, st, da_w,
+                     a_r, dalpha, p.a_dt, route_grad(p.routing), N, static_cast<int>(p.K));
+}
+
 bool prefill_supported(const Problem& p, bool has_cache) {
   // (prefill kernels are built for 2 to 8 taps)
   if (!bwd_supported(p) || p.S > 8 || p.seq.cu != nullptr || p.seq.seq_len <= 0 ||

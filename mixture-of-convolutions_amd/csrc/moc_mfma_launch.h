@@ -516,6 +516,55 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
   }
 }
 
+// Pieces of the backward of bf16 layers with 9 to 16 taps and 17 to 64 routes
+// (backward_chunks): the dx pass over every route (dx, and with the activation
+// g = dy silu'(P) into gbuf), and the taps pass of one 16-route chunk on its
+// own operands (a_c16 [N, 16], b_c16 [16, S, D]), into the partials of a
+// 16-route problem's plan.  (The one-pass and route-split forms do not fit
+// these sizes: spills past what the compiler handles, LDS past 160 KB.)
+template <int S>
+void launch_dx_pass(const Problem& p, const void* x, const void* dy, const uint16_t* a_c,
+                    const uint16_t* b_c, void* dx, float* gbuf, hipStream_t st) {
+  if constexpr (S > 8) {
+    const Grid2 g = bwd_grid(p.n_tokens, p.D, S);
+    const int gx = static_cast<int>(g.gx), gy = static_cast<int>(g.gy);
+    const bool act = p.activation != 0;
+    auto run = [&](auto kct, auto actt) {
+      constexpr int KC = decltype(kct)::value;
+      constexpr bool ACT = decltype(actt)::value;
+      hipLaunchKernelGGL((bwd_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, false, kBwdDx>),
+                         dim3(g.gx, g.gy), dim3(64 * kBwdWPG), 0, st, x, dy, p.dy_stride, a_c, b_c, dx,
+                         nullptr, nullptr, p.seq, p.D, gx, gy, g.gy1, g.n_old, g.n_total, gbuf);
+    };
+    if (dx == nullptr && !act) return;
+    if (route_chunks(p.K) == 2) {
+      if (act) run(std::integral_constant<int, 2>{}, std::true_type{});
+      else run(std::integral_constant<int, 2>{}, std::false_type{});
+    } else {
+      if (act) run(std::integral_constant<int, 4>{}, std::true_type{});
+      else run(std::integral_constant<int, 4>{}, std::false_type{});
+    }
+  }
+}
+
+template <int S>
+void launch_taps_chunk(const Problem& p, const void* x, const void* dy, const uint16_t* a_c16,
+                       const uint16_t* b_c16, float* part_da, float* part_db, float* gbuf,
+                       hipStream_t st) {
+  if constexpr (S > 8) {
+    const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(p.D, kTapsCW), p.D, S, device_cu_count());
+    const int gx = static_cast<int>(gt.gx), gy = static_cast<int>(gt.gy);
+    if (p.activation != 0)
+      hipLaunchKernelGGL((bwd_kernel<S, 1, kBwdNB, kBwdNC, kTapsWPG, true, true, false, kBwdTaps>),
+                         dim3(gt.gx, gt.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a_c16, b_c16,
+                         nullptr, part_da, part_db, p.seq, p.D, gx, gy, gt.gy1, gt.n_old, gt.n_total, gbuf);
+    else
+      hipLaunchKernelGGL((bwd_kernel<S, 1, kBwdNB, kBwdNC, kTapsWPG, false, true, false, kBwdTaps>),
+                         dim3(gt.gx, gt.gy), dim3(64 * kTapsWPG), 0, st, x, dy, p.dy_stride, a_c16, b_c16,
+                         nullptr, part_da, part_db, p.seq, p.D, gx, gy, gt.gy1, gt.n_old, gt.n_total, gbuf);
+  }
+}
+
 // Prefill from a cache (Pre, fixed-length sequences): the forward on
 // fwd_kernel's grid; the backward's fused pass (for every K, activation and
 // dtype) on the grid that owns the partials, so the workspace and stage 2 are
@@ -658,7 +707,13 @@ MOC_DECLARE_S(8)
   extern template void launch_fwd<S_>(const Problem&, const void*, const void*, const void*, \
                                       void*, hipStream_t);                                    \
   extern template void launch_bwd<S_>(const Problem&, const void*, const void*, const void*, \
-                                      const void*, void*, float*, float*, float*, hipStream_t);
+                                      const void*, void*, float*, float*, float*, hipStream_t); \
+  extern template void launch_dx_pass<S_>(const Problem&, const void*, const void*,           \
+                                          const uint16_t*, const uint16_t*, void*, float*,   \
+                                          hipStream_t);                                       \
+  extern template void launch_taps_chunk<S_>(const Problem&, const void*, const void*,        \
+                                             const uint16_t*, const uint16_t*, float*, float*, \
+                                             float*, hipStream_t);
 MOC_DECLARE_S_LONG(9)
 MOC_DECLARE_S_LONG(10)
 MOC_DECLARE_S_LONG(11)

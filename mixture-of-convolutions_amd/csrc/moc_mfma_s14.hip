@@ -9,6 +9,10 @@ template void launch_fwd<14>(const Problem&, const void*, const void*, const voi
                               hipStream_t);
 template void launch_bwd<14>(const Problem&, const void*, const void*, const void*, const void*,
                               void*, float*, float*, float*, hipStream_t);
+template void launch_dx_pass<14>(const Problem&, const void*, const void*, const uint16_t*,
+                                  const uint16_t*, void*, float*, hipStream_t);
+template void launch_taps_chunk<14>(const Problem&, const void*, const void*, const uint16_t*,
+                                     const uint16_t*, float*, float*, float*, hipStream_t);
 
 }  // namespace mfma
 }  // namespace moc

@@ -231,8 +231,10 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
     (torch.bfloat16, 13, 16, None, 1),
     (torch.bfloat16, 16, 16, "silu", 1),
     (torch.bfloat16, 16, 12, None, 1),
-    (torch.bfloat16, 10, 32, "silu", 0),    # forward only on the matrix cores
-    (torch.bfloat16, 16, 64, None, 0),
+    (torch.bfloat16, 10, 32, "silu", 1),    # past 16 routes: dx pass, then taps per 16-route chunk
+    (torch.bfloat16, 16, 64, None, 1),
+    (torch.bfloat16, 12, 24, "silu", 1),
+    (torch.bfloat16, 13, 48, None, 1),
     (torch.float32, 11, 16, None, 0),
     (torch.float32, 16, 32, "silu", 0),
     (torch.float32, 4, 48, "silu", 1),      # fp32, 33-64 routes: the backward in route halves
@@ -241,8 +243,9 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
 ])
 def test_mfma_long_kernels(dtype, S, K, act, bwd):
     """9 to 16 taps: the forward on the matrix cores for every route count, the
-    backward for bf16 with up to 16 routes (its two-pass form; the others on
-    the generic kernels); fp32 with 33-64 routes: the forward on the matrix
+    backward for bf16 (up to 16 routes its two-pass form; past 16 the dx pass
+    over every route, then the taps pass per 16-route chunk; fp32 on the
+    generic kernels); fp32 with 33-64 routes: the forward on the matrix
     cores, the backward in two route halves on the 32-route kernels (dy = g
     from the forward's P, the router gradient over all routes at the end).
     Against the oracle and the generic kernels."""
