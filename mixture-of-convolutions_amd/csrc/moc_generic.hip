@@ -304,9 +304,9 @@ update_kernel(const void* __restrict__ x, const void* __restrict__ alpha, int a_
 
 // ---------------------------------------------------------------------------
 // Decode step for the shapes the matrix-core decode kernel does not take (fp32
-// data, mixed storage dtypes, strided caches, any D), 2 to 8 taps and up to 64
-// routes.  A workgroup covers 64 channels (one per lane) and 4 T tokens (T per
-// wave):
+// data, mixed storage dtypes, strided caches, any D, 9 to 16 taps), 2 to 16
+// taps and up to 64 routes.  A workgroup covers 64 channels (one per lane) and
+// 4 T tokens (T per wave):
 //   * every load goes out first: the wave's logits, x, the cache slots and its
 //     quarter of the basis tile (KT routes x S taps x 64 channels), with
 //     clamped indices and selected values (a load under a per-lane condition
@@ -357,8 +357,8 @@ update_tile_kernel(const void* __restrict__ x, const void* __restrict__ alpha, i
   constexpr int T = dec_tokens_per_wave(S);
   constexpr int LPT = 64 / T;             // lanes per token in the softmax
   constexpr int NV = kDecMaxK / LPT;      // routing entries per lane
-  constexpr int KT = S <= 2 ? 32 : S <= 4 ? 16 : 8;  // routes per basis chunk
-  constexpr int R = KT * S;               // basis rows (route, tap) per chunk: 40 to 64
+  constexpr int KT = S <= 2 ? 32 : S <= 4 ? 16 : S <= 8 ? 8 : 4;  // routes per basis chunk
+  constexpr int R = KT * S;               // basis rows (route, tap) per chunk: 36 to 64
   constexpr int RP = R + 4;               // padded LDS row of one channel (16-byte reads
                                           // of 8 lanes fall in distinct banks)
   constexpr int ES = F32 ? 4 : 2;         // element bytes of x, y and the cache
@@ -667,7 +667,7 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
                            int64_t D, int64_t K, int64_t S, int x_dt, int a_dt, int b_dt,
                            int activation, int routing, hipStream_t st) {
   // (the wave kernel addresses the basis with 32-bit byte offsets)
-  if (S >= 2 && S <= 8 && K <= kDecMaxK && K * S * D * 4 < (int64_t(1) << 31)) {
+  if (S >= 2 && S <= 16 && K <= kDecMaxK && K * S * D * 4 < (int64_t(1) << 31)) {
     const int es = x_dt == DT_F32 ? 4 : 2;
     const int vb = dec_row_vec_bytes(static_cast<int>(S), es);
     const bool row = cs_s == 1 && vb > 0 && reinterpret_cast<uintptr_t>(cache) % vb == 0 &&
@@ -696,6 +696,14 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
       MOC_WAVE_S(6)
       MOC_WAVE_S(7)
       MOC_WAVE_S(8)
+      MOC_WAVE_S(9)
+      MOC_WAVE_S(10)
+      MOC_WAVE_S(11)
+      MOC_WAVE_S(12)
+      MOC_WAVE_S(13)
+      MOC_WAVE_S(14)
+      MOC_WAVE_S(15)
+      MOC_WAVE_S(16)
       default: break;
     }
 #undef MOC_WAVE_S

@@ -454,13 +454,19 @@ def alpha_pad(alpha, S):
     (torch.float32, torch.float32, torch.float32, "contiguous", 8, 64, "softmax"),
     (torch.float32, torch.bfloat16, torch.float32, "aligned-padded", 4, 40, "softmax"),
     (torch.bfloat16, torch.bfloat16, torch.float32, "aligned-padded", 8, 16, None),
-    (torch.float32, torch.float32, torch.float32, "contiguous", 9, 16, "softmax"),   # 9 taps, 80 routes:
-    (torch.float32, torch.float32, torch.float32, "slot-major", 4, 80, "exp"),       # the per-row kernel
+    (torch.float32, torch.float32, torch.float32, "contiguous", 9, 16, "softmax"),   # 9 to 16 taps
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, "contiguous", 12, 32, "softmax"),
+    (torch.bfloat16, torch.bfloat16, torch.float32, "contiguous", 11, 16, "exp"),
+    (torch.bfloat16, torch.float32, torch.bfloat16, "slot-major", 16, 64, "softmax"),
+    (torch.float32, torch.float32, torch.float32, "padded", 16, 20, "exp"),
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, "aligned-padded", 14, 16, None),
+    (torch.float32, torch.float32, torch.float32, "slot-major", 4, 80, "exp"),       # 80 routes, 17 taps:
+    (torch.bfloat16, torch.bfloat16, torch.bfloat16, "contiguous", 17, 8, "softmax"),  # the per-row kernel
 ])
 def test_decode_other_dtypes_and_strided_caches(xdt, adt, bdt, layout, S, K, route):
     """Decode steps (moc_update) on what the matrix-core decode kernel does not
     take: fp32 data, mixed storage dtypes (fp16 / bf16 weights or basis), caches with any strides, a
-    channel count that is not a multiple of 4, up to 64 routes and 8 taps (the
+    channel count that is not a multiple of 4, up to 64 routes and 16 taps (the
     tile kernel, with whole-row cache accesses where the rows are contiguous and
     aligned and per-slot ones otherwise), and past them (the per-row kernel).  y against the oracle
     step with the weights and basis rounded as the kernels round them; the
