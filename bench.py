@@ -221,7 +221,8 @@ def entry_calls(dev, rotate=ROTATE):
 SHAPES = (("bf16 S4 D2048", torch.bfloat16, 4, 2048, 16), ("bf16 S4 D2050", torch.bfloat16, 4, 2050, 16),
           ("bf16 S8 D2048", torch.bfloat16, 8, 2048, 16), ("bf16 S12 D2048", torch.bfloat16, 12, 2048, 16),
           ("bf16 S16 D2048", torch.bfloat16, 16, 2048, 16), ("fp32 S8 D2048", torch.float32, 8, 2048, 16),
-          ("fp32 S12 D2048", torch.float32, 12, 2048, 16), ("fp32 S4 K32 D2048", torch.float32, 4, 2048, 32),
+          ("fp32 S12 D2048", torch.float32, 12, 2048, 16), ("fp32 S16 D2048", torch.float32, 16, 2048, 16),
+          ("fp32 S8 K32 D2048", torch.float32, 8, 2048, 32), ("fp32 S4 K32 D2048", torch.float32, 4, 2048, 32),
           ("fp32 S4 K64 D2048", torch.float32, 4, 2048, 64), ("bf16 S12 K32 D2048", torch.bfloat16, 12, 2048, 32))
 
 
@@ -230,7 +231,8 @@ def shape_calls(dev):
     token count (B 4 x T 4096), SiLU, softmax weights given, full dy, for the
     kernel sizes, channel counts and route counts of SHAPES: the headline shape,
     an even channel count that is not a multiple of 4, 8 / 12 / 16 taps (bf16
-    and fp32), fp32 with 32 and 64 routes, and bf16 with 12 taps and 32 routes.
+    and fp32), fp32 with 32 routes (4 and 8 taps) and 64, and bf16 with 12 taps
+    and 32 routes.
     Returns [(label, fwd, bwd)]."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX_WEIGHTS

@@ -809,10 +809,17 @@ constexpr bool kBwdOneWaveFused = BF ? ((S >= 8 && KC >= 2) || KC >= 4)
 // registers); at one wave, B4 T4096 D2048, 64 routes, backward entry: 8 taps
 // 541 -> 427 us, with SiLU 926 -> 538.  Without SiLU at 6 taps one wave was
 // slower (316 -> 333).
+// The fp32 dx pass spills at two waves with 32 routes from 5 taps with SiLU
+// (40-372 bytes) and from 7 without, with 16 routes at 8 taps with SiLU: one
+// wave there (B4 T4096 D2048 with SiLU, 32 routes: 8 taps 982 -> 816 us, 6
+// taps 638 -> 595).
+template <int S, int KC, bool ACT>
+constexpr bool kF32DxSpills = (KC >= 2 && S >= (ACT ? 5 : 7)) || (KC == 1 && ACT && S == 8);
 template <int S, int KC, int MODE, bool BF, bool ACT = false>
 constexpr int kBwdMinWaves = ((MODE == kBwdFused && kBwdOneWaveFused<S, KC, BF>) ||
                               (MODE == kBwdDx && KC >= 4 && (S >= 7 || (ACT && S >= 5))) ||
-                              (MODE == kBwdDx && KC >= 2 && S > 8))
+                              (MODE == kBwdDx && (KC >= 2 || !BF) && S > 8) ||
+                              (MODE == kBwdDx && !BF && kF32DxSpills<S, KC, ACT>))
                                  ? 1
                                  : (MODE == kBwdTaps ? MOC_BWD_TAPS_WAVES : MOC_BWD_MIN_WAVES);
 
@@ -852,7 +859,6 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
   static_assert(S >= 2 && EOWN > 0, "super-block too small for the kernel size");
   // work of this MODE: dx rows, m products of ST taps from tap s0
   constexpr bool DO_DX = MODE != kBwdTaps, DO_M = MODE != kBwdDx;
-  static_assert(MODE == kBwdFused || BF, "the partial passes are built for bf16");
   // with the activation: P (and g) formed in this pass; g read from gbuf (taps
   // pass) or written there (dx pass)
   constexpr bool PACT = ACT != 0 && MODE != kBwdTaps;
@@ -989,23 +995,29 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
       for (int c = 0; c < NC; ++c) bop[c][s][kc] = C::make(rows[0][c], rows[1][c], rows[2][c], rows[3][c]);
     }
   }
-  // dalpha B operands: bda[s][cg][kx] = basis[16 (kc0 + kx) + j, s0 + s, d0 + 16cg + 4q + v]
-  Op bda[ST][NC][KX];
-  if constexpr (DO_M)
+  // dalpha B operands: bda[s][cg][kx] = basis[16 (kc0 + kx) + j, s0 + s, d0 + 16cg + 4q + v].
+  // The fp32 taps pass loads them per tap where it uses them (from L2): held
+  // through the super-block loop they spill past 8 taps
+  constexpr bool kBdaMem = !BF && MODE == kBwdTaps;
+  auto load_bda = [&](int s, int cg, int kx, E (&e4)[4]) {
+    // (with D % 4 == 2 the last group's upper two channels read the next
+    // row's first two: finite basis values that meet m products of zero, as
+    // a channel pair past D loads x and dy as zeros)
+    const int64_t ch = d0 + 16 * cg + 4 * q;
+    bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s0 + s, 0, rb,
+                             static_cast<uint32_t>(ch * ESZ), wave_on && ch < D && tap_in(s)),
+                     e4);
+  };
+  Op bda[kBdaMem ? 1 : ST][NC][KX];
+  if constexpr (DO_M && !kBdaMem)
 #pragma unroll
   for (int kx = 0; kx < KX; ++kx) {
 #pragma unroll
     for (int s = 0; s < ST; ++s) {
 #pragma unroll
       for (int cg = 0; cg < NC; ++cg) {
-        // (with D % 4 == 2 the last group's upper two channels read the next
-        // row's first two: finite basis values that meet m products of zero, as
-        // a channel pair past D loads x and dy as zeros)
-        const int64_t ch = d0 + 16 * cg + 4 * q;
         E e4[4];
-        bb.load<4 * ESZ>(row_off((16 * (kc0 + kx) + j) * S + s0 + s, 0, rb,
-                                 static_cast<uint32_t>(ch * ESZ), wave_on && ch < D && tap_in(s)),
-                         e4);
+        load_bda(s, cg, kx, e4);
         if constexpr (kBdaLds)  // read back per tap in the dalpha loop (wave-private rows)
           Vec<E, 4>::store(&b_lds[wave][s * 16 * KX + 16 * kx + j][16 * cg + 4 * q], e4);
         else
@@ -1504,8 +1516,24 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
           }
           wave_lds_sync();
         } else {
+        // taps pass: the next super-block's routing weights are loaded before the
+        // m products and go to LDS after them (the other half of the double
+        // buffer has been free since the previous super-block's closing barrier)
+        if constexpr (MODE == kBwdTaps) {
+          if (more) fetch_a(t0 + EOWN);
+        }
 #pragma unroll
         for (int s = 0; s < ST; ++s) {
+          Op bm[kBdaMem ? NC : 1][KX];
+          if constexpr (kBdaMem)
+#pragma unroll
+            for (int cg = 0; cg < NC; ++cg)
+#pragma unroll
+              for (int kx = 0; kx < KX; ++kx) {
+                E e4[4];
+                load_bda(s, cg, kx, e4);
+                bm[cg][kx] = C::make(e4[0], e4[1], e4[2], e4[3]);
+              }
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
             E mv[NP][4][NC];
@@ -1516,7 +1544,8 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
 #pragma unroll
               for (int c = 0; c < NC; ++c) {
                 E parts[NP];
-                float mval = on ? g[r][c] * xw[r + s][c] : 0.f;
+                const float xv = kXOnUse ? C::to_f(xr[r + s][c]) : xw[kXOnUse ? 0 : r + s][c];
+                float mval = on ? g[r][c] * xv : 0.f;
                 if (HXW && use_h && !on && tap_in(s)) mval = g[r][c] * hx[HXW ? r + s : 0][c];
                 MS::split(mval, parts);
 #pragma unroll
@@ -1544,9 +1573,14 @@ bwd_tile(const void* __restrict__ xv, const void* __restrict__ dyv, int64_t dys,
               for (int cg = 0; cg < NC; ++cg) {
                 const Op am = *reinterpret_cast<const Op*>(&m_lds[wave][h][16 * rb + j][16 * cg + 4 * q]);
 #pragma unroll
-                for (int kx = 0; kx < KX; ++kx) dacc[rb][kx] = C::mma(am, bda[s][cg][kx], dacc[rb][kx]);
+                for (int kx = 0; kx < KX; ++kx)
+                  dacc[rb][kx] = C::mma(am, kBdaMem ? bm[kBdaMem ? cg : 0][kx] : bda[kBdaMem ? 0 : s][cg][kx],
+                                        dacc[rb][kx]);
               }
           wave_lds_sync();
+        }
+        if constexpr (MODE == kBwdTaps) {
+          if (more) stage_alpha(buf ^ 1);
         }
         }
       }

@@ -416,7 +416,7 @@ bool supported(const Problem& p) {
 // (the two-pass form)
 bool bwd_supported(const Problem& p) {
   return supported(p) && (p.x_dt == DT_BF16 || p.K <= 32) &&
-         (p.S <= 8 || (p.x_dt == DT_BF16 && p.K <= 16));
+         (p.S <= 8 || p.K <= 16);
 }
 
 size_t forward_workspace(const Problem& p) { return plan(p, false).total; }

@@ -182,8 +182,19 @@ inline Grid2 bwd_grid_tiered(int64_t N, int64_t gx, int64_t D, int64_t S, int n_
 // and no activation needs P: bf16, 32 routes and 4 to 8 taps, 16 routes and 7
 // or 8 taps (measured against the fused pass at every kernel size: below those
 // the fused pass is faster).
+// fp32 (the same two passes on fp32 operands, with and without the activation):
+// 16 routes from 5 taps (4 without the activation) to 16, 32 routes from 4 to
+// 8 taps.  Past 8 taps the fused fp32 tile does not build (its register file);
+// below, measured against the fused pass (B4 T4096 D2048, backward entry, us,
+// without / with SiLU): 16 routes, 4 taps 234 / 290 -> 222 / 295, 6 taps
+// 323 / 414 -> 275 / 356, 8 taps 463 / 562 -> 354 / 461; 32 routes, 4 taps
+// 381 / 464 -> 324 / 415, 6 taps 1177 / 1427 -> 450 / 615, 8 taps
+// 1046 / 1425 -> 704 / 986.
+constexpr bool f32_two_pass(int S, int KC, bool act) {
+  return (KC == 1 && (S >= 5 || (S == 4 && !act))) || (KC == 2 && S >= 4 && S <= 8);
+}
 constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
-  return bf && !act && ((KC == 2 && S >= 4) || (KC == 1 && S >= 7));
+  return !act && ((bf && ((KC == 2 && S >= 4) || (KC == 1 && S >= 7))) || (!bf && f32_two_pass(S, KC, act)));
 }
 // With the activation, the two passes where the fused pass spills or forms the
 // same work per route chunk (bf16: 32 routes and 5 to 8 taps, 16 routes and 8,
@@ -191,7 +202,8 @@ constexpr bool bwd_two_pass(int S, int KC, bool act, bool bf) {
 // pass forms g = dy silu'(P) and leaves it in the workspace (fp32 [N, D]) for the
 // taps pass.  Single launches only (the grouped launch keeps the fused pass).
 constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
-  return bf && act && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8) || (KC == 4 && S >= 3));
+  return act && ((bf && ((KC == 2 && S >= 5) || (KC == 1 && S >= 8) || (KC == 4 && S >= 3))) ||
+                 (!bf && f32_two_pass(S, KC, act)));
 }
 // The prefill runs those two passes (the dx pass's P reading the cache) with 32
 // routes and 6-8 taps and with 64 routes; elsewhere its fused pass measured
@@ -199,9 +211,10 @@ constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
 // routes, 8 taps 232 against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 ->
 // 257 / 335 / 429).
 constexpr bool pre_two_pass_g(int S, int KC) { return (KC == 2 && S >= 6) || KC == 4; }
+// (the prefill passes are built for bf16: fp32 prefill keeps the fused pass)
 inline bool bwd_two_pass_g(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
-  return !p.grouped && (!p.pre || pre_two_pass_g(S, KC)) &&
+  return !p.grouped && (!p.pre || (pre_two_pass_g(S, KC) && p.x_dt == DT_BF16)) &&
          bwd_two_pass_g(S, KC, p.activation != 0, p.x_dt == DT_BF16);
 }
 // 64 routes without activation: the two passes, the taps pass split in route
@@ -213,7 +226,7 @@ constexpr bool pre_two_pass_r(int S) { return S >= 2; }
 inline bool bwd_two_pass(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
   const bool act = p.activation != 0, bf = p.x_dt == DT_BF16;
-  return bwd_two_pass(S, KC, act, bf) || bwd_two_pass_g(p) ||
+  return (bwd_two_pass(S, KC, act, bf) && (bf || !p.pre)) || bwd_two_pass_g(p) ||
          (!p.grouped && (!p.pre || pre_two_pass_r(S)) && bwd_two_pass_r(S, KC, act, bf));
 }
 // route parts of the taps pass's grid (halves with 64 routes), whose single
@@ -489,13 +502,18 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
                 void* dx, float* part_da, float* part_db, float* gbuf, hipStream_t st) {
   const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
-  // 9 to 16 taps: bf16 with up to 16 routes (its two-pass form; the others
-  // spill past what the compiler handles, or past the LDS, and stay generic:
-  // bwd_supported)
+  // 9 to 16 taps: up to 16 routes (the two-pass form; bf16 with more routes
+  // runs backward_chunks, the fp32 forms with more spill past what the compiler
+  // handles and stay generic: bwd_supported)
   if constexpr (S > 8) {
-    if (kc == 1 && bf) {
-      if (act) bwd_one<S, 1, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
-      else bwd_one<S, 1, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+    if (kc == 1) {
+      if (bf) {
+        if (act) bwd_one<S, 1, true, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+        else bwd_one<S, 1, false, true>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+      } else {
+        if (act) bwd_one<S, 1, true, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+        else bwd_one<S, 1, false, false>(p, x, dy, a_c, b_c, dx, part_da, part_db, gbuf, st);
+      }
     }
   } else {
 #define MOC_BWD(KC_)                                                                          \
@@ -592,9 +610,9 @@ void bwd_pre_one(const Problem& p, const void* x, const void* dy, const void* a_
   const Grid2 g = bwd_partials_grid(p);
   // the two-pass shapes of the plain backward: without the activation all of
   // them; with it those of pre_two_pass_g
-  constexpr bool kTwo = bwd_two_pass(S, KC, ACT, BF) ||
-                        (bwd_two_pass_r(S, KC, ACT, BF) && pre_two_pass_r(S)) ||
-                        (bwd_two_pass_g(S, KC, ACT, BF) && pre_two_pass_g(S, KC));
+  constexpr bool kTwo = BF && (bwd_two_pass(S, KC, ACT, BF) ||
+                               (bwd_two_pass_r(S, KC, ACT, BF) && pre_two_pass_r(S)) ||
+                               (bwd_two_pass_g(S, KC, ACT, BF) && pre_two_pass_g(S, KC)));
   if constexpr (kTwo) {
     // the dx pass: without the activation the plain one (dx reads no cache);
     // with it bwd_pre_dx_kernel, which forms P with the cache and writes g to

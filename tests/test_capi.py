@@ -262,12 +262,15 @@ def test_matrix_core_supported_names_the_kernel_family():
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, _lib.DT_F16, bwd) == 0
         assert L.moc_matrix_core_supported(0, 2048, 16, 4, bf, bwd) == 0
     # 9-16 taps: the forward for every route count, the backward for bf16 (past
-    # 16 routes per 16-route chunk) and not for fp32
+    # 16 routes per 16-route chunk) and for fp32 up to 16 routes
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 0) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 1) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 64, 9, bf, 1) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 0) == 1
-    assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 0
+    assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 16, 16, f32, 1) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 32, 9, f32, 0) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 32, 9, f32, 1) == 0
     # fp32 with 33-64 routes up to 8 taps: the forward, and the backward in two
     # route halves
     assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 0) == 1

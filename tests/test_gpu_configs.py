@@ -214,6 +214,8 @@ def test_mfma_matches_generic(dtype, S, K, act):
     (torch.bfloat16, 6, 48, "silu"),   # 64-route two passes, g through the workspace
     (torch.float32, 4, 16, "silu"),
     (torch.float32, 7, 32, None),
+    (torch.float32, 12, 16, "silu"),   # fp32 two passes, g through the workspace
+    (torch.float32, 15, 16, None),     # fp32 two passes
 ])
 @pytest.mark.parametrize("D", [198, 130])
 def test_mfma_even_channel_tails(dtype, S, K, act, D):
@@ -235,7 +237,11 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
     (torch.bfloat16, 16, 64, None, 1),
     (torch.bfloat16, 12, 24, "silu", 1),
     (torch.bfloat16, 13, 48, None, 1),
-    (torch.float32, 11, 16, None, 0),
+    (torch.float32, 11, 16, None, 1),       # fp32 up to 16 routes: the two-pass form
+    (torch.float32, 9, 16, "silu", 1),
+    (torch.float32, 14, 12, "silu", 1),
+    (torch.float32, 16, 16, None, 1),
+    (torch.float32, 13, 8, "silu", 1),
     (torch.float32, 16, 32, "silu", 0),
     (torch.float32, 4, 48, "silu", 1),      # fp32, 33-64 routes: the backward in route halves
     (torch.float32, 8, 64, None, 1),
@@ -243,9 +249,9 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
 ])
 def test_mfma_long_kernels(dtype, S, K, act, bwd):
     """9 to 16 taps: the forward on the matrix cores for every route count, the
-    backward for bf16 (up to 16 routes its two-pass form; past 16 the dx pass
-    over every route, then the taps pass per 16-route chunk; fp32 on the
-    generic kernels); fp32 with 33-64 routes: the forward on the matrix
+    backward up to 16 routes in its two-pass form (bf16 and fp32), for bf16
+    past 16 routes the dx pass over every route, then the taps pass per
+    16-route chunk (fp32 there on the generic kernels); fp32 with 33-64 routes: the forward on the matrix
     cores, the backward in two route halves on the 32-route kernels (dy = g
     from the forward's P, the router gradient over all routes at the end).
     Against the oracle and the generic kernels."""
@@ -303,48 +309,51 @@ def _mfma_vs_generic(dtype, S, K, act, D, Bt=3, T=333, lengths=(1, 2, 70, 3, 200
 
 
 @pytest.mark.parametrize("form", ["rows", "element"])
-@pytest.mark.parametrize("S,K", [(8, 32), (8, 16)])
-def test_two_pass_silu_without_dx(form, S, K):
+@pytest.mark.parametrize("S,K,dtype", [(8, 32, torch.bfloat16), (8, 16, torch.bfloat16),
+                                       (12, 16, torch.float32)])
+def test_two_pass_silu_without_dx(form, S, K, dtype):
     """With SiLU the two-pass backward's dx pass also forms g for the taps pass:
     without dx (need_x false) dalpha and dbasis are those of the call with dx,
     bit for bit, for a full dy and for the one-element dy of y.sum()."""
     from moc import ops
     g = gen(S * 10 + K)
-    x = randn(g, 2, 150, 192, scale=0.5).to(DEV, torch.bfloat16)
-    a = torch.softmax(randn(g, 2, 150, K), -1).to(DEV, torch.bfloat16)
-    b = randn(g, K, S, 192, scale=0.2).to(DEV, torch.bfloat16)
+    x = randn(g, 2, 150, 192, scale=0.5).to(DEV, dtype)
+    a = torch.softmax(randn(g, 2, 150, K), -1).to(DEV, dtype)
+    b = randn(g, K, S, 192, scale=0.2).to(DEV, dtype)
     if form == "rows":
-        dy = randn(g, 2, 150, 192).to(DEV, torch.bfloat16)
+        dy = randn(g, 2, 150, 192).to(DEV, dtype)
     else:
-        dy = torch.ones((), device=DEV, dtype=torch.bfloat16).expand(2, 150, 192)
+        dy = torch.ones((), device=DEV, dtype=dtype).expand(2, 150, 192)
     with_dx = ops.launch_backward(x, a, b, dy, activation_flag=1, need_x=True)
     no_dx = ops.launch_backward(x, a, b, dy, activation_flag=1, need_x=False)
     assert no_dx[0] is None
     assert torch.equal(with_dx[1], no_dx[1]) and torch.equal(with_dx[2], no_dx[2])
-    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
     ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu().expand(2, 150, 192).contiguous(), "silu")
     for n, u, r in zip(("dx", "dalpha", "dbasis"), with_dx, ref[1:]):
-        assert_close(n, u, r, torch.bfloat16)
+        assert_close(n, u, r, dtype)
 
 
-@pytest.mark.parametrize("S,K", [(5, 32), (7, 32), (8, 16), (7, 16)])
+@pytest.mark.parametrize("S,K,dtype", [(5, 32, torch.bfloat16), (7, 32, torch.bfloat16),
+                                       (8, 16, torch.bfloat16), (7, 16, torch.bfloat16),
+                                       (12, 16, torch.float32), (9, 8, torch.float32)])
 @pytest.mark.parametrize("B,T,D", [(1, 1, 64), (1, 2, 4), (2, 3, 132), (1, 17, 260), (3, 40, 68)])
-def test_two_pass_small_and_ragged(S, K, B, T, D):
-    """The two-pass backward (bf16, no activation) at token counts below one
-    super-block and channel counts that leave partial channel groups, against
-    the oracle."""
+def test_two_pass_small_and_ragged(S, K, dtype, B, T, D):
+    """The two-pass backward (no activation; bf16, and fp32 past 8 taps) at
+    token counts below one super-block and channel counts that leave partial
+    channel groups, against the oracle."""
     g = gen(S * 1000 + K * 10 + T)
-    x = randn(g, B, T, D, scale=0.5).to(DEV, torch.bfloat16)
-    a = torch.softmax(randn(g, B, T, K), -1).to(DEV, torch.bfloat16)
-    b = randn(g, K, S, D, scale=0.2).to(DEV, torch.bfloat16)
-    dy = randn(g, B, T, D).to(DEV, torch.bfloat16)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, dtype)
+    a = torch.softmax(randn(g, B, T, K), -1).to(DEV, dtype)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
+    dy = randn(g, B, T, D).to(DEV, dtype)
     xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
     y, _ = moc_triton(xx, aa, bb)
     y.backward(dy)
-    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
     ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), None)
     for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), (y, xx.grad, aa.grad, bb.grad), ref):
-        assert_close(n, u, r, torch.bfloat16)
+        assert_close(n, u, r, dtype)
 
 
 @pytest.mark.parametrize("S,K", [(2, 8), (3, 16), (4, 16), (4, 20), (8, 32), (8, 5), (5, 16), (6, 24),
