@@ -126,7 +126,13 @@ bool use_mfma_bwd(const moc::Problem& p) {
   if (p.path == MOC_PATH_GENERIC) return false;
   return moc::mfma::bwd_supported(p);
 }
-// fp32 with 33-64 routes: the backward in two route halves on the matrix cores
+// fp32 forward with 33-64 routes at 9-16 taps: route halves on the matrix cores
+bool use_routesplit_fwd(const moc::Problem& p) {
+  if (p.path == MOC_PATH_GENERIC) return false;
+  return !moc::mfma::supported(p) && moc::mfma::routesplit_fwd_supported(p);
+}
+// fp32 backward with 33-64 routes up to 8 taps or 17-64 at 9-16: route parts on
+// the matrix cores
 bool use_routesplit(const moc::Problem& p) {
   if (p.path == MOC_PATH_GENERIC) return false;
   return !moc::mfma::bwd_supported(p) && moc::mfma::routesplit_supported(p);
@@ -139,7 +145,9 @@ bool use_chunks(const moc::Problem& p) {
 }
 
 size_t forward_bytes(const moc::Problem& p) {
-  return use_mfma(p) ? moc::mfma::forward_workspace(p) : fwd_bytes(p.n_tokens, p.D, p.K, p.S);
+  if (use_mfma(p)) return moc::mfma::forward_workspace(p);
+  if (use_routesplit_fwd(p)) return moc::mfma::routesplit_fwd_workspace(p);
+  return fwd_bytes(p.n_tokens, p.D, p.K, p.S);
 }
 
 size_t backward_bytes(const moc::Problem& p) {
@@ -203,6 +211,10 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (use_mfma(p)) {
     moc::mfma::forward(p, x, alpha, basis, y, workspace, st);
+    return hip_status("moc_forward launch");
+  }
+  if (use_routesplit_fwd(p)) {
+    moc::mfma::forward_routesplit(p, x, alpha, basis, y, workspace, st);
     return hip_status("moc_forward launch");
   }
   Carve cv{static_cast<char*>(workspace), 0};
@@ -379,7 +391,10 @@ int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t 
   if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return (backward ? use_mfma_bwd(p) || use_routesplit(p) || use_chunks(p) : use_mfma(p)) ? 1 : 0;
+  return (backward ? use_mfma_bwd(p) || use_routesplit(p) || use_chunks(p)
+                   : use_mfma(p) || use_routesplit_fwd(p))
+             ? 1
+             : 0;
 }
 
 int moc_prefill_supported(int64_t n_seqs, int64_t seq_len, int64_t dim, int64_t k,

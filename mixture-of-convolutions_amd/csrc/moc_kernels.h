@@ -57,15 +57,22 @@ void launch_update_generic(const void* x, const void* alpha, const void* basis, 
 // MFMA path (moc_mfma_common.hip): supported() for the forward (2 <= S <= 16,
 // K <= 32, or <= 64 with bf16 x or S <= 8; D even), bwd_supported() for the
 // backward in one pass family (the same with S <= 8 and K <= 32 for fp32 x, or
-// bf16 with K <= 16 up to S = 16), routesplit_supported() for fp32 with 33-64
-// routes up to S = 8
+// bf16 and fp32 with K <= 16 up to S = 16), routesplit_supported() for the
+// fp32 backward in route parts (33-64 routes up to S = 8, 17-64 routes at S 9
+// to 16), routesplit_fwd_supported() for the fp32 forward in route halves (33-64
+// routes at S 9 to 16)
 namespace mfma {
 bool supported(const Problem& p);
 bool bwd_supported(const Problem& p);
-// the backward of fp32 layers with 33-64 routes up to 8 taps in two route
-// halves on the 32-route kernels (moc_routesplit.hip)
+// fp32 layers in route parts (moc_routesplit.hip): the backward with 33-64
+// routes up to 8 taps (parts of 32) and 17-64 routes at 9-16 taps (parts of
+// 16); the forward with 33-64 routes at 9-16 taps (halves of 32)
 bool routesplit_supported(const Problem& p);
 size_t routesplit_workspace(const Problem& p);
+bool routesplit_fwd_supported(const Problem& p);
+size_t routesplit_fwd_workspace(const Problem& p);
+void forward_routesplit(const Problem& p, const void* x, const void* alpha, const void* basis,
+                        void* y, void* workspace, hipStream_t st);
 // the backward of bf16 layers with 9-16 taps and 17-64 routes: the dx pass over
 // every route, then the taps pass per 16-route chunk (moc_mfma_common.hip)
 bool chunks_supported(const Problem& p);

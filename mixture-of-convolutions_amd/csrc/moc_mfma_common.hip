@@ -412,8 +412,8 @@ bool supported(const Problem& p) {
 }
 
 // The backward: fp32 with up to 32 routes (the fused fp32 tile over 64 routes
-// crashes LLVM's AGPR-copy rewrite); 9 to 16 taps for bf16 with up to 16 routes
-// (the two-pass form)
+// crashes LLVM's AGPR-copy rewrite); 9 to 16 taps with up to 16 routes (the
+// two-pass form)
 bool bwd_supported(const Problem& p) {
   return supported(p) && (p.x_dt == DT_BF16 || p.K <= 32) &&
          (p.S <= 8 || p.K <= 16);

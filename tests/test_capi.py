@@ -255,14 +255,16 @@ def test_matrix_core_supported_names_the_kernel_family():
         assert L.moc_matrix_core_supported(1024, 2050, 32, 8, f32, bwd) == 1
         assert L.moc_matrix_core_supported(1024, 197, 16, 4, bf, bwd) == 0    # D odd
         assert L.moc_matrix_core_supported(1024, 2048, 64, 2, bf, bwd) == 1
-        assert L.moc_matrix_core_supported(1024, 2048, 48, 12, f32, bwd) == 0  # fp32 x, K > 32, S > 8
+        assert L.moc_matrix_core_supported(1024, 2048, 48, 12, f32, bwd) == 1  # fp32, route parts
+        assert L.moc_matrix_core_supported(1024, 2048, 80, 12, f32, bwd) == 0  # past 64 routes
         assert L.moc_matrix_core_supported(1024, 2048, 16, 12, bf, bwd) == 1  # 9-16 taps, 16 routes
         assert L.moc_matrix_core_supported(1024, 2048, 16, 17, bf, bwd) == 0
         assert L.moc_matrix_core_supported(1024, 2048, 16, 1, bf, bwd) == 0
         assert L.moc_matrix_core_supported(1024, 2048, 16, 4, _lib.DT_F16, bwd) == 0
         assert L.moc_matrix_core_supported(0, 2048, 16, 4, bf, bwd) == 0
-    # 9-16 taps: the forward for every route count, the backward for bf16 (past
-    # 16 routes per 16-route chunk) and for fp32 up to 16 routes
+    # 9-16 taps: the forward for every route count (fp32 past 32 routes in
+    # route halves), the backward for bf16 (past 16 routes per 16-route chunk)
+    # and for fp32 (past 16 routes in parts of 16)
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 0) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 32, 16, bf, 1) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 64, 9, bf, 1) == 1
@@ -270,7 +272,9 @@ def test_matrix_core_supported_names_the_kernel_family():
     assert L.moc_matrix_core_supported(1024, 2048, 16, 9, f32, 1) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 16, 16, f32, 1) == 1
     assert L.moc_matrix_core_supported(1024, 2048, 32, 9, f32, 0) == 1
-    assert L.moc_matrix_core_supported(1024, 2048, 32, 9, f32, 1) == 0
+    assert L.moc_matrix_core_supported(1024, 2048, 32, 9, f32, 1) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 64, 16, f32, 0) == 1
+    assert L.moc_matrix_core_supported(1024, 2048, 64, 16, f32, 1) == 1
     # fp32 with 33-64 routes up to 8 taps: the forward, and the backward in two
     # route halves
     assert L.moc_matrix_core_supported(1024, 2048, 48, 4, f32, 0) == 1

@@ -242,7 +242,11 @@ def test_mfma_even_channel_tails(dtype, S, K, act, D):
     (torch.float32, 14, 12, "silu", 1),
     (torch.float32, 16, 16, None, 1),
     (torch.float32, 13, 8, "silu", 1),
-    (torch.float32, 16, 32, "silu", 0),
+    (torch.float32, 16, 32, "silu", 1),     # fp32 past 16 routes: parts of 16 routes
+    (torch.float32, 10, 20, None, 1),
+    (torch.float32, 12, 48, "silu", 1),     # and the forward in halves of 32 routes
+    (torch.float32, 9, 64, None, 1),
+    (torch.float32, 15, 40, "silu", 1),
     (torch.float32, 4, 48, "silu", 1),      # fp32, 33-64 routes: the backward in route halves
     (torch.float32, 8, 64, None, 1),
     (torch.float32, 3, 40, "silu", 1),
@@ -251,10 +255,12 @@ def test_mfma_long_kernels(dtype, S, K, act, bwd):
     """9 to 16 taps: the forward on the matrix cores for every route count, the
     backward up to 16 routes in its two-pass form (bf16 and fp32), for bf16
     past 16 routes the dx pass over every route, then the taps pass per
-    16-route chunk (fp32 there on the generic kernels); fp32 with 33-64 routes: the forward on the matrix
-    cores, the backward in two route halves on the 32-route kernels (dy = g
-    from the forward's P, the router gradient over all routes at the end).
-    Against the oracle and the generic kernels."""
+    16-route chunk, for fp32 past 16 routes in parts of 16 routes (dy = g from
+    P, the router gradient over all routes at the end), with P and the forward
+    past 32 routes as the sum of two 32-route forwards; fp32 with 33-64 routes
+    up to 8 taps: the forward on the matrix cores, the backward in two route
+    halves on the 32-route kernels.  Against the oracle and the generic
+    kernels."""
     L = _lib.lib()
     assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 0) == 1
     assert L.moc_matrix_core_supported(3 * 333, 192, K, S, _lib.dtype_code(dtype), 1) == bwd
