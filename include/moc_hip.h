@@ -85,10 +85,11 @@ int moc_set_kernel_path(int path);
  * current moc_set_kernel_path), 0 when it runs the generic kernels.  No
  * counterpart in the reference, whose Triton kernels take every shape; it lets
  * a caller or a test see which family serves a shape.  Matrix-core forward
- * and backward: 2 <= kernel_size <= 16, k <= 64, dim even, x bf16 or f32
- * (some shapes in route parts: the f32 forward past 32 routes beyond
- * kernel_size 8, the backward past 16 routes beyond kernel_size 8 and the f32
- * backward past 32 routes).
+ * and backward: 2 <= kernel_size <= 16, k <= 64, x bf16 or f32 (some shapes
+ * in route parts: the f32 forward past 32 routes beyond kernel_size 8, the
+ * backward past 16 routes beyond kernel_size 8 and the f32 backward past 32
+ * routes); an odd dim through a copy padded with a zero channel (not with
+ * route parts).
  */
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
                               int x_dtype, int backward);

@@ -144,14 +144,22 @@ bool use_chunks(const moc::Problem& p) {
   return !moc::mfma::bwd_supported(p) && moc::mfma::chunks_supported(p);
 }
 
+// odd channel counts: the matrix-core kernels on a zero-padded copy
+bool use_pad(const moc::Problem& p, bool backward) {
+  if (p.path == MOC_PATH_GENERIC) return false;
+  return moc::mfma::pad_supported(p, backward);
+}
+
 size_t forward_bytes(const moc::Problem& p) {
   if (use_mfma(p)) return moc::mfma::forward_workspace(p);
+  if (use_pad(p, false)) return moc::mfma::pad_workspace(p, false);
   if (use_routesplit_fwd(p)) return moc::mfma::routesplit_fwd_workspace(p);
   return fwd_bytes(p.n_tokens, p.D, p.K, p.S);
 }
 
 size_t backward_bytes(const moc::Problem& p) {
   if (use_mfma_bwd(p)) return moc::mfma::backward_workspace(p);
+  if (use_pad(p, true)) return moc::mfma::pad_workspace(p, true);
   if (use_chunks(p)) return moc::mfma::chunks_workspace(p);
   return use_routesplit(p) ? moc::mfma::routesplit_workspace(p) : bwd_bytes(p);
 }
@@ -215,6 +223,10 @@ int moc_forward(const void* x, const void* alpha, const void* basis, void* y,
   }
   if (use_routesplit_fwd(p)) {
     moc::mfma::forward_routesplit(p, x, alpha, basis, y, workspace, st);
+    return hip_status("moc_forward launch");
+  }
+  if (use_pad(p, false)) {
+    moc::mfma::forward_padded(p, x, alpha, basis, y, workspace, st);
     return hip_status("moc_forward launch");
   }
   Carve cv{static_cast<char*>(workspace), 0};
@@ -284,6 +296,10 @@ int backward_launch(const moc::Problem& p, const void* x, const void* alpha, con
   }
   if (use_routesplit(p)) {
     moc::mfma::backward_routesplit(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
+    return hip_status("moc_backward launch");
+  }
+  if (use_pad(p, true)) {
+    moc::mfma::backward_padded(p, x, alpha, basis, dy, dx, dalpha, dbasis, workspace, st);
     return hip_status("moc_backward launch");
   }
   if (use_chunks(p)) {
@@ -391,8 +407,8 @@ int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t 
   if (x_dtype != MOC_DT_BF16 && x_dtype != MOC_DT_F32) return 0;
   moc::Problem p = make_problem(nullptr, 0, 0, n_tokens, n_tokens, dim, k, kernel_size, x_dtype,
                                 MOC_DT_F32, MOC_DT_F32, 0, MOC_ROUTE_ALPHA);
-  return (backward ? use_mfma_bwd(p) || use_routesplit(p) || use_chunks(p)
-                   : use_mfma(p) || use_routesplit_fwd(p))
+  return (backward ? use_mfma_bwd(p) || use_routesplit(p) || use_chunks(p) || use_pad(p, true)
+                   : use_mfma(p) || use_routesplit_fwd(p) || use_pad(p, false))
              ? 1
              : 0;
 }

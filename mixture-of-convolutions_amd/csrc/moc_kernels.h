@@ -83,6 +83,14 @@ void backward_chunks(const Problem& p, const void* x, const void* alpha, const v
 void backward_routesplit(const Problem& p, const void* x, const void* alpha, const void* basis,
                          const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
                          hipStream_t st);
+// odd channel counts through a zero-padded copy at D + 1 channels (moc_pad.hip)
+bool pad_supported(const Problem& p, bool backward);
+size_t pad_workspace(const Problem& p, bool backward);
+void forward_padded(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,
+                    void* workspace, hipStream_t st);
+void backward_padded(const Problem& p, const void* x, const void* alpha, const void* basis,
+                     const void* dy, void* dx, void* dalpha, void* dbasis, void* workspace,
+                     hipStream_t st);
 size_t forward_workspace(const Problem& p);
 size_t backward_workspace(const Problem& p);
 void forward(const Problem& p, const void* x, const void* alpha, const void* basis, void* y,

@@ -268,9 +268,46 @@ def test_mfma_long_kernels(dtype, S, K, act, bwd):
 
 
 @pytest.mark.parametrize("dtype,S,K,act,D", [
+    (torch.bfloat16, 4, 16, "silu", 197),    # the lean fused pass
+    (torch.bfloat16, 8, 32, None, 129),      # two passes
+    (torch.float32, 6, 24, "silu", 65),
+    (torch.bfloat16, 12, 16, None, 131),     # 12 taps
+    (torch.bfloat16, 3, 64, "silu", 191),    # 64 routes
+])
+def test_odd_channel_counts_padded(dtype, S, K, act, D):
+    """Odd channel counts run the matrix-core kernels on a copy padded with a
+    zero channel, against the oracle and the generic kernels, fixed and packed."""
+    L = _lib.lib()
+    for bwd in (0, 1):
+        assert L.moc_matrix_core_supported(3 * 333, D, K, S, _lib.dtype_code(dtype), bwd) == 1
+    _mfma_vs_generic(dtype, S, K, act, D)
+
+
+@pytest.mark.parametrize("form", ["element", "row"])
+def test_odd_channel_count_broadcast_dy(form):
+    """The padded backward with the dy of y.sum() (one element) and with one
+    dy row for every token, against the oracle."""
+    from moc import ops
+    g = gen(7)
+    D, K, S = 197, 16, 4
+    x = randn(g, 2, 150, D, scale=0.5).to(DEV, torch.bfloat16)
+    a = torch.softmax(randn(g, 2, 150, K), -1).to(DEV, torch.bfloat16)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, torch.bfloat16)
+    if form == "element":
+        dy = torch.ones((), device=DEV, dtype=torch.bfloat16).expand(2, 150, D)
+    else:
+        dy = randn(g, D).to(DEV, torch.bfloat16).expand(2, 150, D)
+    got = ops.launch_backward(x, a, b, dy, activation_flag=1, need_x=True)
+    rx, ra, rb = O.reference_inputs(x, a, b, torch.bfloat16)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu().contiguous(), "silu")
+    for n, u, r in zip(("dx", "dalpha", "dbasis"), got, ref[1:]):
+        assert_close(n, u, r, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype,S,K,act,D", [
     (torch.bfloat16, 17, 16, "silu", 192),   # past 16 taps
     (torch.bfloat16, 4, 80, None, 192),      # past 64 routes
-    (torch.bfloat16, 4, 16, "silu", 197),    # odd channel count
+    (torch.float32, 12, 48, "silu", 197),    # odd channel count with fp32 route parts
 ])
 def test_generic_path_matches_oracle(dtype, S, K, act, D):
     """The shapes outside the matrix-core kernels (forward and backward) run
