@@ -56,9 +56,10 @@ struct Grid2 {
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Route chunks of 16 the kernels are built for: 1, 2 or 4 (K <= 64; K in
-// (32, 64] is padded to 64 routes).  Four chunks with bf16 data only: the fp32
-// fused backward at four chunks crashes LLVM's AGPR-copy rewrite, so fp32 x
-// with K > 32 stays on the generic kernels.
+// (32, 64] is padded to 64 routes).  Four chunks in the backward with bf16
+// data only: the fp32 fused backward at four chunks crashes LLVM's AGPR-copy
+// rewrite, so the fp32 backward with K > 32 runs in route parts
+// (moc_routesplit.hip).
 inline int route_chunks(int64_t K) { return K <= 16 ? 1 : (K <= 32 ? 2 : 4); }
 template <int KC, bool BF>
 constexpr bool kcOK = KC <= 2 || BF;
@@ -502,9 +503,9 @@ void launch_bwd(const Problem& p, const void* x, const void* dy, const void* a_c
                 void* dx, float* part_da, float* part_db, float* gbuf, hipStream_t st) {
   const int kc = route_chunks(p.K);
   const bool bf = p.x_dt == DT_BF16, act = p.activation != 0;
-  // 9 to 16 taps: up to 16 routes (the two-pass form; bf16 with more routes
-  // runs backward_chunks, the fp32 forms with more spill past what the compiler
-  // handles and stay generic: bwd_supported)
+  // 9 to 16 taps: up to 16 routes (the two-pass form; with more routes bf16
+  // runs backward_chunks and fp32 the route parts of moc_routesplit.hip: the
+  // forms over more routes spill past what the compiler handles)
   if constexpr (S > 8) {
     if (kc == 1) {
       if (bf) {
