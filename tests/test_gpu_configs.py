@@ -283,6 +283,33 @@ def test_odd_channel_counts_padded(dtype, S, K, act, D):
     _mfma_vs_generic(dtype, S, K, act, D)
 
 
+@pytest.mark.parametrize("S,K,dtype,act,D", [
+    (4, 16, torch.bfloat16, "silu", 65),     # padded copy
+    (8, 32, torch.bfloat16, None, 3),        # padded copy, two passes
+    (12, 32, torch.float32, "silu", 66),     # route parts of 16
+    (12, 48, torch.float32, None, 130),      # route parts, forward in halves
+    (6, 64, torch.float32, "silu", 4),       # route halves of 32
+])
+@pytest.mark.parametrize("B,T", [(1, 1), (1, 2), (2, 3), (1, 17), (3, 40)])
+def test_parts_and_padding_small(S, K, dtype, act, D, B, T):
+    """The padded and route-part forms at token counts below one super-block
+    and small channel counts, forward and backward against the oracle."""
+    L = _lib.lib()
+    assert L.moc_matrix_core_supported(B * T, D, K, S, _lib.dtype_code(dtype), 1) == 1
+    g = gen(S * 1000 + K * 10 + T + D)
+    x = randn(g, B, T, D, scale=0.5).to(DEV, dtype)
+    a = torch.softmax(randn(g, B, T, K), -1).to(DEV, dtype)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, dtype)
+    dy = randn(g, B, T, D).to(DEV, dtype)
+    xx, aa, bb = (t.clone().requires_grad_() for t in (x, a, b))
+    y, _ = moc_triton(xx, aa, bb, activation=act)
+    y.backward(dy)
+    rx, ra, rb = O.reference_inputs(x, a, b, dtype)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu(), act)
+    for n, u, r in zip(("y", "dx", "dalpha", "dbasis"), (y, xx.grad, aa.grad, bb.grad), ref):
+        assert_close(n, u, r, dtype)
+
+
 @pytest.mark.parametrize("form", ["element", "row"])
 def test_odd_channel_count_broadcast_dy(form):
     """The padded backward with the dy of y.sum() (one element) and with one
