@@ -379,6 +379,7 @@ struct BwdLayer {
   int64_t D;
   int gx, gy, gy1, n_old, n_total, blk0;
   int act;         // this layer's activation (read where the kernel's ACT is kActRuntime)
+  float* gbuf;     // the two passes with the activation: g = dy silu'(P), fp32 [N, D]
 };
 struct BwdLayers {
   int n;
@@ -1818,7 +1819,7 @@ bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(
       Lp->x, Lp->dy, Lp->dys, static_cast<const E*>(Lp->a), static_cast<const E*>(Lp->b), Lp->dx,
       Lp->part_da, Lp->part_db, seq, Lp->D, bx, by, zh, Lp->gy, Lp->gy1, Lp->n_old, Lp->n_total,
-      Pre{nullptr, nullptr}, nullptr, Lp->act != 0);
+      Pre{nullptr, nullptr}, Lp->gbuf, Lp->act != 0);
 }
 
 }  // namespace mfma

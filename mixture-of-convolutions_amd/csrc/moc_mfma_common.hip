@@ -748,13 +748,14 @@ bool layers_grouped(const Problem* ps, int n, bool backward) {
     if (p.S != ps[0].S || p.n_tokens != ps[0].n_tokens || p.path != ps[0].path) return false;
   }
   // the backward shapes whose single launch runs a two-pass form the grouped
-  // launch does not have (with SiLU; 64 routes) run as single launches, so the
-  // results stay those of the per-layer calls
+  // launch does not have (64 routes: the taps pass in route halves) run as
+  // single launches, so the results stay those of the per-layer calls
   if (backward) {
     for (int i = 0; i < n; ++i) {
       const int S = static_cast<int>(ps[i].S), KC = route_chunks(ps[i].K);
       const bool act = ps[i].activation != 0;
-      if (bwd_two_pass_g(S, KC, act, true) || bwd_two_pass_r(S, KC, act, true)) return false;
+      if ((bwd_two_pass_g(S, KC, act, true) && KC == 4) || bwd_two_pass_r(S, KC, act, true))
+        return false;
     }
   }
   return true;
@@ -762,11 +763,12 @@ bool layers_grouped(const Problem* ps, int n, bool backward) {
 
 namespace {
 // Stage-1 class of a layer in a grouped backward: its route chunks, and its
-// activation where the layers without one run the two-pass form (the layers
-// with one run the fused pass: they cannot share that launch).
+// activation where either activation's layers run a two-pass form (the two
+// forms, or a two-pass and a fused one, cannot share a launch).
 int bwd_class(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
-  const int act = bwd_two_pass(S, KC, false, true) ? (p.activation != 0 ? 1 : 0) : 2;
+  const bool two = bwd_two_pass(S, KC, false, true) || bwd_two_pass_g(S, KC, true, true);
+  const int act = two ? (p.activation != 0 ? 1 : 0) : 2;
   return KC * 4 + act;
 }
 }  // namespace
@@ -853,6 +855,7 @@ void backward_layers(const Problem* ps, const LayerIO* io, int n, void* workspac
     L[i].D = p.D;
     L[i].act = p.activation != 0;
     L[i].kc = route_chunks(p.K);
+    L[i].gbuf = bwd_two_pass_g(p) ? reinterpret_cast<float*>(ws + pl.off_g) : nullptr;
     const int grad = route_grad(p.routing);
     s2.l[i] = Stage2Layer{L[i].part_da,
                           static_cast<int64_t>(pl.bg.gx),

@@ -212,10 +212,11 @@ constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
 // routes, 8 taps 232 against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 ->
 // 257 / 335 / 429).
 constexpr bool pre_two_pass_g(int S, int KC) { return (KC == 2 && S >= 6) || KC == 4; }
-// (the prefill passes are built for bf16: fp32 prefill keeps the fused pass)
+// (the prefill passes are built for bf16: fp32 prefill keeps the fused pass;
+// grouped launches take it up to 32 routes: their taps pass has no route halves)
 inline bool bwd_two_pass_g(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
-  return !p.grouped && (!p.pre || (pre_two_pass_g(S, KC) && p.x_dt == DT_BF16)) &&
+  return (!p.grouped || KC <= 2) && (!p.pre || (pre_two_pass_g(S, KC) && p.x_dt == DT_BF16)) &&
          bwd_two_pass_g(S, KC, p.activation != 0, p.x_dt == DT_BF16);
 }
 // 64 routes without activation: the two passes, the taps pass split in route
@@ -265,6 +266,7 @@ struct LayerOps {
   int64_t D;
   int act;   // the layer's activation (0 / 1)
   int kc;    // the layer's route chunks (1, 2 or 4)
+  float* gbuf;  // backward, two passes with the activation: the layer's g buffer
 };
 
 template <int S, int KC, bool ACT, bool BF>
@@ -373,8 +375,11 @@ template <int S, int KC, int ACT>
 void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
   constexpr bool kSplit = KC >= 2;
   // (mixed activations run the fused pass: grouping admits them only where
-  // both activations' single launches run it)
-  constexpr bool kTwo = ACT != kActRuntime && bwd_two_pass(S, KC, ACT == 1, true);
+  // both activations' single launches run it).  The two passes: without the
+  // activation as bwd_two_pass, with it as bwd_two_pass_g up to 32 routes (the
+  // dx pass then forms g for every layer, also those without dx)
+  constexpr bool kTwoG = ACT == 1 && KC <= 2 && bwd_two_pass_g(S, KC, true, true);
+  constexpr bool kTwo = (ACT != kActRuntime && bwd_two_pass(S, KC, ACT == 1, true)) || kTwoG;
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, true> == 2;
   const int n_cu = device_cu_count();
   // each layer's grid as bwd_one forms it (the taps pass has its own)
@@ -388,11 +393,13 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
                            : bwd_grid(p.n_tokens, L[i].D, S);
     ly.l[i] = BwdLayer{L[i].x, L[i].dy, L[i].dys, L[i].a_c, L[i].b_c, L[i].dx, L[i].part_da,
                        L[i].part_db, L[i].D, static_cast<int>(g.gx), static_cast<int>(g.gy),
-                       g.gy1, g.n_old, g.n_total, static_cast<int>(blk), L[i].act};
+                       g.gy1, g.n_old, g.n_total, static_cast<int>(blk), L[i].act,
+                       kTwoG ? L[i].gbuf : nullptr};
     const int64_t tiles = static_cast<int64_t>(g.gx) * g.gy;
-    // the dx pass of the two-pass form skips layers without dx (no blocks:
-    // layer_index then never selects them)
-    blk += kSplit ? 8 * KC * cdiv(tiles, 8) : (kTwo && L[i].dx == nullptr ? 0 : tiles);
+    // the dx pass of the two-pass form without the activation skips layers
+    // without dx (no blocks: layer_index then never selects them)
+    blk += kSplit && !kTwo ? 8 * KC * cdiv(tiles, 8)
+                           : (kTwo && !kTwoG && L[i].dx == nullptr ? 0 : tiles);
     any_dx = any_dx || L[i].dx != nullptr;
     if constexpr (kTwo) {
       const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(L[i].D, kTapsCW), L[i].D, S, n_cu);
@@ -408,7 +415,7 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
     }
   }
   if constexpr (kTwo) {
-    if (any_dx)
+    if (any_dx || kTwoG)
       hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, false, kBwdDx>),
                          dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
     hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, true, false, kBwdTaps>),

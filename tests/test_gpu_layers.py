@@ -3,9 +3,10 @@ single-layer entries, through the C ABI: every layer's y, dx, dalpha and dbasis
 bit for bit.  The grouped kernels run each layer's own grid inside one launch,
 so each workgroup does exactly the work of the single-layer launch; layers may
 differ in K and activation (one forward launch; one backward stage-1 launch
-per route count, and per activation where the layers without one run the
-two-pass form); layers that cannot share one launch (fp32, or the generic
-kernels) run one by one inside the same entry."""
+per route count, and per activation where a two-pass form runs: with SiLU
+each layer's g goes through its own workspace); layers that cannot share one
+launch (fp32, 64 routes in two passes, or the generic kernels) run one by one
+inside the same entry."""
 from __future__ import annotations
 
 import itertools
@@ -41,7 +42,11 @@ CASES = [
      torch.bfloat16),                                                            # 16 | 32 (two passes)
     ([128, 256], [16, 32], 3, [0, 1], [0, 3], [False, True], torch.bfloat16),    # 16 | 32 with SiLU
     ([128, 64, 96], [32, 16, 12], 5, [1, 1, 0], [3, 3, 4], [True, True, True], torch.bfloat16),
-    ([128, 64], 32, 8, [0, 1], [3, 3], [True, True], torch.bfloat16),            # one by one (SiLU two passes)
+    ([128, 64], 32, 8, [0, 1], [3, 3], [True, True], torch.bfloat16),            # two forms, two launches
+    # SiLU two passes (g through each layer's workspace), grouped
+    ([512, 256, 128], 32, 6, 1, [3, 4, 3], [True, True, False], torch.bfloat16),
+    ([256, 192], 16, 8, 1, [3, 0], [False, True], torch.bfloat16),
+    ([256, 128, 64], [32, 16, 32], 8, [1, 1, 0], [3, 3, 4], [True, False, True], torch.bfloat16),
 ]
 
 
@@ -85,7 +90,7 @@ def test_layers_match_single_layer_entries(dims, K, S, act, codes, need, dtype):
     _check(dims, K, S, act, codes, need, dtype, (3, 211))
 
 
-@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3] + CASES[11:15])
+@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3] + CASES[11:15] + CASES[-3:])
 def test_layers_match_single_layer_entries_packed(dims, K, S, act, codes, need, dtype):
     lengths = [1, 90, 3, 250, 17, 199, 73]
     cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int32, device=DEV)
