@@ -240,8 +240,8 @@ int moc_backward_prefill(const void* x, const void* alpha, const void* basis, co
  * every layer is bf16 and on the matrix-core kernels, the forward is one launch
  * over all layers' channels, and the backward one stage-1 launch per route
  * count present (per route count and activation where the single launches
- * run a two-pass form) plus one stage-2 launch; layers of 64 routes whose
- * single launch runs two passes, and any other set, run one by one.  Results equal moc_forward / moc_backward per
+ * run a two-pass form) plus one stage-2 launch; otherwise the layers run one
+ * by one.  Results equal moc_forward / moc_backward per
  * layer bit for bit.  1 <= n_layers <= 4.
  */
 typedef struct MocLayer {

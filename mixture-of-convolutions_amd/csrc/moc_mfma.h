@@ -1814,7 +1814,7 @@ bwd_layers_kernel(BwdLayers ly, SeqLayout seq) {
     }
   }
   int bx, by, zh;
-  if (!bwd_block<SPLIT ? KC : 1>(Lp->gx, Lp->gy, local, row, bx, by, zh))
+  if (!bwd_block<kRouteParts<KC, SPLIT, MODE>>(Lp->gx, Lp->gy, local, row, bx, by, zh))
     return;  // whole workgroup, before any barrier
   bwd_tile<S, KC, NB, NC, WPG, ACT, BF, SPLIT, MODE>(
       Lp->x, Lp->dy, Lp->dys, static_cast<const E*>(Lp->a), static_cast<const E*>(Lp->b), Lp->dx,

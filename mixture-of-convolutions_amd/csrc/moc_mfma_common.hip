@@ -747,17 +747,7 @@ bool layers_grouped(const Problem* ps, int n, bool backward) {
     if (!supported(p) || p.x_dt != DT_BF16 || p.S > 8) return false;
     if (p.S != ps[0].S || p.n_tokens != ps[0].n_tokens || p.path != ps[0].path) return false;
   }
-  // the backward shapes whose single launch runs a two-pass form the grouped
-  // launch does not have (64 routes: the taps pass in route halves) run as
-  // single launches, so the results stay those of the per-layer calls
-  if (backward) {
-    for (int i = 0; i < n; ++i) {
-      const int S = static_cast<int>(ps[i].S), KC = route_chunks(ps[i].K);
-      const bool act = ps[i].activation != 0;
-      if ((bwd_two_pass_g(S, KC, act, true) && KC == 4) || bwd_two_pass_r(S, KC, act, true))
-        return false;
-    }
-  }
+  (void)backward;  // every backward form of a single launch has its grouped counterpart
   return true;
 }
 
@@ -767,7 +757,8 @@ namespace {
 // forms, or a two-pass and a fused one, cannot share a launch).
 int bwd_class(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
-  const bool two = bwd_two_pass(S, KC, false, true) || bwd_two_pass_g(S, KC, true, true);
+  const bool two = bwd_two_pass(S, KC, false, true) || bwd_two_pass_r(S, KC, false, true) ||
+                   bwd_two_pass_g(S, KC, true, true);
   const int act = two ? (p.activation != 0 ? 1 : 0) : 2;
   return KC * 4 + act;
 }

@@ -212,24 +212,23 @@ constexpr bool bwd_two_pass_g(int S, int KC, bool act, bool bf) {
 // routes, 8 taps 232 against 262; 32 routes, 6 / 7 / 8 taps 365 / 610 / 970 ->
 // 257 / 335 / 429).
 constexpr bool pre_two_pass_g(int S, int KC) { return (KC == 2 && S >= 6) || KC == 4; }
-// (the prefill passes are built for bf16: fp32 prefill keeps the fused pass;
-// grouped launches take it up to 32 routes: their taps pass has no route halves)
+// (the prefill passes are built for bf16: fp32 prefill keeps the fused pass)
 inline bool bwd_two_pass_g(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
-  return (!p.grouped || KC <= 2) && (!p.pre || (pre_two_pass_g(S, KC) && p.x_dt == DT_BF16)) &&
+  return (!p.pre || (pre_two_pass_g(S, KC) && p.x_dt == DT_BF16)) &&
          bwd_two_pass_g(S, KC, p.activation != 0, p.x_dt == DT_BF16);
 }
 // 64 routes without activation: the two passes, the taps pass split in route
 // halves (two workgroups per tile, each forming the tile's m products for two of
-// the four route chunks; the fused pass forms them once per chunk).  Single and
-// prefill launches (not grouped), every kernel size.
+// the four route chunks; the fused pass forms them once per chunk).  Every
+// kernel size.
 constexpr bool bwd_two_pass_r(int S, int KC, bool act, bool bf) { return bf && !act && KC == 4; }
 constexpr bool pre_two_pass_r(int S) { return S >= 2; }
 inline bool bwd_two_pass(const Problem& p) {
   const int S = static_cast<int>(p.S), KC = route_chunks(p.K);
   const bool act = p.activation != 0, bf = p.x_dt == DT_BF16;
   return (bwd_two_pass(S, KC, act, bf) && (bf || !p.pre)) || bwd_two_pass_g(p) ||
-         (!p.grouped && (!p.pre || pre_two_pass_r(S)) && bwd_two_pass_r(S, KC, act, bf));
+         ((!p.pre || pre_two_pass_r(S)) && bwd_two_pass_r(S, KC, act, bf));
 }
 // route parts of the taps pass's grid (halves with 64 routes), whose single
 // round of workgroups then covers half as many tiles
@@ -375,11 +374,15 @@ template <int S, int KC, int ACT>
 void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) {
   constexpr bool kSplit = KC >= 2;
   // (mixed activations run the fused pass: grouping admits them only where
-  // both activations' single launches run it).  The two passes: without the
-  // activation as bwd_two_pass, with it as bwd_two_pass_g up to 32 routes (the
-  // dx pass then forms g for every layer, also those without dx)
-  constexpr bool kTwoG = ACT == 1 && KC <= 2 && bwd_two_pass_g(S, KC, true, true);
-  constexpr bool kTwo = (ACT != kActRuntime && bwd_two_pass(S, KC, ACT == 1, true)) || kTwoG;
+  // both activations' single launches run it).  The two passes as the single
+  // launches run them: without the activation as bwd_two_pass / bwd_two_pass_r,
+  // with it as bwd_two_pass_g (the dx pass then forms g for every layer, also
+  // those without dx); with 64 routes the taps pass in route halves
+  constexpr bool kTwoG = ACT == 1 && bwd_two_pass_g(S, KC, true, true);
+  constexpr bool kTwo = (ACT == 0 && (bwd_two_pass(S, KC, false, true) ||
+                                      bwd_two_pass_r(S, KC, false, true))) ||
+                        kTwoG;
+  constexpr int kParts = kTwo ? taps_route_parts(KC) : 1;
   constexpr bool kTiers = !kTwo && !kSplit && kBwdMinWaves<S, KC, kBwdFused, true> == 2;
   const int n_cu = device_cu_count();
   // each layer's grid as bwd_one forms it (the taps pass has its own)
@@ -402,7 +405,7 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
                            : (kTwo && !kTwoG && L[i].dx == nullptr ? 0 : tiles);
     any_dx = any_dx || L[i].dx != nullptr;
     if constexpr (kTwo) {
-      const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(L[i].D, kTapsCW), L[i].D, S, n_cu);
+      const Grid2 gt = bwd_taps_grid(p.n_tokens, cdiv(L[i].D, kTapsCW), L[i].D, S, n_cu / kParts);
       lt.l[i] = ly.l[i];
       lt.l[i].dx = nullptr;
       lt.l[i].gx = static_cast<int>(gt.gx);
@@ -411,14 +414,16 @@ void bwd_layers_one(const Problem& p, const LayerOps* L, int n, hipStream_t st) 
       lt.l[i].n_old = gt.n_old;
       lt.l[i].n_total = gt.n_total;
       lt.l[i].blk0 = static_cast<int>(blkt);
-      blkt += static_cast<int64_t>(gt.gx) * gt.gy;
+      const int64_t tiles_t = static_cast<int64_t>(gt.gx) * gt.gy;
+      // (route halves: the 1-D split grid, the halves of a tile 8 ids apart)
+      blkt += kParts > 1 ? 8 * kParts * cdiv(tiles_t, 8) : tiles_t;
     }
   }
   if constexpr (kTwo) {
     if (any_dx || kTwoG)
       hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kBwdWPG, ACT, true, false, kBwdDx>),
                          dim3(static_cast<unsigned>(blk)), dim3(64 * kBwdWPG), 0, st, ly, p.seq);
-    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, true, false, kBwdTaps>),
+    hipLaunchKernelGGL((bwd_layers_kernel<S, KC, kBwdNB, kBwdNC, kTapsWPG, ACT, true, (kParts > 1), kBwdTaps>),
                        dim3(static_cast<unsigned>(blkt)), dim3(64 * kTapsWPG), 0, st, lt, p.seq);
   } else if constexpr (MOC_BWD_LEAN && bwd_lean(S, KC, true)) {
     // (layers whose dy is one element each, or none of them: one instantiation

@@ -5,8 +5,8 @@ so each workgroup does exactly the work of the single-layer launch; layers may
 differ in K and activation (one forward launch; one backward stage-1 launch
 per route count, and per activation where a two-pass form runs: with SiLU
 each layer's g goes through its own workspace); layers that cannot share one
-launch (fp32, 64 routes in two passes, or the generic kernels) run one by one
-inside the same entry."""
+launch (fp32, or the generic kernels) run one by one inside the same
+entry."""
 from __future__ import annotations
 
 import itertools
@@ -47,6 +47,9 @@ CASES = [
     ([512, 256, 128], 32, 6, 1, [3, 4, 3], [True, True, False], torch.bfloat16),
     ([256, 192], 16, 8, 1, [3, 0], [False, True], torch.bfloat16),
     ([256, 128, 64], [32, 16, 32], 8, [1, 1, 0], [3, 3, 4], [True, False, True], torch.bfloat16),
+    # 64 routes in two passes (taps pass in route halves), grouped
+    ([256, 192], 64, 6, 0, [3, 4], [True, False], torch.bfloat16),
+    ([128, 256], [64, 32], 5, [1, 1], [3, 0], [True, True], torch.bfloat16),
 ]
 
 
@@ -90,7 +93,7 @@ def test_layers_match_single_layer_entries(dims, K, S, act, codes, need, dtype):
     _check(dims, K, S, act, codes, need, dtype, (3, 211))
 
 
-@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3] + CASES[11:15] + CASES[-3:])
+@pytest.mark.parametrize("dims,K,S,act,codes,need,dtype", CASES[:3] + CASES[11:15] + CASES[-5:])
 def test_layers_match_single_layer_entries_packed(dims, K, S, act, codes, need, dtype):
     lengths = [1, 90, 3, 250, 17, 199, 73]
     cu = torch.tensor([0, *itertools.accumulate(lengths)], dtype=torch.int32, device=DEV)

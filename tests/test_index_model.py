@@ -315,3 +315,68 @@ def test_lean_partials_written_once():
                     db[key] = db.get(key, 0) + 1
         assert all(n == 1 for n in da.values()) and len(da) == g["gx"] * N * KP
         assert all(n == 1 for n in db.values()) and len(db) == g["gy"] * KP * S * D
+
+
+# ---------------------------------------------------------------------------
+# grouped launches (csrc/moc_mfma_launch.h bwd_layers_one, csrc/moc_mfma.h
+# layer_index / bwd_layers_kernel)
+
+def layers_grid(layer_grids, nz):
+    """blk0 of each layer and the launch's block count: a layer's grid is its
+    gx gy tiles, or with nz route parts the 1-D split grid of 8 nz ids per 8
+    tiles (the taps pass in route halves, the fused pass split in chunks)."""
+    blk0, blk = [], 0
+    for g in layer_grids:
+        blk0.append(blk)
+        tiles = g["gx"] * g["gy"]
+        blk += 8 * nz * cdiv(tiles, 8) if nz > 1 else tiles
+    return blk0, blk
+
+
+def layers_blocks(layer_grids, nz):
+    """(layer, bx, by, zh) of every live block id of the grouped launch, mapped
+    as the kernel maps it: the owning layer is the last whose blk0 <= id; the
+    local id is split into (bx, row) by the layer's gx (no route parts) or
+    through bwd_block's split mapping."""
+    blk0, blk = layers_grid(layer_grids, nz)
+    out = []
+    for b in range(blk):
+        li = max(i for i in range(len(blk0)) if blk0[i] <= b)
+        g = layer_grids[li]
+        local = b - blk0[li]
+        if nz == 1:
+            out.append((li, local % g["gx"], local // g["gx"], 0))
+            continue
+        t = (local // (8 * nz)) * 8 + (local & 7)
+        if t >= g["gx"] * g["gy"]:
+            continue
+        out.append((li, t % g["gx"], t // g["gx"], (local >> 3) % nz))
+    return out
+
+
+@pytest.mark.parametrize("dims,S,KC,mode,n_cu", [
+    ([512, 256, 128], 6, 2, "dx", 256),      # SiLU two passes, 32 routes: dx pass
+    ([512, 256, 128], 6, 2, "taps", 256),
+    ([256, 128], 4, 4, "taps", 256),         # 64 routes: taps pass in route halves
+    ([4096, 1024, 1024], 8, 2, "dx", 256),   # configs[4]
+    ([256, 192], 8, 4, "fused", 256),        # fused pass split in route chunks
+])
+def test_grouped_grid_covers_each_layer_once(dims, S, KC, mode, n_cu):
+    """Every block of a layer's single launch runs exactly once in the grouped
+    launch, and no block id maps past a layer's tiles (a block with by >= gy
+    would take a token range past the layer's last)."""
+    N = 999
+    if mode == "taps":
+        nz = 2 if KC == 4 else 1
+        grids = [bwd_grid_gx(N, cdiv(D, 128), D, S, n_cu // nz, taps=True) for D in dims]
+    elif mode == "dx":
+        nz = 1
+        grids = [bwd_grid_gx(N, cdiv(D, 128), D, S, 512) for D in dims]
+    else:
+        nz = KC
+        grids = [bwd_grid_gx(N, cdiv(D, 128), D, S, 512) for D in dims]
+    got = layers_blocks(grids, nz)
+    want = [(li,) + blk for li, g in enumerate(grids) for blk in blocks(g, nz)]
+    assert sorted(got) == sorted(want)
+    assert len(set(got)) == len(got)
+    assert all(by < grids[li]["gy"] for li, _, by, _ in got)
