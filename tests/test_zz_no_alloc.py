@@ -84,6 +84,27 @@ def test_noalloc_backward_matches_workspace_backward(dtype):
     _same("packed", got, ref)
 
 
+@pytest.mark.parametrize("D,K,S,dtype,act", [
+    (197, 16, 4, torch.bfloat16, 1),    # odd channel count: the padded copy
+    (192, 32, 12, torch.float32, 1),    # fp32 route parts of 16 routes
+    (128, 48, 4, torch.float32, 0),     # fp32 route halves of 32 routes
+    (192, 32, 12, torch.bfloat16, 1),   # bf16 route chunks past 8 taps
+    (192, 64, 6, torch.bfloat16, 0),    # 64 routes in two passes, taps in route halves
+])
+def test_noalloc_other_backward_forms(D, K, S, dtype, act):
+    """The backward forms that carve more of the workspace (padded copies, route
+    parts and chunks, route-half taps) on the scratch: bit for bit with
+    moc_backward, on a second call after a larger first one."""
+    x, a, b, dy = _inputs(5, 2 * 300, D, K, S, dtype, True)
+    ref = _call(False, x, a, b, dy, D, act, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=300)
+    got = _call(True, x, a, b, dy, D, act, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=300)
+    _same("call 1", got, ref)
+    x, a, b, dy = _inputs(6, 2 * 77, D, K, S, dtype, True)
+    ref = _call(False, x, a, b, dy, D, act, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=77)
+    got = _call(True, x, a, b, dy, D, act, _lib.ROUTE_SOFTMAX_WEIGHTS, seq_len=77)
+    _same("call 2", got, ref)
+
+
 def test_noalloc_rejects_a_problem_beyond_its_scratch():
     L = _lib.lib()
     N, D = 1 << 20, 2048
