@@ -310,6 +310,22 @@ def test_parts_and_padding_small(S, K, dtype, act, D, B, T):
         assert_close(n, u, r, dtype)
 
 
+@pytest.mark.parametrize("D,K,S,dtype,act", [
+    (1, 1, 2, torch.bfloat16, "silu"),     # one channel (padded to 2), one route
+    (2, 2, 3, torch.bfloat16, None),
+    (3, 5, 2, torch.float32, "silu"),
+    (2, 1, 16, torch.float32, None),       # 16 taps, two passes
+    (5, 33, 4, torch.bfloat16, "silu"),    # 33 routes padded to 64
+    (4, 17, 9, torch.float32, "silu"),     # fp32 route parts past 8 taps
+])
+def test_tiny_shapes(D, K, S, dtype, act):
+    """The smallest channel and route counts on the matrix-core paths (padded
+    copies, padded routes, route parts), fixed and packed, against the oracle."""
+    L = _lib.lib()
+    assert L.moc_matrix_core_supported(2 * 37, D, K, S, _lib.dtype_code(dtype), 1) == 1
+    _mfma_vs_generic(dtype, S, K, act, D, Bt=2, T=37, lengths=(1, 2, 30, 4, 37))
+
+
 @pytest.mark.parametrize("form", ["element", "row"])
 def test_odd_channel_count_broadcast_dy(form):
     """The padded backward with the dy of y.sum() (one element) and with one
