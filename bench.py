@@ -22,6 +22,7 @@ inputs already resident in HBM.  Printed as one JSON line:
                 MoC.forward call from the prompt's cache (inputs known up front);
                 and (update_us) moc_update per launch in bf16 / fp32 with a
                 contiguous or slot-major cache (matrix-core and generic kernels)
+                and at 12 / 16 taps
   cpu_baseline  the CPU oracle on a bounded slice of the same workload
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
@@ -418,8 +419,8 @@ def decode_step_call(dev):
                                           routing=ROUTE_SOFTMAX)
 
 
-UPDATE_FORMS = (("bf16", "contiguous"), ("fp32", "contiguous"), ("bf16", "slot-major"),
-                ("fp32", "slot-major"))
+UPDATE_FORMS = (("bf16", "contiguous", 4), ("fp32", "contiguous", 4), ("bf16", "slot-major", 4),
+                ("fp32", "slot-major", 4), ("bf16", "contiguous", 12), ("fp32", "contiguous", 16))
 
 
 def update_calls(dev):
@@ -427,13 +428,14 @@ def update_calls(dev):
     shape (batch 256, D 2048, K 16, S 4, softmax, SiLU) in four forms: bf16 with
     a contiguous [B, D, S] cache (the matrix-core decode kernel), and fp32 data
     or a slot-major cache ([B, D, S] view of a [B, S, D] store), which take the
-    generic tile kernel.  Returns [(label, fn)]."""
+    generic tile kernel; and the tile kernel at 12 taps (bf16) and 16 taps
+    (fp32).  Returns [(label, fn)]."""
     from moc import ops
     from moc._lib import ROUTE_SOFTMAX
     c = DECODE
-    B, D, K, S = c["B"], c["D"], c["K"], c["S"]
+    B, D, K = c["B"], c["D"], c["K"]
     calls = []
-    for dt_name, layout in UPDATE_FORMS:
+    for dt_name, layout, S in UPDATE_FORMS:
         dt = torch.bfloat16 if dt_name == "bf16" else torch.float32
         g = torch.Generator().manual_seed(0)
         x = torch.randn(B, D, generator=g).to(dev, dt)
@@ -442,7 +444,7 @@ def update_calls(dev):
         cache = torch.randn(B, D, S, generator=g).to(dev, dt)
         if layout == "slot-major":
             cache = cache.transpose(1, 2).contiguous().transpose(1, 2)
-        calls.append((f"{dt_name} {layout}",
+        calls.append((f"{dt_name} {layout}" + ("" if S == c["S"] else f" S{S}"),
                       lambda x=x, lg=lg, b=b, cache=cache: ops.launch_update(
                           x, lg, b, cache, activation_flag=1, routing=ROUTE_SOFTMAX)))
     return calls
