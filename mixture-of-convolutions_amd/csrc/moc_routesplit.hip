@@ -7,7 +7,7 @@
 // activation is linear in the routes (moc/kernels.py:36-439):
 //   P      = sum over the parts of the forward without the activation;
 //   y      = act(P);
-//   g      = dy silu'(P) (or dy);
+//   g      = dy silu'(P) (without the activation dy itself, P not formed);
 //   dx     = sum over the parts of the backward of (x, weights_i, basis_i) with
 //            dy = g and no activation (its dx is sum_s g W_i);
 //   dalpha = the router gradient (softmax / exp) over all K routes of the
@@ -244,10 +244,17 @@ void backward_routesplit(const Problem& p, const void* x, const void* alpha, con
   const int64_t N = p.n_tokens, D = p.D;
   launch_prep_alpha(p, alpha, a_r, st);
   prof_begin(p, st);
-  // P over all routes (no activation), then g
-  forward_p(p, x, a_r, a_p, basis, P, reinterpret_cast<float*>(ws + s.p1), ws + s.ws_f, false, st);
-  hipLaunchKernelGGL(g_kernel, dim3(grid_of(N * D, 256)), dim3(256), 0, st, P, dy, p.dy_stride,
-                     p.x_dt, g, N, D, p.activation);
+  // with the activation: P over all routes (no activation), then g; without
+  // it g is dy, which the parts read as it is (rows, one row or one element)
+  const void* gsrc = dy;
+  int64_t gstride = p.dy_stride;
+  if (p.activation != 0) {
+    forward_p(p, x, a_r, a_p, basis, P, reinterpret_cast<float*>(ws + s.p1), ws + s.ws_f, false, st);
+    hipLaunchKernelGGL(g_kernel, dim3(grid_of(N * D, 256)), dim3(256), 0, st, P, dy, p.dy_stride,
+                       p.x_dt, g, N, D, p.activation);
+    gsrc = g;
+    gstride = D;
+  }
   // the parts' weights (the halves' split in forward_p shares a_p: the same
   // stream runs this after those forwards), then each part with dy = g
   split_weights(p, a_r, a_p, s.h, st);
@@ -255,7 +262,9 @@ void backward_routesplit(const Problem& p, const void* x, const void* alpha, con
   for (int64_t i = 0; i < s.n; ++i) {
     const int64_t k = part_k(p.K, s.h, i);
     const size_t boff = static_cast<size_t>(s.h * i * p.S * D) * esz_b;
-    backward(part_problem(p, k), x, a_p + N * s.h * i, static_cast<const char*>(basis) + boff, g,
+    Problem q = part_problem(p, k);
+    q.dy_stride = gstride;
+    backward(q, x, a_p + N * s.h * i, static_cast<const char*>(basis) + boff, gsrc,
              dx == nullptr ? nullptr : (i == 0 ? dx : dx1), da + N * s.h * i,
              static_cast<char*>(dbasis) + boff, ws + s.ws_b, st);
     if (i > 0 && dx != nullptr)

@@ -326,6 +326,31 @@ def test_tiny_shapes(D, K, S, dtype, act):
     _mfma_vs_generic(dtype, S, K, act, D, Bt=2, T=37, lengths=(1, 2, 30, 4, 37))
 
 
+@pytest.mark.parametrize("form", ["element", "row", "full"])
+@pytest.mark.parametrize("S,K,act", [(12, 48, 0), (4, 64, 0), (12, 32, 1)])
+def test_route_parts_broadcast_dy(form, S, K, act):
+    """The fp32 route-part backward with the dy of y.sum() (one element), one dy
+    row for every token and full rows: without the activation the parts read
+    dy as it is; with it g = dy silu'(P) comes first.  Against the oracle."""
+    from moc import ops
+    g = gen(S * 100 + K)
+    D = 128
+    x = randn(g, 2, 150, D, scale=0.5).to(DEV, torch.float32)
+    a = torch.softmax(randn(g, 2, 150, K), -1).to(DEV, torch.float32)
+    b = randn(g, K, S, D, scale=0.2).to(DEV, torch.float32)
+    if form == "element":
+        dy = torch.ones((), device=DEV, dtype=torch.float32).expand(2, 150, D)
+    elif form == "row":
+        dy = randn(g, D).to(DEV, torch.float32).expand(2, 150, D)
+    else:
+        dy = randn(g, 2, 150, D).to(DEV, torch.float32)
+    got = ops.launch_backward(x, a, b, dy, activation_flag=act, need_x=True)
+    rx, ra, rb = O.reference_inputs(x, a, b, torch.float32)
+    ref = O.moc_grads_ref(rx, ra, rb, dy.float().cpu().contiguous(), "silu" if act else None)
+    for n, u, r in zip(("dx", "dalpha", "dbasis"), got, ref[1:]):
+        assert_close(n, u, r, torch.float32)
+
+
 @pytest.mark.parametrize("form", ["element", "row"])
 def test_odd_channel_count_broadcast_dy(form):
     """The padded backward with the dy of y.sum() (one element) and with one
