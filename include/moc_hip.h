@@ -88,8 +88,7 @@ int moc_set_kernel_path(int path);
  * and backward: 2 <= kernel_size <= 16, k <= 64, x bf16 or f32 (some shapes
  * in route parts: the f32 forward past 32 routes beyond kernel_size 8, the
  * backward past 16 routes beyond kernel_size 8 and the f32 backward past 32
- * routes); an odd dim through a copy padded with a zero channel (not with
- * route parts).
+ * routes); an odd dim through a copy padded with a zero channel.
  */
 int moc_matrix_core_supported(int64_t n_tokens, int64_t dim, int64_t k, int64_t kernel_size,
                               int x_dtype, int backward);

@@ -1,7 +1,9 @@
 // Odd channel counts on the matrix-core kernels through a padded copy.  The
 // tiles give each lane a pair of channels, so they take D even only.  With D
 // odd the layer runs at D + 1 channels on copies of x, dy and basis with a zero
-// last channel, and y, dx and dbasis are copied back without it.  The extra
+// last channel (in whichever form the padded shape takes: one launch family,
+// route chunks or route parts), and y, dx and dbasis are copied back without
+// it.  The extra
 // channel changes nothing the caller sees: its x, dy and basis are zero, so its
 // y is act(0) and dropped, its m products x dy are zero (dalpha sums over
 // channels add exact zeros) and its dbasis is dropped.  Costs two passes over
@@ -83,6 +85,13 @@ void unpad(const void* src, void* dst, int64_t rows, int64_t D, int dt, hipStrea
                        static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), D);
 }
 
+// The padded problem's own forms: one launch family, or route chunks / parts.
+size_t inner_ws(const Problem& q, bool backward) {
+  if (!backward) return supported(q) ? forward_workspace(q) : routesplit_fwd_workspace(q);
+  if (bwd_supported(q)) return backward_workspace(q);
+  return chunks_supported(q) ? chunks_workspace(q) : routesplit_workspace(q);
+}
+
 struct PadPlan {
   size_t x, b, io, dy, db, inner, total;  // io: y (forward) or dx (backward)
 };
@@ -100,7 +109,7 @@ PadPlan pad_plan(const Problem& p, bool backward) {
     s.dy = off; off += p.dy_stride < 0 ? 0 : al((p.dy_stride == 0 ? 1 : N) * W * esz(p.x_dt));
     s.db = off; off += al(KS * W * esz(p.b_dt));
   }
-  s.inner = off; off += al(backward ? backward_workspace(q) : forward_workspace(q));
+  s.inner = off; off += al(inner_ws(q, backward));
   s.total = off;
   return s;
 }
@@ -110,7 +119,8 @@ PadPlan pad_plan(const Problem& p, bool backward) {
 bool pad_supported(const Problem& p, bool backward) {
   if (p.D % 2 == 0 || p.D + 1 > (int64_t(1) << 20)) return false;
   const Problem q = padded(p);
-  return backward ? bwd_supported(q) : supported(q);
+  return backward ? bwd_supported(q) || chunks_supported(q) || routesplit_supported(q)
+                  : supported(q) || routesplit_fwd_supported(q);
 }
 
 size_t pad_workspace(const Problem& p, bool backward) { return pad_plan(p, backward).total; }
@@ -122,7 +132,8 @@ void forward_padded(const Problem& p, const void* x, const void* alpha, const vo
   char* ws = static_cast<char*>(workspace);
   pad(x, p.D, ws + s.x, p.n_tokens, p.D, p.x_dt, st);
   pad(basis, p.D, ws + s.b, p.K * p.S, p.D, p.b_dt, st);
-  forward(q, ws + s.x, alpha, ws + s.b, ws + s.io, ws + s.inner, st);
+  if (supported(q)) forward(q, ws + s.x, alpha, ws + s.b, ws + s.io, ws + s.inner, st);
+  else forward_routesplit(q, ws + s.x, alpha, ws + s.b, ws + s.io, ws + s.inner, st);
   unpad(ws + s.io, y, p.n_tokens, p.D, p.x_dt, st);
 }
 
@@ -139,8 +150,13 @@ void backward_padded(const Problem& p, const void* x, const void* alpha, const v
     pad(dy, p.dy_stride, ws + s.dy, p.dy_stride == 0 ? 1 : p.n_tokens, p.D, p.x_dt, st);
     dyq = ws + s.dy;
   }
-  backward(q, ws + s.x, alpha, ws + s.b, dyq, dx != nullptr ? ws + s.io : nullptr, dalpha,
-           ws + s.db, ws + s.inner, st);
+  void* dxq = dx != nullptr ? ws + s.io : nullptr;
+  if (bwd_supported(q))
+    backward(q, ws + s.x, alpha, ws + s.b, dyq, dxq, dalpha, ws + s.db, ws + s.inner, st);
+  else if (chunks_supported(q))
+    backward_chunks(q, ws + s.x, alpha, ws + s.b, dyq, dxq, dalpha, ws + s.db, ws + s.inner, st);
+  else
+    backward_routesplit(q, ws + s.x, alpha, ws + s.b, dyq, dxq, dalpha, ws + s.db, ws + s.inner, st);
   if (dx != nullptr) unpad(ws + s.io, dx, p.n_tokens, p.D, p.x_dt, st);
   unpad(ws + s.db, dbasis, p.K * p.S, p.D, p.b_dt, st);
 }

@@ -254,7 +254,8 @@ def test_matrix_core_supported_names_the_kernel_family():
         assert L.moc_matrix_core_supported(1024, 198, 16, 4, bf, bwd) == 1    # D % 4 == 2
         assert L.moc_matrix_core_supported(1024, 2050, 32, 8, f32, bwd) == 1
         assert L.moc_matrix_core_supported(1024, 197, 16, 4, bf, bwd) == 1    # D odd: padded copy
-        assert L.moc_matrix_core_supported(1024, 197, 48, 12, f32, bwd) == 0  # padded, route parts: no
+        assert L.moc_matrix_core_supported(1024, 197, 48, 12, f32, bwd) == 1  # padded, route parts
+        assert L.moc_matrix_core_supported(1024, 197, 80, 4, bf, bwd) == 0     # past 64 routes
         assert L.moc_matrix_core_supported(1024, 2048, 64, 2, bf, bwd) == 1
         assert L.moc_matrix_core_supported(1024, 2048, 48, 12, f32, bwd) == 1  # fp32, route parts
         assert L.moc_matrix_core_supported(1024, 2048, 80, 12, f32, bwd) == 0  # past 64 routes

@@ -273,6 +273,8 @@ def test_mfma_long_kernels(dtype, S, K, act, bwd):
     (torch.float32, 6, 24, "silu", 65),
     (torch.bfloat16, 12, 16, None, 131),     # 12 taps
     (torch.bfloat16, 3, 64, "silu", 191),    # 64 routes
+    (torch.float32, 12, 48, "silu", 197),    # fp32 route parts and forward halves
+    (torch.bfloat16, 12, 32, "silu", 131),   # bf16 route chunks past 8 taps
 ])
 def test_odd_channel_counts_padded(dtype, S, K, act, D):
     """Odd channel counts run the matrix-core kernels on a copy padded with a
@@ -375,7 +377,7 @@ def test_odd_channel_count_broadcast_dy(form):
 @pytest.mark.parametrize("dtype,S,K,act,D", [
     (torch.bfloat16, 17, 16, "silu", 192),   # past 16 taps
     (torch.bfloat16, 4, 80, None, 192),      # past 64 routes
-    (torch.float32, 12, 48, "silu", 197),    # odd channel count with fp32 route parts
+    (torch.float32, 17, 8, "silu", 197),     # past 16 taps, odd channel count
 ])
 def test_generic_path_matches_oracle(dtype, S, K, act, D):
     """The shapes outside the matrix-core kernels (forward and backward) run
